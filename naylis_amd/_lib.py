@@ -1,0 +1,88 @@
+"""Loader for libnaylis_mom.so, the C-ABI library of HIP kernels.
+
+The library is built in-tree (``naylis_amd/_lib/libnaylis_mom.so``, see
+``naylis_amd/build.py``) and loaded with ctypes; argument types of every
+entry point are declared here from ``include/naylis_mom.h``.  There is no
+fallback: a missing or stale library raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
+LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
+ABI_VERSION = 1
+
+NAYLIS_OK = 0
+NAYLIS_ERR_ARG = 1
+NAYLIS_ERR_WORKSPACE = 2
+NAYLIS_ERR_HIP = 3
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_size_t = ctypes.c_size_t
+_int = ctypes.c_int
+_float = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/naylis_mom.h
+SIGNATURES = {
+    "naylis_mom_abi_version": (_int, []),
+    "naylis_mom_last_error": (ctypes.c_char_p, []),
+    "naylis_mom_read_workspace_bytes": (_size_t, [_i64] * 7),
+    "naylis_mom_read_fwd": (_int, [_c_void_p] * 7 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_read_bwd": (_int, [_c_void_p] * 12 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NaylisError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+
+
+def load():
+    """Load (once) and return the ctypes handle; raises if unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"naylis_amd: HIP library not built ({LIB_PATH} missing). "
+                "Run `python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`python -m naylis_amd.build` first.")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.naylis_mom_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"naylis_amd: library ABI {ver} != expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def check(rc):
+    """Raise NaylisError for a non-zero status code."""
+    if rc != NAYLIS_OK:
+        msg = load().naylis_mom_last_error()
+        msg = msg.decode() if msg else "unknown error"
+        raise NaylisError(rc, msg)
+
+
+def available():
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False

@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 (CDNA4) MoM kernels.
+//
+// MFMA conventions used everywhere (v_mfma_f32_32x32x16_bf16, wave64),
+// checked on MI355X hardware:
+//   A operand (32 x 16, bf16x8 per lane):  lane l holds A[l%32][8*(l/32) + e]
+//   B operand (16 x 32, bf16x8 per lane):  lane l holds B[8*(l/32) + e][l%32]
+//   D (32 x 32, f32x16 per lane):          lane l, reg v holds
+//                                           D[8*(v/4) + 4*(l/32) + v%4][l%32]
+// So the accumulator of one product has "column = lane" and "rows spread
+// over registers"; the K index of the next product can be any fixed
+// permutation as long as both operands use it.  Two permutations follow:
+//
+//  * slot_perm16(p): position p of a 16-wide K group holds element
+//    8*((p%8)/4) + 4*(p/8) + p%4, i.e. bits 2 and 3 of p swapped.  With it,
+//    registers 8*h .. 8*h+7 of an accumulator tile are exactly the bf16x8
+//    B fragment for K-step h of the next product (no cross-lane moves).
+//  * row_perm32(r): A-operand row r of a 32-row tile computes output
+//    feature row_perm32(r) = 16*bit2(r) + 4*(r>>3) + (r&3); with it lane
+//    group g (= l/32) of the product holds features 16*g .. 16*g+15 in
+//    registers 0..15, so each lane stores 64 contiguous bytes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace naylis {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t bf16_t;  // bf16 storage in global memory
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__host__ __device__ constexpr int slot_perm16(int p) {
+  return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);
+}
+
+__host__ __device__ constexpr int row_perm32(int r) {
+  return (((r >> 2) & 1) << 4) | ((r >> 3) << 2) | (r & 3);
+}
+
+// Inverse of row_perm32: the A-operand row that computes feature f.
+__host__ __device__ constexpr int row_unperm32(int f) {
+  return (((f >> 2) & 3) << 3) | ((f >> 4) << 2) | (f & 3);
+}
+
+// Row of the 32x32 accumulator held by (lane group g, register v).
+__device__ __forceinline__ int acc_row(int g, int v) { return 8 * (v >> 2) + 4 * g + (v & 3); }
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t u) {
+  return __uint_as_float(((uint32_t)u) << 16);
+}
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;  // round to nearest even
+  return __builtin_bit_cast(bf16_t, b);
+}
+
+// Pack 8 fp32 values (registers lo..lo+7 of an accumulator) to a bf16x8 fragment.
+__device__ __forceinline__ bf16x8 pack8(const f32x16& acc, int lo) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (__bf16)acc[lo + e];
+  return r;
+}
+
+__device__ __forceinline__ float wave_max_pair(float x) {
+  // Combine lane l with lane l^32 (the two lane groups that share a column).
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+__device__ __forceinline__ float wave_sum_pair(float x) { return x + __shfl_xor(x, 32, 64); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for running maxima
+
+}  // namespace naylis

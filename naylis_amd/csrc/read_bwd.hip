@@ -1,0 +1,695 @@
+// Gated flash read of the shared MoM bank, backward (gfx950).
+//
+// Gradients of o = softmax(q k^T * scale + bias) v, bias = routed log-gates
+// (mom_kernels/reference.py:14-61), the set mom_kernels/triton_gpu.py:359-409
+// returns: dq, dk and dv of the SHARED bank projections (reduced over every
+// token of the batch), and d(top_gates).  P is recomputed from the forward's
+// log2-domain lse; dS = P (dP - delta), delta = rowsum(o * do).
+//
+// Three launches, all deterministic (no floating-point atomics):
+//  1. read_bwd_dq_kernel   — one workgroup per (b, h, 128-token tile), walks
+//     the tile's active slot groups: S^T, dP^T, dS^T, dQ^T += K^T dS^T; also
+//     writes delta and the per-head partial of dlog_gates (sum of dS over
+//     each selected block).
+//  2. read_bwd_dkdv_kernel — one workgroup per (h, 128-slot group, token
+//     chunk), K/V of its slots resident in registers, walks the chunk's
+//     64-token tiles that select any block of the group: S, dP, dS,
+//     dV^T += dO^T P, dK^T += Q^T dS, written as fp32 partials per chunk.
+//  3. read_bwd_reduce kernels — partials summed over chunks in a fixed order
+//     (dk scaled), per-head dlog partials summed over heads and mapped to
+//     d(top_gates) through log(max(g, 1e-9)).
+#include "launch.h"
+#include "read_common.h"
+
+namespace naylis {
+
+template <int HD, int SG, bool ALIGNED, int TK>
+__global__ __launch_bounds__(256) void read_bwd_dq_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ kt, const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates,
+    const bf16_t* __restrict__ o, const bf16_t* __restrict__ dout, const float* __restrict__ lse,
+    bf16_t* __restrict__ dq, float* __restrict__ delta, float* __restrict__ dlg_part, int B, int S, int H,
+    int L, int Lp, int E, int block_size, int topk, float alpha, float scale, int n_tiles) {
+  constexpr int HDP = HD < 32 ? 32 : HD;
+  constexpr int KS = HD / 16;
+  constexpr int NS = SG / 32;
+  constexpr int NO = HDP / 32;
+  constexpr int KPAD = HD + 8;
+  constexpr int VPAD = SG + 8;
+
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * KPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[SG * KPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t kt_lds[HDP * VPAD];
+  __shared__ uint8_t flags[kMaxBlocks];
+  __shared__ uint16_t groups[kMaxGroups];
+  __shared__ int n_active;
+
+  const int G = B * H * n_tiles;
+  const int wid = xcd_remap(blockIdx.x, G);
+  const int tile = wid % n_tiles;
+  const int b = (wid / n_tiles) % B;
+  const int h = wid / (n_tiles * B);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const int s_tok = tile * 128 + wave * 32 + col;
+  const bool tok_ok = s_tok < S;
+  const long tok = (long)b * S + s_tok;
+  const int D = H * HD;
+
+  TokenRoute<TK> rt;
+  load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
+  for (int e = tid; e < E; e += 256) flags[e] = 0;
+  __syncthreads();
+  if (g == 0 && tok_ok) {
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+  }
+  __syncthreads();
+  const int n_groups = Lp / SG;
+  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
+
+  // Q^T and dO^T fragments; delta = rowsum(o * do) from the same rows
+  bf16x8 qf[KS], df[KS];
+  float dl = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (tok_ok) {
+      const long off = tok * D + (long)h * HD + 16 * ks + 8 * g;
+      qf[ks] = *reinterpret_cast<const bf16x8*>(q + off);
+      df[ks] = *reinterpret_cast<const bf16x8*>(dout + off);
+      const bf16x8 of = *reinterpret_cast<const bf16x8*>(o + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dl = fmaf((float)of[e], (float)df[ks][e], dl);
+    } else {
+      qf[ks] = bf16x8{};
+      df[ks] = bf16x8{};
+    }
+  }
+  dl = wave_sum_pair(dl);
+  const float lse_t = tok_ok ? lse[((long)b * H + h) * S + s_tok] : 0.f;
+
+  f32x16 acc_dq[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) acc_dq[j] = f32x16{};
+  // dlog_gates without the bf16 rounding of o inside delta: per selection t
+  // accumulate A_t = sum_{n in block t} P dP and M_t = sum_{n in block t} P,
+  // plus dx = sum_n P dP (= the exact delta); then dlog_t = A_t - dx * M_t.
+  float accA[TK], accM[TK];
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    accA[t] = 0.f;
+    accM[t] = 0.f;
+  }
+  float dx = 0.f;
+
+  __syncthreads();
+  const int n_act = n_active;
+
+  constexpr int KV_VEC = SG * HD / 8;
+  constexpr int KT_VEC = HDP * SG / 8;
+  constexpr int K_PER = (KV_VEC + 255) / 256;
+  constexpr int T_PER = (KT_VEC + 255) / 256;
+  uint4 kreg[K_PER], vreg[K_PER], treg[T_PER];
+
+  auto load_group = [&](int gi) {
+    const int s0 = gi * SG;
+#pragma unroll
+    for (int r = 0; r < K_PER; ++r) {
+      const int vi = tid + 256 * r;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (vi < KV_VEC) {
+        const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
+        if (s0 + srow < L) {
+          const long off = (long)(s0 + srow) * D + (long)h * HD + 8 * c8;
+          kv = *reinterpret_cast<const uint4*>(k + off);
+          vv = *reinterpret_cast<const uint4*>(v + off);
+        }
+      }
+      kreg[r] = kv;
+      vreg[r] = vv;
+    }
+#pragma unroll
+    for (int r = 0; r < T_PER; ++r) {
+      const int vi = tid + 256 * r;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (vi < KT_VEC) {
+        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
+        val = *reinterpret_cast<const uint4*>(kt + ((long)h * HDP + hr) * Lp + s0 + 8 * c8);
+      }
+      treg[r] = val;
+    }
+  };
+  auto store_group = [&]() {
+#pragma unroll
+    for (int r = 0; r < K_PER; ++r) {
+      const int vi = tid + 256 * r;
+      if (vi < KV_VEC) {
+        const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
+        *reinterpret_cast<uint4*>(&k_lds[srow * KPAD + 8 * c8]) = kreg[r];
+        *reinterpret_cast<uint4*>(&v_lds[srow * KPAD + 8 * c8]) = vreg[r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < T_PER; ++r) {
+      const int vi = tid + 256 * r;
+      if (vi < KT_VEC) {
+        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
+        *reinterpret_cast<uint4*>(&kt_lds[hr * VPAD + 8 * c8]) = treg[r];
+      }
+    }
+  };
+
+  if (n_act > 0) load_group(groups[0]);
+
+  for (int it = 0; it < n_act; ++it) {
+    const int gi = groups[it];
+    __syncthreads();
+    store_group();
+    __syncthreads();
+    if (it + 1 < n_act) load_group(groups[it + 1]);
+
+    f32x16 acc_s[NS], acc_p[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      acc_s[i] = f32x16{};
+      acc_p[i] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (32 * i + col) * KPAD + 16 * ks + 8 * g;
+        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(&k_lds[off]);
+        const bf16x8 av = *reinterpret_cast<const bf16x8*>(&v_lds[off]);
+        acc_s[i] = mfma32(ak, qf[ks], acc_s[i]);
+        acc_p[i] = mfma32(av, df[ks], acc_p[i]);
+      }
+    }
+
+    if constexpr (ALIGNED) {
+      const int e = (gi * SG) / block_size;
+      bool sel;
+      const float c2 = route_bias<TK>(rt, e, topk, sel);
+      const float add = sel ? c2 - lse_t : -INFINITY;
+      float rsA = 0.f, rsM = 0.f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int vv = 0; vv < 16; ++vv) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, add));
+          const float dp = acc_p[i][vv];
+          acc_s[i][vv] = p * (dp - dl);
+          rsA = fmaf(p, dp, rsA);
+          rsM += p;
+        }
+      dx += rsA;
+#pragma unroll
+      for (int t = 0; t < TK; ++t)
+        if (t < topk && rt.idx[t] == e) {
+          accA[t] += rsA;
+          accM[t] += rsM;
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int vv = 0; vv < 16; ++vv) {
+          const int slot = gi * SG + 32 * i + acc_row(g, vv);
+          bool sel = false;
+          float c2 = 0.f;
+          const int e = slot < L ? slot / block_size : -2;
+          if (slot < L) c2 = route_bias<TK>(rt, e, topk, sel);
+          const float p = sel ? __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, c2 - lse_t)) : 0.f;
+          const float dp = acc_p[i][vv];
+          acc_s[i][vv] = p * (dp - dl);
+          const float pdp = p * dp;
+          dx += pdp;
+#pragma unroll
+          for (int t = 0; t < TK; ++t)
+            if (t < topk && rt.idx[t] == e) {
+              accA[t] += pdp;
+              accM[t] += p;
+            }
+        }
+    }
+
+    // dQ^T += K^T . dS^T
+#pragma unroll
+    for (int kk = 0; kk < SG / 16; ++kk) {
+      const bf16x8 bs = pack8(acc_s[kk >> 1], 8 * (kk & 1));
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kt_lds[(32 * j + col) * VPAD + 16 * kk + 8 * g]);
+        acc_dq[j] = mfma32(a, bs, acc_dq[j]);
+      }
+    }
+  }
+
+  dx = wave_sum_pair(dx);
+  float dlg[TK];
+#pragma unroll
+  for (int t = 0; t < TK; ++t) dlg[t] = wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t]);
+
+  if (tok_ok) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int f0 = 32 * j + 16 * g;
+      if (f0 < HD) {
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          lo[e] = (__bf16)(acc_dq[j][e] * scale);
+          hi[e] = (__bf16)(acc_dq[j][8 + e] * scale);
+        }
+        bf16_t* dst = dq + tok * D + (long)h * HD + f0;
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+      }
+    }
+    if (g == 0) {
+      const long ntok = (long)B * S;
+      delta[((long)b * H + h) * S + s_tok] = dx;
+#pragma unroll
+      for (int t = 0; t < TK; ++t)
+        if (t < topk) dlg_part[((long)h * ntok + tok) * topk + t] = dlg[t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV over the shared bank.  Lanes own slots (S = Q K^T orientation), so
+// P and dS come out of the accumulators already in the B-operand layout of
+// dV^T = dO^T P and dK^T = Q^T dS; Q^T and dO^T are staged transposed (rows
+// in row_perm32 order, tokens in slot_perm16 order) in LDS.
+template <int HD, bool ALIGNED, int TK, bool SPLIT>
+__global__ __launch_bounds__(256) void read_bwd_dkdv_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dk_part,
+    float* __restrict__ dv_part, int B, int S, int H, int L, int Lq, int E, int block_size, int topk,
+    float alpha, int n_chunks, int tiles_per_chunk) {
+  constexpr int HDP = HD < 32 ? 32 : HD;
+  constexpr int KS = HD / 16;
+  constexpr int NO = HDP / 32;
+  constexpr int TT = 64;            // tokens per staged tile
+  constexpr int NT = TT / 32;       // 32-token accumulator tiles
+  constexpr int QPAD = HD + 8;
+  constexpr int TPAD = TT + 8;
+
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds[TT * QPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t do_lds[TT * QPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t qt_lds[HDP * TPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t dot_lds[HDP * TPAD];
+  __shared__ __attribute__((aligned(16))) float add_lds[4][TT];   // per wave-block: c2 - lse or -inf
+  __shared__ __attribute__((aligned(16))) float dl_lds[TT];
+  __shared__ int32_t idx_lds[TT * TK];
+  __shared__ float lg_lds[TT * TK];
+  __shared__ float lse_lds[TT];
+
+  const int n_sg = Lq / 128;  // Lq = L rounded up to 128: rows of the partials
+  const int G = H * n_sg * n_chunks;
+  const int wid = xcd_remap(blockIdx.x, G);
+  const int chunk = wid % n_chunks;
+  const int sg = (wid / n_chunks) % n_sg;
+  const int h = wid / (n_chunks * n_sg);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const int slot = sg * 128 + wave * 32 + col;
+  const bool slot_ok = slot < L;
+  const int D = H * HD;
+  const long ntok = (long)B * S;
+  const int n_ttiles = (int)((ntok + TT - 1) / TT);
+
+  // blocks covered by this workgroup's 128 slots
+  const int blk_lo = (sg * 128) / block_size;
+  const int blk_hi = (min(sg * 128 + 128, L) - 1) / block_size;
+  const int lane_blk = slot / block_size;
+
+  // K and V rows of this lane's slot as B fragments (K^T / V^T columns)
+  bf16x8 kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (slot_ok) {
+      const long off = (long)slot * D + (long)h * HD + 16 * ks + 8 * g;
+      kf[ks] = *reinterpret_cast<const bf16x8*>(k + off);
+      vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
+    } else {
+      kf[ks] = bf16x8{};
+      vf[ks] = bf16x8{};
+    }
+  }
+
+  f32x16 acc_dk[NO], acc_dv[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    acc_dk[j] = f32x16{};
+    acc_dv[j] = f32x16{};
+  }
+
+  const int t_begin = chunk * tiles_per_chunk;
+  const int t_end = min(n_ttiles, t_begin + tiles_per_chunk);
+  for (int tt = t_begin; tt < t_end; ++tt) {
+    const long tok0 = (long)tt * TT;
+    // ---- routing of the tile; is any block of this group selected?
+    bool any = false;
+    if (tid < TT) {
+      const long tk = tok0 + tid;
+      const bool ok = tk < ntok;
+#pragma unroll
+      for (int t = 0; t < TK; ++t) {
+        int id = -1;
+        float lg = 0.f;
+        if (t < topk && ok) {
+          id = top_idx[tk * topk + t];
+          lg = log2f(fmaxf(top_gates[tk * topk + t], 1e-9f));
+          any |= (id >= blk_lo && id <= blk_hi);
+        }
+        idx_lds[tid * TK + t] = id;
+        lg_lds[tid * TK + t] = lg;
+      }
+      float ls = 0.f, dlv = 0.f;
+      if (ok) {
+        const long bb = tk / S, ss = tk % S;
+        ls = lse[(bb * H + h) * S + ss];
+        dlv = delta[(bb * H + h) * S + ss];
+      }
+      lse_lds[tid] = ls;
+      dl_lds[tid] = dlv;
+    }
+    if (!__syncthreads_or(any)) continue;
+
+    // ---- stage Q, dO (natural) and Q^T, dO^T (transposed) for the tile
+    for (int vi = tid; vi < TT * HD / 8; vi += 256) {
+      const int r = vi / (HD / 8), c8 = vi % (HD / 8);
+      const long tk = tok0 + r;
+      uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
+      if (tk < ntok) {
+        const long off = tk * D + (long)h * HD + 8 * c8;
+        qv = *reinterpret_cast<const uint4*>(q + off);
+        dv4 = *reinterpret_cast<const uint4*>(dout + off);
+      }
+      *reinterpret_cast<uint4*>(&q_lds[r * QPAD + 8 * c8]) = qv;
+      *reinterpret_cast<uint4*>(&do_lds[r * QPAD + 8 * c8]) = dv4;
+      const bf16_t* qs = reinterpret_cast<const bf16_t*>(&qv);
+      const bf16_t* ds = reinterpret_cast<const bf16_t*>(&dv4);
+      const int tp = 16 * (r / 16) + slot_perm16(r % 16);  // token position (involution)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int hd = 8 * c8 + e;
+        const int row = 32 * (hd / 32) + row_unperm32(hd % 32);
+        qt_lds[row * TPAD + tp] = qs[e];
+        dot_lds[row * TPAD + tp] = ds[e];
+      }
+    }
+    if constexpr (HD < 32) {
+      // zero the padding rows of the transposed tiles (features >= HD)
+      for (int i = tid; i < 32 * TT; i += 256) {
+        const int row = i / TT, c = i % TT;
+        if (row_perm32(row) >= HD) {
+          qt_lds[row * TPAD + c] = 0;
+          dot_lds[row * TPAD + c] = 0;
+        }
+      }
+    }
+    if constexpr (ALIGNED) {
+      // per (wave block, token) additive term of the exp2 argument
+      const int w = tid >> 6, r = tid & 63;
+      const int e = (sg * 128 + w * 32) / block_size;
+      float c = 0.f;
+      bool sel = false;
+#pragma unroll
+      for (int t = 0; t < TK; ++t)
+        if (t < topk && idx_lds[r * TK + t] == e) {
+          c += lg_lds[r * TK + t];
+          sel = true;
+        }
+      add_lds[w][r] = sel ? c - lse_lds[r] : -INFINITY;
+    }
+    __syncthreads();
+
+    // ---- S = Q K^T and dP = dO V^T (tokens x slots, lanes = slots)
+    f32x16 acc_s[NT], acc_p[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      acc_s[i] = f32x16{};
+      acc_p[i] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (32 * i + col) * QPAD + 16 * ks + 8 * g;
+        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
+        const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[off]);
+        acc_s[i] = mfma32(aq, kf[ks], acc_s[i]);
+        acc_p[i] = mfma32(ad, vf[ks], acc_p[i]);
+      }
+    }
+
+    // ---- P and dS, registers indexed by token
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int r0 = 32 * i + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
+        const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&dl_lds[r0]);
+        f32x4 ad4;
+        if constexpr (ALIGNED) {
+          ad4 = *reinterpret_cast<const f32x4*>(&add_lds[wave][r0]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float c = 0.f;
+            bool sel = false;
+#pragma unroll
+            for (int t = 0; t < TK; ++t)
+              if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
+                c += lg_lds[(r0 + u) * TK + t];
+                sel = true;
+              }
+            ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int vv = 4 * j4 + u;
+          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, ad4[u]));
+          acc_s[i][vv] = p;
+          acc_p[i][vv] = p * (acc_p[i][vv] - dl4[u]);
+        }
+      }
+    }
+
+    // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = tokens)
+    // These two products sum over every token of the batch (thousands of
+    // terms), so P and dS enter as a compensated pair hi + lo of bf16
+    // values (hi = bf16(x), lo = bf16(x - hi)): the bf16 rounding of P/dS
+    // would otherwise dominate the error of small dK/dV entries.
+#pragma unroll
+    for (int kk = 0; kk < TT / 16; ++kk) {
+      const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
+      const bf16x8 bd = pack8(acc_p[kk >> 1], 8 * (kk & 1));
+      bf16x8 bp_lo, bd_lo;
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bp_lo[e] = (__bf16)(acc_s[kk >> 1][8 * (kk & 1) + e] - (float)bp[e]);
+          bd_lo[e] = (__bf16)(acc_p[kk >> 1][8 * (kk & 1) + e] - (float)bd[e]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int off = (32 * j + col) * TPAD + 16 * kk + 8 * g;
+        const bf16x8 a_do = *reinterpret_cast<const bf16x8*>(&dot_lds[off]);
+        const bf16x8 a_q = *reinterpret_cast<const bf16x8*>(&qt_lds[off]);
+        acc_dv[j] = mfma32(a_do, bp, acc_dv[j]);
+        acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
+        if constexpr (SPLIT) {
+          acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
+          acc_dk[j] = mfma32(a_q, bd_lo, acc_dk[j]);
+        }
+      }
+    }
+    __syncthreads();  // LDS tiles are rewritten by the next iteration
+  }
+
+  // ---- fp32 partials of this chunk: part[chunk][slot][h*HD + f]
+  if (slot_ok) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int f0 = 32 * j + 16 * g;
+      if (f0 < HD) {
+        const long base = ((long)chunk * Lq + slot) * D + (long)h * HD + f0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          *reinterpret_cast<f32x4*>(dk_part + base + 4 * u) =
+              f32x4{acc_dk[j][4 * u], acc_dk[j][4 * u + 1], acc_dk[j][4 * u + 2], acc_dk[j][4 * u + 3]};
+          *reinterpret_cast<f32x4*>(dv_part + base + 4 * u) =
+              f32x4{acc_dv[j][4 * u], acc_dv[j][4 * u + 1], acc_dv[j][4 * u + 2], acc_dv[j][4 * u + 3]};
+        }
+      }
+    }
+  }
+}
+
+// dk/dv = sum over chunks (fixed order) of the fp32 partials; dk scaled.
+__global__ void read_bwd_reduce_kv_kernel(const float* __restrict__ dk_part, const float* __restrict__ dv_part,
+                                          bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long n, long stride,
+                                          int n_chunks, float scale) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n / 4; i += (long)gridDim.x * blockDim.x) {
+    f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < n_chunks; ++c) {
+      sk += *reinterpret_cast<const f32x4*>(dk_part + c * stride + 4 * i);
+      sv += *reinterpret_cast<const f32x4*>(dv_part + c * stride + 4 * i);
+    }
+    bf16x4 ok, ov;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ok[u] = (__bf16)(sk[u] * scale);
+      ov[u] = (__bf16)sv[u];
+    }
+    *reinterpret_cast<bf16x4*>(dk + 4 * i) = ok;
+    *reinterpret_cast<bf16x4*>(dv + 4 * i) = ov;
+  }
+}
+
+// d(top_gates) = (sum_h dlog partial) / g  where g >= 1e-9, else 0
+// (the gradient of log(clamp_min(g, 1e-9)), triton_gpu.py:435).
+__global__ void read_bwd_reduce_gates_kernel(const float* __restrict__ dlg_part, const float* __restrict__ top_gates,
+                                             float* __restrict__ dgates, long n, int H) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int h = 0; h < H; ++h) s += dlg_part[(long)h * n + i];
+    const float gt = top_gates[i];
+    dgates[i] = gt >= 1e-9f ? s / gt : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+static float read_scale(int HD) { return (float)(1.0 / __builtin_sqrt((double)HD)); }
+
+template <int HD, int SG, bool AL, int TK>
+static void dq_inst(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
+                    const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
+                    const ReadDims& d, hipStream_t st) {
+  const int n_tiles = (d.S + 127) / 128;
+  const float scale = read_scale(HD);
+  hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)kt, ti, tg,
+                     (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.B, d.S, d.H, d.L,
+                     read_lp(d.L), d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles);
+}
+
+template <int HD, int TK>
+static void dq_hdk(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
+                  const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
+                  const ReadDims& d, hipStream_t st) {
+  constexpr int SGMAX = HD <= 64 ? 64 : 32;
+  if (d.block_size % SGMAX == 0)
+    dq_inst<HD, SGMAX, true, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+  else if (d.block_size % 32 == 0)
+    dq_inst<HD, 32, true, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+  else
+    dq_inst<HD, 32, false, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+}
+
+template <int HD>
+static void dq_hd(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
+                  const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
+                  const ReadDims& d, hipStream_t st) {
+  if (d.topk <= 2)
+    dq_hdk<HD, 2>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+  else
+    dq_hdk<HD, kMaxTopK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+}
+
+hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const void* kt, const int32_t* top_idx,
+                              const float* top_gates, const void* o, const void* dout, const float* lse, void* dq,
+                              float* delta, float* dlg_part, const ReadDims& d, hipStream_t st) {
+  switch (d.HD) {
+    case 16: dq_hd<16>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 32: dq_hd<32>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 64: dq_hd<64>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 128: dq_hd<128>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int read_bwd_chunks(const ReadDims& d) {
+  const long ntok = (long)d.B * d.S;
+  const int n_ttiles = (int)((ntok + 63) / 64);
+  const int per_chunk_wgs = d.H * (read_lq(d.L) / 128);
+  int nc = (512 + per_chunk_wgs - 1) / per_chunk_wgs;
+  if (nc > n_ttiles) nc = n_ttiles;
+  if (nc < 1) nc = 1;
+  return nc;
+}
+
+template <int HD, bool AL, int TK>
+static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg,
+                      const void* dout, const float* lse, const float* delta, float* dkp, float* dvp, int nc,
+                      const ReadDims& d, hipStream_t st) {
+  const long ntok = (long)d.B * d.S;
+  const int n_ttiles = (int)((ntok + 63) / 64);
+  const int tpc = (n_ttiles + nc - 1) / nc;
+  const int Lq = read_lq(d.L);
+  const float alpha = read_scale(HD) * kLog2e;
+  hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(256), 0, st,
+                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)dout, lse, delta,
+                     dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc, tpc);
+}
+
+hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
+                                const float* top_gates, const void* dout, const float* lse, const float* delta,
+                                float* dk_part, float* dv_part, int n_chunks, const ReadDims& d, hipStream_t st) {
+  const bool al = d.block_size % 32 == 0;
+#define NAYLIS_DKDV2(HDV, TKV)                                                                                \
+  if (al)                                                                                                     \
+    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, dk_part, dv_part, n_chunks, d,   \
+                              st);                                                                            \
+  else                                                                                                        \
+    dkdv_inst<HDV, false, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, dk_part, dv_part, n_chunks, d,  \
+                               st);
+#define NAYLIS_DKDV(HDV)          \
+  if (d.topk <= 2) {              \
+    NAYLIS_DKDV2(HDV, 2)          \
+  } else {                        \
+    NAYLIS_DKDV2(HDV, kMaxTopK)   \
+  }
+  switch (d.HD) {
+    case 16: NAYLIS_DKDV(16) break;
+    case 32: NAYLIS_DKDV(32) break;
+    case 64: NAYLIS_DKDV(64) break;
+    case 128: NAYLIS_DKDV(128) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef NAYLIS_DKDV
+#undef NAYLIS_DKDV2
+  return hipGetLastError();
+}
+
+hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const float* dlg_part,
+                                  const float* top_gates, void* dk, void* dv, float* dgates, int n_chunks,
+                                  const ReadDims& d, hipStream_t st) {
+  const long D = (long)d.H * d.HD;
+  const long n = (long)d.L * D;
+  const long stride = (long)read_lq(d.L) * D;
+  long blocks = (n / 4 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
+                     (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD));
+  const long ng = (long)d.B * d.S * d.topk;
+  if (ng > 0) {
+    long gb = (ng + 255) / 256;
+    if (gb > 8192) gb = 8192;
+    hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates, dgates,
+                       ng, d.H);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace naylis

@@ -1,0 +1,332 @@
+// Gated flash read of the shared MoM bank, forward (gfx950).
+//
+// Computes, per (b, s, h):  o = softmax_n(q.k_n / sqrt(hd) + bias[b,s,n]) v_n
+// with bias = log(gate) summed over the token's selections that hit the
+// block of slot n and a hard mask elsewhere (mom_kernels/reference.py:14-61,
+// the structured form of mom_kernels/triton_gpu.py:64-141).  The bias is
+// never materialised: it is one scalar per (token, bank block), folded into
+// the exp2 argument together with the running max.
+//
+// Work decomposition: one workgroup = (b, h, tile of 128 tokens), 4 waves,
+// each wave owns 32 tokens (one MFMA column each).  The tile first marks
+// which bank blocks any of its tokens selects and then walks only those
+// blocks' slot groups (SG slots): S^T = K_g Q^T (slots x tokens, K from LDS,
+// Q^T resident in registers), online softmax per token column, O^T += V_g^T P^T
+// with P^T taken straight from the accumulator registers.
+#include "launch.h"
+#include "read_common.h"
+
+namespace naylis {
+
+// Relayout of a (L, H*HD) bank projection into (H, HDP, Lp): per head, rows
+// are features in row_perm32 order (padded to HDP = max(HD, 32)), columns are
+// slots in slot_perm16 order (padded to Lp = L rounded up to 32), zero fill.
+// This is the A operand of every "X^T . P^T" product of the read.
+__global__ void bank_relayout_kernel(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, int L,
+                                     int Lp, int H, int HD, int HDP) {
+  const long n = (long)H * HDP * Lp;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const int sp = (int)(i % Lp);
+    const int hr = (int)((i / Lp) % HDP);
+    const int h = (int)(i / ((long)Lp * HDP));
+    const int hd = 32 * (hr / 32) + row_perm32(hr % 32);
+    const int slot = 16 * (sp / 16) + slot_perm16(sp % 16);
+    bf16_t v = 0;
+    if (hd < HD && slot < L) v = src[(long)slot * H * HD + (long)h * HD + hd];
+    dst[i] = v;
+  }
+}
+
+template <int HD, int SG, bool ALIGNED, int TK>
+__global__ __launch_bounds__(256) void read_fwd_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
+    float* __restrict__ lse, int B, int S, int H, int L, int Lp, int E, int block_size, int topk,
+    float alpha, int n_tiles) {
+  constexpr int HDP = HD < 32 ? 32 : HD;
+  constexpr int KS = HD / 16;       // K-steps over features for Q.K^T
+  constexpr int NS = SG / 32;       // 32-slot accumulator tiles per group
+  constexpr int NO = HDP / 32;      // 32-feature output tiles
+  constexpr int KPAD = HD + 8;      // LDS row pitch (bf16) of the K tile
+  constexpr int VPAD = SG + 8;      // LDS row pitch (bf16) of the V^T tile
+
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * KPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t vt_lds[HDP * VPAD];
+  __shared__ uint8_t flags[kMaxBlocks];
+  __shared__ uint16_t groups[kMaxGroups];
+  __shared__ int n_active;
+
+  const int G = B * H * n_tiles;
+  const int wid = xcd_remap(blockIdx.x, G);
+  const int tile = wid % n_tiles;
+  const int b = (wid / n_tiles) % B;
+  const int h = wid / (n_tiles * B);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const int s_tok = tile * 128 + wave * 32 + col;
+  const bool tok_ok = s_tok < S;
+  const long tok = (long)b * S + s_tok;
+  const int D = H * HD;
+
+  // ---- routing of this lane's token; active-block flags of the tile
+  TokenRoute<TK> rt;
+  load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
+  for (int e = tid; e < E; e += 256) flags[e] = 0;
+  __syncthreads();
+  if (g == 0 && tok_ok) {
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+  }
+  __syncthreads();
+  const int n_groups = Lp / SG;
+  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
+
+  // ---- Q^T fragments (B operand): lane holds q[token][16*ks + 8*g .. +8]
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (tok_ok)
+      qf[ks] = *reinterpret_cast<const bf16x8*>(q + tok * D + (long)h * HD + 16 * ks + 8 * g);
+    else
+      qf[ks] = bf16x8{};
+  }
+
+  f32x16 acc_o[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) acc_o[j] = f32x16{};
+  float m_run = kNegBig, l_run = 0.f;
+
+  __syncthreads();
+  const int n_act = n_active;
+
+  // staging: K group (SG x HD) and V^T group (HDP x SG) as 16-byte vectors
+  constexpr int KV_VEC = SG * HD / 8;
+  constexpr int VT_VEC = HDP * SG / 8;
+  constexpr int K_PER = (KV_VEC + 255) / 256;
+  constexpr int V_PER = (VT_VEC + 255) / 256;
+  uint4 kreg[K_PER], vreg[V_PER];
+
+  auto load_group = [&](int gi) {
+    const int s0 = gi * SG;
+#pragma unroll
+    for (int r = 0; r < K_PER; ++r) {
+      const int vi = tid + 256 * r;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (vi < KV_VEC) {
+        const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
+        if (s0 + srow < L)
+          val = *reinterpret_cast<const uint4*>(k + (long)(s0 + srow) * D + (long)h * HD + 8 * c8);
+      }
+      kreg[r] = val;
+    }
+#pragma unroll
+    for (int r = 0; r < V_PER; ++r) {
+      const int vi = tid + 256 * r;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (vi < VT_VEC) {
+        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
+        val = *reinterpret_cast<const uint4*>(vt + ((long)h * HDP + hr) * Lp + s0 + 8 * c8);
+      }
+      vreg[r] = val;
+    }
+  };
+  auto store_group = [&]() {
+#pragma unroll
+    for (int r = 0; r < K_PER; ++r) {
+      const int vi = tid + 256 * r;
+      if (vi < KV_VEC) {
+        const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
+        *reinterpret_cast<uint4*>(&k_lds[srow * KPAD + 8 * c8]) = kreg[r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < V_PER; ++r) {
+      const int vi = tid + 256 * r;
+      if (vi < VT_VEC) {
+        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
+        *reinterpret_cast<uint4*>(&vt_lds[hr * VPAD + 8 * c8]) = vreg[r];
+      }
+    }
+  };
+
+  if (n_act > 0) load_group(groups[0]);
+
+  for (int it = 0; it < n_act; ++it) {
+    const int gi = groups[it];
+    __syncthreads();  // previous group's LDS reads are done
+    store_group();
+    __syncthreads();
+    if (it + 1 < n_act) load_group(groups[it + 1]);  // in flight during the math below
+
+    // ---- S^T = K_g . Q^T  (SG slots x 32 tokens per wave)
+    f32x16 acc_s[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      acc_s[i] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * i + col) * KPAD + 16 * ks + 8 * g]);
+        acc_s[i] = mfma32(a, qf[ks], acc_s[i]);
+      }
+    }
+
+    // ---- online softmax over this group, per token column
+    float m_new = m_run;
+    if constexpr (ALIGNED) {
+      bool sel;
+      const float c2 = route_bias(rt, (gi * SG) / block_size, topk, sel);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc_s[i][v]);
+      mx = wave_max_pair(mx);
+      if (sel) m_new = fmaxf(m_run, fmaf(mx, alpha, c2));
+      const float add = sel ? c2 - m_new : -INFINITY;
+      float rs = 0.f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][v], alpha, add));
+          acc_s[i][v] = p;
+          rs += p;
+        }
+      rs = wave_sum_pair(rs);
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run = fmaf(l_run, corr, rs);
+#pragma unroll
+      for (int j = 0; j < NO; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc_o[j][v] *= corr;
+    } else {
+      // generic slot->block lookup per element (block_size not a multiple of SG)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int slot = gi * SG + 32 * i + acc_row(g, v);
+          bool sel = false;
+          float c2 = 0.f;
+          if (slot < L) c2 = route_bias(rt, slot / block_size, topk, sel);
+          const float t = sel ? fmaf(acc_s[i][v], alpha, c2) : -INFINITY;
+          acc_s[i][v] = t;
+          mx = fmaxf(mx, t);
+        }
+      mx = wave_max_pair(mx);
+      m_new = fmaxf(m_run, mx);
+      float rs = 0.f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float p = __builtin_amdgcn_exp2f(acc_s[i][v] - m_new);
+          acc_s[i][v] = p;
+          rs += p;
+        }
+      rs = wave_sum_pair(rs);
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run = fmaf(l_run, corr, rs);
+#pragma unroll
+      for (int j = 0; j < NO; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc_o[j][v] *= corr;
+    }
+    m_run = m_new;
+
+    // ---- O^T += V_g^T . P^T   (P^T fragments come straight from acc_s)
+#pragma unroll
+    for (int kk = 0; kk < SG / 16; ++kk) {
+      const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&vt_lds[(32 * j + col) * VPAD + 16 * kk + 8 * g]);
+        acc_o[j] = mfma32(a, bp, acc_o[j]);
+      }
+    }
+  }
+
+  // ---- epilogue: normalise, store o (bf16) and the log2-domain lse
+  if (tok_ok) {
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int f0 = 32 * j + 16 * g;  // features held by this lane group
+      if (f0 < HD) {
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          lo[e] = (__bf16)(acc_o[j][e] * inv);
+          hi[e] = (__bf16)(acc_o[j][8 + e] * inv);
+        }
+        bf16_t* dst = out + tok * D + (long)h * HD + f0;
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+      }
+    }
+    if (g == 0) lse[((long)b * H + h) * S + s_tok] = m_run + log2f(l_run);
+  }
+}
+
+// ---------------------------------------------------------------------------
+hipError_t launch_bank_relayout(const void* src, void* dst, const ReadDims& d, hipStream_t st) {
+  const int HDP = read_hdp(d.HD), Lp = read_lp(d.L);
+  const long n = (long)d.H * HDP * Lp;
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(bank_relayout_kernel, dim3(blocks), dim3(256), 0, st, (const bf16_t*)src, (bf16_t*)dst, d.L, Lp,
+                     d.H, d.HD, HDP);
+  return hipGetLastError();
+}
+
+template <int HD, int SG, bool AL, int TK>
+static void fwd_inst(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
+                     float* lse, const ReadDims& d, hipStream_t st) {
+  const int n_tiles = (d.S + 127) / 128;
+  const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
+  hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st, (const bf16_t*)q,
+                     (const bf16_t*)k, (const bf16_t*)vt, ti, tg, (bf16_t*)out, lse, d.B, d.S, d.H, d.L,
+                     read_lp(d.L), d.E, d.block_size, d.topk, alpha, n_tiles);
+}
+
+template <int HD, int TK>
+static void fwd_hdk(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
+                   float* lse, const ReadDims& d, hipStream_t st) {
+  constexpr int SGMAX = HD <= 64 ? 128 : 64;
+  if (d.block_size % SGMAX == 0)
+    fwd_inst<HD, SGMAX, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+  else if (d.block_size % 64 == 0)
+    fwd_inst<HD, 64, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+  else if (d.block_size % 32 == 0)
+    fwd_inst<HD, 32, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+  else
+    fwd_inst<HD, 32, false, TK>(q, k, vt, ti, tg, out, lse, d, st);
+}
+
+template <int HD>
+static void fwd_hd(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
+                   float* lse, const ReadDims& d, hipStream_t st) {
+  if (d.topk <= 2)
+    fwd_hdk<HD, 2>(q, k, vt, ti, tg, out, lse, d, st);
+  else
+    fwd_hdk<HD, kMaxTopK>(q, k, vt, ti, tg, out, lse, d, st);
+}
+
+hipError_t launch_read_fwd(const void* q, const void* k, const void* vt, const int32_t* top_idx,
+                           const float* top_gates, void* out, float* lse, const ReadDims& d, hipStream_t st) {
+  switch (d.HD) {
+    case 16: fwd_hd<16>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
+    case 32: fwd_hd<32>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
+    case 64: fwd_hd<64>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
+    case 128: fwd_hd<128>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace naylis

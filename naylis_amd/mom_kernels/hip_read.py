@@ -1,0 +1,111 @@
+"""Autograd binding of the HIP gated flash read (C ABI: naylis_mom_read_*).
+
+Drop-in for mom_kernels/triton_gpu.py:323-439 of the reference: same
+``mom_read(q_sh, k, v, top_idx, top_gates, *, num_blocks, block_size)``
+signature, same preconditions (triton_gpu.py:420-429), same gradient set
+(dq, dk, dv, d top_gates; triton_gpu.py:409 plus the log-gate transform of
+triton_gpu.py:435, which the kernels fold in).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class MomReadFunction(torch.autograd.Function):
+    """Forward saves (q, k, v, top_idx, top_gates, o, lse); backward runs the
+    dq / dk-dv / reduce launches of the library."""
+
+    @staticmethod
+    def forward(ctx, q_sh, k, v, top_idx, top_gates, num_blocks, block_size):
+        lib = _lib.load()
+        B, S, H, HD = q_sh.shape
+        topk = top_idx.shape[-1]
+        dev = q_sh.device
+        out = torch.empty_like(q_sh)
+        lse = torch.empty((B, H, S), device=dev, dtype=torch.float32)
+        nbytes = lib.naylis_mom_read_workspace_bytes(B, S, H, HD, num_blocks, block_size, topk)
+        if nbytes == 0:
+            _lib.check(_lib.NAYLIS_ERR_ARG)
+        ws = _workspace(nbytes, dev)
+        with torch.cuda.device(dev):
+            rc = lib.naylis_mom_read_fwd(
+                q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
+                out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
+                B, S, H, HD, num_blocks, block_size, topk, _stream(dev))
+        _lib.check(rc)
+        ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, out, lse)
+        ctx.geom = (num_blocks, block_size)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        q_sh, k, v, top_idx, top_gates, out, lse = ctx.saved_tensors
+        num_blocks, block_size = ctx.geom
+        B, S, H, HD = q_sh.shape
+        topk = top_idx.shape[-1]
+        dev = q_sh.device
+        dout = dout.contiguous()
+        if dout.dtype != q_sh.dtype:
+            dout = dout.to(q_sh.dtype)
+        dq = torch.empty_like(q_sh)
+        dk = torch.empty_like(k)
+        dv = torch.empty_like(v)
+        dgates = torch.empty_like(top_gates)
+        nbytes = lib.naylis_mom_read_workspace_bytes(B, S, H, HD, num_blocks, block_size, topk)
+        ws = _workspace(nbytes, dev)
+        with torch.cuda.device(dev):
+            rc = lib.naylis_mom_read_bwd(
+                q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
+                out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                dgates.data_ptr(), ws.data_ptr(), ws.numel(),
+                B, S, H, HD, num_blocks, block_size, topk, _stream(dev))
+        _lib.check(rc)
+        return dq, dk, dv, None, dgates, None, None
+
+
+def mom_read(q_sh, k, v, top_idx, top_gates, *, num_blocks, block_size):
+    """Flash MoM read with the in-register gate bias (ROCm, bf16).
+
+    q_sh (B, S, H, hd) bf16; shared k/v (L, D) bf16; per-token (top_idx,
+    top_gates) (B, S, k); returns (B, S, H, hd) bf16.  Raises RuntimeError
+    on the reference's preconditions (triton_gpu.py:420-429) and when the
+    HIP library is missing — there is no eager fallback.
+    """
+    if k.dim() != 2 or v.dim() != 2:
+        raise RuntimeError("hip mom_read: shared K/V (L, D) only, got batched inputs")
+    if q_sh.dtype != torch.bfloat16:
+        raise RuntimeError(f"hip mom_read requires bf16 activations, got {q_sh.dtype}")
+    if k.shape[0] != num_blocks * block_size:
+        raise RuntimeError(
+            f"hip mom_read: bank is {k.shape[0]} slots but num_blocks "
+            f"({num_blocks}) x block_size ({block_size}) disagrees")
+    if q_sh.dim() != 4:
+        raise RuntimeError(f"hip mom_read: q_sh must be (B, S, H, hd), got {tuple(q_sh.shape)}")
+    B, S, H, HD = q_sh.shape
+    if k.shape[1] != H * HD or v.shape != k.shape:
+        raise RuntimeError(
+            f"hip mom_read: k/v must be (L, H*hd) = ({k.shape[0]}, {H * HD}), got {tuple(k.shape)} / {tuple(v.shape)}")
+    if top_idx.shape[:2] != (B, S) or top_gates.shape != top_idx.shape:
+        raise RuntimeError("hip mom_read: top_idx / top_gates must both be (B, S, top_k)")
+    if q_sh.device.type != "cuda" or torch.version.hip is None:
+        raise RuntimeError(f"hip mom_read: needs a ROCm device tensor, got {q_sh.device}")
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        k = k.to(torch.bfloat16)
+        v = v.to(torch.bfloat16)
+    q_sh = q_sh.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    top_idx = top_idx.to(torch.int32).contiguous()
+    top_gates = top_gates.float().contiguous()
+    return MomReadFunction.apply(q_sh, k, v, top_idx, top_gates, int(num_blocks), int(block_size))
