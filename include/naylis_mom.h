@@ -31,9 +31,14 @@ extern "C" {
 #define NAYLIS_ERR_WORKSPACE 2 /* workspace smaller than the query returned */
 #define NAYLIS_ERR_HIP 3       /* a HIP launch failed */
 
+#define NAYLIS_DTYPE_F32 0
+#define NAYLIS_DTYPE_BF16 1
+
 #define NAYLIS_MAX_TOPK 8
 #define NAYLIS_MAX_BLOCKS 1024
 #define NAYLIS_MAX_SLOTS 16384
+#define NAYLIS_ROUTER_MAX_RANK 64
+#define NAYLIS_ROUTER_MAX_BLOCKS 64
 
 int naylis_mom_abi_version(void);
 const char* naylis_mom_last_error(void);
@@ -74,6 +79,65 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
                         void* dk, void* dv, float* dgates, void* workspace, size_t workspace_bytes, int64_t B,
                         int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
                         int64_t top_k, void* stream);
+
+/* -------------------------------------------------------------- router ---
+ * The causal prefix-mean router of MoMLayer, which the reference runs as
+ * eager torch ops with no kernel boundary: model.py:169-187
+ * (_prefix_mean, _router_logits) and model.py:209-220 (noise, softmax probs,
+ * topk, gates); mirror in mom_kernels/reference.py:32-36,75-84.
+ *
+ *   x          (B, T, D) fp32 or bf16 (x_dtype: NAYLIS_DTYPE_*)
+ *   w_down     (R, D) fp32          router_down.weight
+ *   w_up       (E, R) fp32          router_up.weight
+ *   noise      (B, T, E) fp32 or NULL; topk ranks logits + noise_scale*noise
+ *              (the Gumbel draw of model.py:210 or any additive logit bias)
+ *   logits     (B, T, E) fp32       clean router logits
+ *   probs      (B, T, E) fp32       softmax(logits)
+ *   top_idx    (B, T, k) int32      descending by perturbed logit; ties ->
+ *                                   lowest block id
+ *   top_gates  (B, T, k) fp32       softmax of the selected perturbed logits
+ *   act        (B, T, R) fp32       tanh activations, saved for the backward
+ *   h_out      (B, T, D) fp32 or NULL: the prefix mean h_t (bit-exact with
+ *              the reference's fp32 cumsum / (t+1))
+ * Constraints: R <= 64, E <= 64, 1 <= k <= min(8, E).
+ */
+size_t naylis_mom_router_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k);
+
+int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* noise,
+                          float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
+                          float* act, float* h_out, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                          int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream);
+
+/* Backward of the router: any of d_gates (B,T,k), d_probs (B,T,E), d_logits
+ * (B,T,E) may be NULL (no gradient from that output).  Writes dx (same dtype
+ * and shape as x), dw_down (R, D) and dw_up (E, R), both fp32, reduced over
+ * all tokens in a fixed order. */
+int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
+                          const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
+                          const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
+                          void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
+                          int64_t E, int64_t top_k, void* stream);
+
+/* ------------------------------------------------------------ bank K/V ---
+ * Projection of the shared bank, once per layer and shared by the batch:
+ * model.py:253-256 (`k_proj(M_blocks.view(L, D))`, `v_proj(...)`), mirror in
+ * mom_kernels/reference.py:86-89.  The reference runs two nn.Linear calls.
+ *
+ *   slots  (L, D_in) bf16        M_blocks viewed as L slots
+ *   w_k, w_v (D_out, D_in) bf16  k_proj.weight, v_proj.weight
+ *   k_out, v_out (L, D_out) bf16
+ * Constraint: D_in a multiple of 8.
+ */
+int naylis_mom_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, void* k_out, void* v_out, int64_t L,
+                           int64_t D_in, int64_t D_out, void* stream);
+
+/* Backward: d_slots = dk w_k + dv w_v  (L, D_in), dw_k = dk^T slots and
+ * dw_v = dv^T slots (D_out, D_in); gradients are written in the requested
+ * dtype (NAYLIS_DTYPE_F32 or _BF16), accumulation is fp32.  D_out a multiple
+ * of 8. */
+int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, const void* dk, const void* dv,
+                           void* d_slots, int slots_grad_dtype, void* dw_k, void* dw_v, int w_grad_dtype, int64_t L,
+                           int64_t D_in, int64_t D_out, void* stream);
 
 #ifdef __cplusplus
 }

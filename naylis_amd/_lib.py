@@ -33,6 +33,14 @@ SIGNATURES = {
     "naylis_mom_read_workspace_bytes": (_size_t, [_i64] * 7),
     "naylis_mom_read_fwd": (_int, [_c_void_p] * 7 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
     "naylis_mom_read_bwd": (_int, [_c_void_p] * 12 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_router_workspace_bytes": (_size_t, [_i64] * 6),
+    "naylis_mom_router_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _float] + [_c_void_p] * 6
+                              + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
+    "naylis_mom_router_bwd": (_int, [_c_void_p, _int] + [_c_void_p] * 12 + [_c_void_p, _size_t] + [_i64] * 6
+                              + [_c_void_p]),
+    "naylis_mom_bank_kv_fwd": (_int, [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p]),
+    "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
+                               + [_c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,166 @@
+// Bank K/V projection of the MoM layer (gfx950, bf16 MFMA, fp32 accumulate).
+//
+// Forward (model.py:253-256, reference.py:86-89), once per layer and shared by
+// the whole batch:   K = slots W_k^T,  V = slots W_v^T,  slots = M_blocks.view(L, D)
+// Backward:           d_slots = dK W_k + dV W_v      (one GEMM, K-dim concatenated)
+//                     dW_k = dK^T slots,  dW_v = dV^T slots
+//
+// One generic tile kernel C(MxN) = sum_k A(m,k) B(k,n) covers the three layouts;
+// A and B are staged into LDS K-contiguous ([row][k]) whatever their global
+// layout, so the MFMA fragments are single 16-byte LDS reads.  Tile 64x64x32,
+// 4 waves in 2x2, one 32x32 accumulator per wave.  Each operand may be split
+// along K at K1 into two tensors (A1|A2, B1;B2), which is how the two terms of
+// d_slots become one product.
+#include "common.h"
+#include "launch_bank.h"
+
+namespace naylis {
+
+struct GemmOperand {
+  const bf16_t* p1;  // k < K1
+  const bf16_t* p2;  // k >= K1 (may equal p1 when K1 >= K)
+  long ld;           // leading dimension (elements)
+};
+
+struct GemmProblem {
+  GemmOperand a, b;
+  void* c;
+  long ldc;
+};
+
+struct GemmBatch {
+  GemmProblem prob[2];
+};
+
+constexpr int GBM = 64, GBN = 64, GBK = 32, GPAD = GBK + 8;
+
+// Element (row, k) of an operand: K-major -> p[row*ld + k]; else p[k*ld + row].
+template <bool KMAJOR>
+__device__ __forceinline__ void stage_operand(const GemmOperand& op, int K1, int rows, int K, int row0, int k0,
+                                              bf16_t* lds, int tid) {
+  if constexpr (KMAJOR) {
+    // thread -> (row = tid/4, 8 consecutive k)
+    const int r = tid >> 2, k8 = (tid & 3) * 8;
+    const int gr = row0 + r, gk = k0 + k8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < rows) {
+      const bf16_t* p = gk < K1 ? op.p1 + (long)gr * op.ld + gk : op.p2 + (long)gr * op.ld + (gk - K1);
+      if (gk + 8 <= K && (gk >= K1 || gk + 8 <= K1)) {
+        v = *reinterpret_cast<const uint4*>(p);
+      } else {
+        bf16_t* ve = reinterpret_cast<bf16_t*>(&v);
+        for (int e = 0; e < 8; ++e) {
+          const int kk = gk + e;
+          if (kk < K) ve[e] = kk < K1 ? op.p1[(long)gr * op.ld + kk] : op.p2[(long)gr * op.ld + (kk - K1)];
+        }
+      }
+    }
+    *reinterpret_cast<uint4*>(&lds[r * GPAD + k8]) = v;
+  } else {
+    // thread -> (k = tid/8, 8 consecutive rows), transposed into [row][k]
+    const int kk = tid >> 3, r8 = (tid & 7) * 8;
+    const int gk = k0 + kk, gr = row0 + r8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gk < K) {
+      const bf16_t* base = gk < K1 ? op.p1 + (long)gk * op.ld : op.p2 + (long)(gk - K1) * op.ld;
+      if (gr + 8 <= rows && ((((uintptr_t)(base + gr)) & 15) == 0)) {
+        v = *reinterpret_cast<const uint4*>(base + gr);
+      } else {
+        bf16_t* ve = reinterpret_cast<bf16_t*>(&v);
+        for (int e = 0; e < 8; ++e)
+          if (gr + e < rows) ve[e] = base[gr + e];
+      }
+    }
+    const bf16_t* ve = reinterpret_cast<const bf16_t*>(&v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lds[(r8 + e) * GPAD + kk] = ve[e];
+  }
+}
+
+template <bool A_KMAJOR, bool B_KMAJOR, bool OUT_F32>
+__global__ __launch_bounds__(256) void bank_gemm_kernel(GemmBatch batch, int M, int N, int K, int K1) {
+  __shared__ __attribute__((aligned(16))) bf16_t a_lds[GBM * GPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t b_lds[GBN * GPAD];
+  const GemmProblem& P = batch.prob[blockIdx.z];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, col = lane & 31;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
+  f32x16 acc = f32x16{};
+  for (int k0 = 0; k0 < K; k0 += GBK) {
+    __syncthreads();
+    stage_operand<A_KMAJOR>(P.a, K1, M, K, m0, k0, a_lds, tid);
+    stage_operand<B_KMAJOR>(P.b, K1, N, K, n0, k0, b_lds, tid);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < GBK / 16; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&a_lds[(wm * 32 + col) * GPAD + 16 * ks + 8 * g]);
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&b_lds[(wn * 32 + col) * GPAD + 16 * ks + 8 * g]);
+      acc = mfma32(a, b, acc);
+    }
+  }
+  const int n = n0 + wn * 32 + col;
+  if (n < N) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = m0 + wm * 32 + acc_row(g, v);
+      if (m < M) {
+        if constexpr (OUT_F32)
+          reinterpret_cast<float*>(P.c)[(long)m * P.ldc + n] = acc[v];
+        else
+          reinterpret_cast<bf16_t*>(P.c)[(long)m * P.ldc + n] = f32_to_bf16(acc[v]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+hipError_t launch_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, void* k_out, void* v_out, int L,
+                              int D_in, int D_out, hipStream_t st) {
+  GemmBatch bt{};
+  for (int z = 0; z < 2; ++z) {
+    GemmProblem& P = bt.prob[z];
+    P.a = {(const bf16_t*)slots, (const bf16_t*)slots, D_in};
+    const bf16_t* w = (const bf16_t*)(z == 0 ? w_k : w_v);
+    P.b = {w, w, D_in};  // B(k, n) = W[n][k]: K-major
+    P.c = z == 0 ? k_out : v_out;
+    P.ldc = D_out;
+  }
+  const dim3 grid((D_out + GBN - 1) / GBN, (L + GBM - 1) / GBM, 2);
+  hipLaunchKernelGGL((bank_gemm_kernel<true, true, false>), grid, dim3(256), 0, st, bt, L, D_out, D_in, D_in);
+  return hipGetLastError();
+}
+
+hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, const void* dk, const void* dv,
+                              void* d_slots, bool slots_f32, void* dw_k, void* dw_v, bool w_f32, int L, int D_in,
+                              int D_out, hipStream_t st) {
+  // d_slots (L x D_in) = [dK | dV] (L x 2D_out) . [W_k ; W_v] (2D_out x D_in)
+  GemmBatch b1{};
+  b1.prob[0].a = {(const bf16_t*)dk, (const bf16_t*)dv, D_out};      // A(m=l, k=o): K-major
+  b1.prob[0].b = {(const bf16_t*)w_k, (const bf16_t*)w_v, D_in};     // B(k=o, n=j) = W[o][j]: N-contiguous
+  b1.prob[0].c = d_slots;
+  b1.prob[0].ldc = D_in;
+  const dim3 g1((D_in + GBN - 1) / GBN, (L + GBM - 1) / GBM, 1);
+  if (slots_f32)
+    hipLaunchKernelGGL((bank_gemm_kernel<true, false, true>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out);
+  else
+    hipLaunchKernelGGL((bank_gemm_kernel<true, false, false>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out);
+  // dW (D_out x D_in) = dK^T (D_out x L) . slots (L x D_in)
+  GemmBatch b2{};
+  for (int z = 0; z < 2; ++z) {
+    GemmProblem& P = b2.prob[z];
+    const bf16_t* g = (const bf16_t*)(z == 0 ? dk : dv);
+    P.a = {g, g, D_out};                                              // A(m=o, k=l) = dK[l][o]: M-contiguous
+    P.b = {(const bf16_t*)slots, (const bf16_t*)slots, D_in};         // B(k=l, n=j) = slots[l][j]: N-contiguous
+    P.c = z == 0 ? dw_k : dw_v;
+    P.ldc = D_in;
+  }
+  const dim3 g2((D_in + GBN - 1) / GBN, (D_out + GBM - 1) / GBM, 2);
+  if (w_f32)
+    hipLaunchKernelGGL((bank_gemm_kernel<false, false, true>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L);
+  else
+    hipLaunchKernelGGL((bank_gemm_kernel<false, false, false>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L);
+  return hipGetLastError();
+}
+
+}  // namespace naylis

@@ -12,6 +12,8 @@
 
 #include "../../include/naylis_mom.h"
 #include "launch.h"
+#include "launch_router.h"
+#include "launch_bank.h"
 
 using namespace naylis;
 
@@ -94,6 +96,36 @@ ReadWs plan_read_ws(const ReadDims& d) {
   return w;
 }
 
+int check_router_dims(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, RouterDims* d) {
+  if (B < 0 || T < 0 || D <= 0)
+    return fail(NAYLIS_ERR_ARG, "mom_route: bad shape B=%lld T=%lld D=%lld", (long long)B, (long long)T,
+                (long long)D);
+  if (R < 1 || R > NAYLIS_ROUTER_MAX_RANK)
+    return fail(NAYLIS_ERR_ARG, "mom_route: router rank %lld must be in [1, %d]", (long long)R,
+                NAYLIS_ROUTER_MAX_RANK);
+  if (E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS)
+    return fail(NAYLIS_ERR_ARG, "mom_route: num_blocks %lld must be in [1, %d]", (long long)E,
+                NAYLIS_ROUTER_MAX_BLOCKS);
+  if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > E)
+    return fail(NAYLIS_ERR_ARG, "mom_route: top_k %lld must be in [1, min(%d, num_blocks=%lld)]", (long long)top_k,
+                NAYLIS_MAX_TOPK, (long long)E);
+  if (B * T > ((int64_t)1 << 30) || D > (1 << 20))
+    return fail(NAYLIS_ERR_ARG, "mom_route: problem too large");
+  d->B = (int)B;
+  d->T = (int)T;
+  d->D = (int)D;
+  d->R = (int)R;
+  d->E = (int)E;
+  d->topk = (int)top_k;
+  return NAYLIS_OK;
+}
+
+int check_dtype(int dt, const char* what) {
+  if (dt != NAYLIS_DTYPE_F32 && dt != NAYLIS_DTYPE_BF16)
+    return fail(NAYLIS_ERR_ARG, "%s: unsupported dtype code %d (0 = fp32, 1 = bf16)", what, dt);
+  return NAYLIS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -163,6 +195,89 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   if (rc) return rc;
   return hip_status(launch_read_bwd_reduce(dkp, dvp, dlg, top_gates, dk, dv, dgates, w.n_chunks, d, st),
                     "mom_read_bwd reduce");
+}
+
+size_t naylis_mom_router_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k) {
+  RouterDims d;
+  if (check_router_dims(B, T, D, R, E, top_k, &d) != NAYLIS_OK) return 0;
+  return plan_router_ws(d).total;
+}
+
+int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* noise,
+                          float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
+                          float* act, float* h_out, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                          int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream) {
+  RouterDims d;
+  int rc = check_router_dims(B, T, D, R, E, top_k, &d);
+  if (rc) return rc;
+  if ((rc = check_dtype(x_dtype, "mom_route"))) return rc;
+  if (B * T == 0) return NAYLIS_OK;
+  if (!x || !w_down || !w_up || !logits || !probs || !top_idx || !top_gates || !act || !workspace)
+    return fail(NAYLIS_ERR_ARG, "mom_route_fwd: null pointer argument");
+  const RouterWs w = plan_router_ws(d);
+  if (workspace_bytes < w.fwd_total)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_route_fwd: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, w.fwd_total);
+  return hip_status(launch_router_fwd(x, x_dtype == NAYLIS_DTYPE_BF16, w_down, w_up, noise, noise_scale, logits, probs,
+                                      top_idx, top_gates, act, h_out, workspace, d, (hipStream_t)stream),
+                    "mom_route_fwd");
+}
+
+int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
+                          const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
+                          const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
+                          void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
+                          int64_t E, int64_t top_k, void* stream) {
+  RouterDims d;
+  int rc = check_router_dims(B, T, D, R, E, top_k, &d);
+  if (rc) return rc;
+  if ((rc = check_dtype(x_dtype, "mom_route"))) return rc;
+  if (!w_down || !w_up || !dw_down || !dw_up || !workspace)
+    return fail(NAYLIS_ERR_ARG, "mom_route_bwd: null pointer argument");
+  if (B * T > 0 && (!x || !act || !probs || !top_idx || !top_gates || !dx))
+    return fail(NAYLIS_ERR_ARG, "mom_route_bwd: null pointer argument");
+  const RouterWs w = plan_router_ws(d);
+  if (workspace_bytes < w.total)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_route_bwd: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, w.total);
+  return hip_status(launch_router_bwd(x, x_dtype == NAYLIS_DTYPE_BF16, w_down, w_up, act, probs, top_idx, top_gates,
+                                      d_gates, d_probs, d_logits, dx, dw_down, dw_up, workspace, d,
+                                      (hipStream_t)stream),
+                    "mom_route_bwd");
+}
+
+int naylis_mom_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, void* k_out, void* v_out, int64_t L,
+                           int64_t D_in, int64_t D_out, void* stream) {
+  if (L < 0 || D_in <= 0 || D_out <= 0 || L > NAYLIS_MAX_SLOTS || D_in > 65536 || D_out > 65536)
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv: bad shape L=%lld D_in=%lld D_out=%lld", (long long)L,
+                (long long)D_in, (long long)D_out);
+  if (D_in % 8 != 0) return fail(NAYLIS_ERR_ARG, "mom_bank_kv: D_in (%lld) must be a multiple of 8", (long long)D_in);
+  if (L == 0) return NAYLIS_OK;
+  if (!slots || !w_k || !w_v || !k_out || !v_out) return fail(NAYLIS_ERR_ARG, "mom_bank_kv_fwd: null pointer argument");
+  return hip_status(launch_bank_kv_fwd(slots, w_k, w_v, k_out, v_out, (int)L, (int)D_in, (int)D_out,
+                                       (hipStream_t)stream),
+                    "mom_bank_kv_fwd");
+}
+
+int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, const void* dk, const void* dv,
+                           void* d_slots, int slots_grad_dtype, void* dw_k, void* dw_v, int w_grad_dtype, int64_t L,
+                           int64_t D_in, int64_t D_out, void* stream) {
+  if (L < 0 || D_in <= 0 || D_out <= 0 || L > NAYLIS_MAX_SLOTS || D_in > 65536 || D_out > 65536)
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv: bad shape L=%lld D_in=%lld D_out=%lld", (long long)L,
+                (long long)D_in, (long long)D_out);
+  if (D_in % 8 != 0 || D_out % 8 != 0)
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_bwd: D_in (%lld) and D_out (%lld) must be multiples of 8",
+                (long long)D_in, (long long)D_out);
+  int rc;
+  if ((rc = check_dtype(slots_grad_dtype, "mom_bank_kv_bwd"))) return rc;
+  if ((rc = check_dtype(w_grad_dtype, "mom_bank_kv_bwd"))) return rc;
+  if (!w_k || !w_v || !dw_k || !dw_v) return fail(NAYLIS_ERR_ARG, "mom_bank_kv_bwd: null pointer argument");
+  if (L > 0 && (!slots || !dk || !dv || !d_slots))
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_bwd: null pointer argument");
+  return hip_status(launch_bank_kv_bwd(slots, w_k, w_v, dk, dv, d_slots, slots_grad_dtype == NAYLIS_DTYPE_F32, dw_k,
+                                       dw_v, w_grad_dtype == NAYLIS_DTYPE_F32, (int)L, (int)D_in, (int)D_out,
+                                       (hipStream_t)stream),
+                    "mom_bank_kv_bwd");
 }
 
 }  // extern "C"

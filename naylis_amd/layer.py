@@ -1,0 +1,133 @@
+"""MoMLayer on MI355X: the reference's layer with every hot op on HIP kernels.
+
+Same constructor, parameter names and forward contract as model.py:71-276
+(``MoMLayer(d_model, n_heads, mem_size, block_size, top_blocks,
+router_rank, use_kernel, mom_grad_ckpt)``; parameters router_down,
+router_up, q_proj, k_proj, v_proj, o_proj, mom_scale), so state dicts move
+between the two unchanged.  The forward is
+
+    logits, probs, idx, gates = mom_route(x)            # fused router kernel
+    K, V  = mom_bank_kv(M_blocks)                       # MFMA bank projection
+    out   = mom_read(q_proj(x), K, V, idx, gates)       # gated flash read
+    y     = mom_scale * o_proj(out)
+
+q_proj / o_proj stay torch linears (hipBLASLt).  There is one backend: the
+HIP kernels (``use_kernel`` is accepted for signature compatibility).  The
+eager SDPA path of model.py:262-275 is the parity oracle and lives in
+``oracle/``, outside the product.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import mom_kernels
+
+__all__ = ["MoMLayer", "mom_aux_loss"]
+
+
+class MoMLayer(nn.Module):
+    """Mixture-of-Memory read over a shared learnable bank, causal routing."""
+
+    def __init__(self, d_model: int, n_heads: int, mem_size: int, block_size: int, top_blocks: int,
+                 router_rank: int, use_kernel: bool = True, mom_grad_ckpt: bool = False):
+        super().__init__()
+        # contract checks of model.py:125-133
+        if d_model % n_heads != 0:
+            raise ValueError(f"d_model ({d_model}) must be divisible by n_heads ({n_heads})")
+        if mem_size % block_size != 0:
+            raise ValueError(f"mem_size ({mem_size}) must be a multiple of block_size ({block_size})")
+        if top_blocks > mem_size // block_size:
+            raise ValueError(
+                f"top_blocks ({top_blocks}) exceeds the number of memory blocks "
+                f"({mem_size // block_size} = mem_size {mem_size} // block_size {block_size})")
+        self.num_blocks = mem_size // block_size
+        self.block_size = block_size
+        self.top_blocks = top_blocks
+        self.mem_slots = mem_size
+        self.n_heads = n_heads
+        self.head_dim = d_model // n_heads
+
+        self.router_down = nn.Linear(d_model, router_rank, bias=False)
+        self.router_up = nn.Linear(router_rank, self.num_blocks, bias=False)
+        self.q_proj = nn.Linear(d_model, d_model, bias=False)
+        self.k_proj = nn.Linear(d_model, d_model, bias=False)
+        self.v_proj = nn.Linear(d_model, d_model, bias=False)
+        self.o_proj = nn.Linear(d_model, d_model, bias=False)
+        self.mom_scale = nn.Parameter(torch.zeros(1))
+
+        self.last_router_probs = None
+        self.last_top_idx = None
+        self.last_entropy = None
+        self.last_dead_frac = None
+        self.noise_scale = 1.0
+        self.use_kernel = use_kernel
+        self.mom_grad_ckpt = mom_grad_ckpt
+        self._kernel_mode = None
+
+    def _resolve_kernel(self, x):
+        mode = mom_kernels.resolve_mode(x.device, x.dtype, head_dim=self.head_dim)
+        mom_kernels.announce(mode)
+        return mode
+
+    def route(self, x, noise=None):
+        """Router outputs (logits, probs, top_idx, top_gates) — model.py:207-220."""
+        return mom_kernels.mom_route(x, self.router_down.weight, self.router_up.weight, self.top_blocks,
+                                     noise=noise, noise_scale=self.noise_scale)
+
+    def forward(self, x, M_blocks):
+        B, S, D = x.shape
+        if self._kernel_mode is None:
+            self._kernel_mode = self._resolve_kernel(x)
+        noise = None
+        if self.training and self.noise_scale > 0:
+            # the Gumbel draw of model.py:210, same shape/dtype as the logits
+            u = torch.rand((B, S, self.num_blocks), device=x.device, dtype=torch.float32)
+            noise = -torch.log(-torch.log(u + 1e-9) + 1e-9)
+        _, router_probs, top_idx, top_gates = self.route(x, noise)
+        if self.training:
+            self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
+            self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
+        if self.mom_grad_ckpt and self.training and torch.is_grad_enabled():
+            out = torch.utils.checkpoint.checkpoint(
+                self._read, x, top_idx, top_gates, M_blocks, use_reentrant=False, preserve_rng_state=False)
+        else:
+            out = self._read(x, top_idx, top_gates, M_blocks)
+        return self.mom_scale * out
+
+    def _read(self, x, top_idx, top_gates, M_blocks):
+        """q projection, bank K/V, gated flash read, o projection (model.py:241-276)."""
+        B, S, D = x.shape
+        q_sh = self.q_proj(x).view(B, S, self.n_heads, self.head_dim)
+        k, v = mom_kernels.mom_bank_kv(M_blocks, self.k_proj.weight, self.v_proj.weight, mem_slots=self.mem_slots)
+        out = mom_kernels.mom_read(q_sh, k, v, top_idx, top_gates, num_blocks=self.num_blocks,
+                                   block_size=self.block_size, mode=self._kernel_mode)
+        return self.o_proj(out.reshape(B, S, D))
+
+
+def mom_aux_loss(layers):
+    """Load-balance aux loss averaged over MoM layers, plus per-layer router
+    entropy / dead-block fraction — model.py:476-517 (`_collect_mom_aux_loss`),
+    consuming the router probs the fused kernel emits."""
+    aux = None
+    count = 0
+    for m in layers:
+        if not isinstance(m, MoMLayer) or m.last_router_probs is None or m.last_top_idx is None:
+            continue
+        probs = m.last_router_probs.float()
+        top_idx = m.last_top_idx
+        blocks = torch.arange(m.num_blocks, device=top_idx.device)
+        sel_mask = (top_idx.unsqueeze(2) == blocks.view(1, 1, -1)).any(1)
+        frac_selected = sel_mask.to(probs.dtype).mean(dim=0)
+        mean_prob = probs.mean(dim=0)
+        term = m.num_blocks * (frac_selected * mean_prob).sum()
+        aux = term if aux is None else aux + term
+        entropy = -(probs * probs.clamp_min(1e-9).log()).sum(-1).mean()
+        m.last_entropy = entropy.detach()
+        m.last_dead_frac = (~sel_mask.any(0)).to(probs.dtype).mean().detach()
+        m.last_router_probs = None
+        m.last_top_idx = None
+        count += 1
+    if count == 0:
+        return torch.zeros(())
+    return aux / count

@@ -1,0 +1,139 @@
+"""GPU parity of the bank K/V GEMM and of the whole MoMLayer (router + bank +
+read + projections) against the CPU oracle layer (model.py:71-276,
+mom_kernels/reference.py:64-95), forward and backward.
+
+Layer checks mirror the reference's tests/test_parity.py §1 (layer ==
+reference), §3a (causality, bitwise), §13 (gradient checkpointing recomputes
+exactly) and probe.py C1-C3 (gradients finite, router and bank alive).
+"""
+import pytest
+import torch
+
+import oracle
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("L,D_in,D_out", [(1024, 1024, 1024), (64, 32, 32), (144, 48, 48), (4096, 1536, 1536)])
+def test_bank_kv(L, D_in, D_out, dev):
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(1)
+    M = (torch.randn(L, D_in, generator=g) * 0.5).bfloat16()
+    wk = (torch.randn(D_out, D_in, generator=g) * 0.03).bfloat16()
+    wv = (torch.randn(D_out, D_in, generator=g) * 0.03).bfloat16()
+    dk = torch.randn(L, D_out, generator=g).bfloat16()
+    dv = torch.randn(L, D_out, generator=g).bfloat16()
+    Md, wkd, wvd = (t.to(dev).requires_grad_(True) for t in (M, wk, wv))
+    k, v = mom_kernels.mom_bank_kv(Md, wkd, wvd, mem_slots=L)
+    torch.autograd.backward([k, v], [dk.to(dev), dv.to(dev)])
+    Mr, wkr, wvr = (t.float().requires_grad_(True) for t in (M, wk, wv))
+    kr, vr = oracle.bank_kv(Mr, wkr, wvr)
+    torch.autograd.backward([kr, vr], [dk.float(), dv.float()])
+    assert_close(k, kr, "K")
+    assert_close(v, vr, "V")
+    assert_close(Md.grad, Mr.grad, "dM")
+    assert_close(wkd.grad, wkr.grad, "dW_k")
+    assert_close(wvd.grad, wvr.grad, "dW_v")
+
+
+def build_pair(D, H, NB, BS, K, R, seed=7, bank_scale=0.5, mom_scale=0.5):
+    from naylis_amd.layer import MoMLayer
+    torch.manual_seed(seed)
+    layer = MoMLayer(d_model=D, n_heads=H, mem_size=NB * BS, block_size=BS, top_blocks=K, router_rank=R)
+    layer.mom_scale.data.fill_(mom_scale)
+    for lin in (layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+        lin.weight.data = lin.weight.data.bfloat16().float()  # identical bf16 values on both sides
+    ref = oracle.OracleMoMLayer(D, H, NB * BS, BS, K, R)
+    ref.load_state_dict(layer.state_dict())
+    g = torch.Generator().manual_seed(seed + 1)
+    M = (torch.randn(NB, BS * D, generator=g) * bank_scale).bfloat16()
+    return layer, ref, M
+
+
+LAYER_CASES = [
+    # B, S, D, H, NB, BS, K, R
+    (2, 64, 32, 2, 4, 16, 2, 8),       # reference suite shapes
+    (2, 256, 256, 4, 8, 128, 2, 32),   # config-2 geometry, small
+    (1, 300, 512, 8, 4, 64, 2, 32),    # ragged S
+]
+
+
+@pytest.mark.parametrize("case", LAYER_CASES, ids=[f"B{c[0]}S{c[1]}D{c[2]}H{c[3]}E{c[4]}bs{c[5]}" for c in LAYER_CASES])
+def test_layer_fwd_bwd_matches_oracle(case, dev):
+    B, S, D, H, NB, BS, K, R = case
+    layer, ref, M = build_pair(D, H, NB, BS, K, R)
+    layer.eval()
+    ref.eval()
+    ref.noise_scale = 0.0
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, S, D, generator=g).bfloat16()
+    dy = torch.randn(B, S, D, generator=g).bfloat16()
+
+    ld = layer.to(dev)
+    for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+        lin.to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    Md = M.to(dev).requires_grad_(True)
+    y = ld(xd, Md)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+
+    xr = x.float().requires_grad_(True)
+    Mr = M.float().requires_grad_(True)
+    yr = ref(xr, Mr)
+    yr.backward(dy.float())
+
+    # mom_scale * out promotes like the reference (model.py:239)
+    assert y.dtype == torch.promote_types(ld.mom_scale.dtype, torch.bfloat16)
+    assert_close(y, yr, "y")
+    assert_close(xd.grad, xr.grad, "dx")
+    assert_close(Md.grad, Mr.grad, "dM_blocks")
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "router_down", "router_up"):
+        got = getattr(ld, name).weight.grad
+        exp = getattr(ref, name).weight.grad
+        assert_close(got, exp, f"d{name}", atol=2e-3 * max(1.0, float(exp.abs().max())))
+    assert_close(ld.mom_scale.grad, ref.mom_scale.grad, "dmom_scale", atol=2e-3 * max(1.0, float(ref.mom_scale.grad.abs().max())))
+
+
+def test_layer_causality_bitwise(dev):
+    B, S, D, H, NB, BS, K, R = 2, 256, 256, 4, 8, 128, 2, 32
+    layer, _, M = build_pair(D, H, NB, BS, K, R, seed=21)
+    ld = layer.to(dev)
+    for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+        lin.to(torch.bfloat16)
+    ld.eval()
+    x = torch.randn(B, S, D).bfloat16().to(dev)
+    cut = S // 2
+    with torch.no_grad():
+        a = ld(x, M.to(dev))
+        x2 = x.clone()
+        x2[:, cut + 1:] += 1.0
+        b = ld(x2, M.to(dev))
+    assert torch.equal(a[:, :cut + 1], b[:, :cut + 1])
+
+
+def test_layer_grad_ckpt_exact_and_alive(dev):
+    B, S, D, H, NB, BS, K, R = 2, 256, 256, 4, 8, 128, 2, 32
+    outs = []
+    for ck in (False, True):
+        layer, _, M = build_pair(D, H, NB, BS, K, R, seed=5)
+        layer.mom_grad_ckpt = ck
+        ld = layer.to(dev)
+        for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+            lin.to(torch.bfloat16)
+        ld.train()
+        ld.noise_scale = 0.0
+        x = torch.randn(B, S, D, generator=torch.Generator().manual_seed(2)).bfloat16().to(dev)
+        Md = M.to(dev).requires_grad_(True)
+        y = ld(x, Md)
+        y.float().pow(2).mean().backward()
+        outs.append((y.detach(), Md.grad.clone(), {n: p.grad.clone() for n, p in ld.named_parameters()}))
+    (y0, m0, g0), (y1, m1, g1) = outs
+    assert torch.equal(y0, y1)
+    assert torch.equal(m0, m1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+        assert torch.isfinite(g0[n]).all(), n
+    assert float(g0["router_up.weight"].abs().sum()) > 0
+    assert float(m0.float().abs().sum()) > 0

@@ -1,0 +1,145 @@
+"""GPU parity of the fused prefix-mean router (C ABI naylis_mom_router_*)
+against the CPU oracle (model.py:169-220 restated in oracle.router).
+
+* The fp32 prefix mean is bit-exact (torch.equal) with the CPU reference's
+  cumsum / (t+1) — reference test_parity.py §2a/2b, probe.py A1.
+* top_idx equals the oracle's on every token whose fp64 k-th / (k+1)-th
+  logit margin exceeds tau = 1e-5 * max|logit| (a near-tie is decided by fp32
+  GEMM rounding order, which no two implementations share); such tokens are
+  counted and must be rare.
+* logits / probs / gates to fp32 rounding; gradients dx, dW_down, dW_up
+  against fp32 autograd of the oracle.
+"""
+import pytest
+import torch
+
+import oracle
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def make(B, T, D, R, E, dtype, seed=0, bias_blocks=None):
+    g = torch.Generator().manual_seed(seed)
+    w_down = torch.randn(R, D, generator=g) * 0.02
+    w_up = torch.randn(E, R, generator=g) * 0.02
+    x = torch.randn(B, T, D, generator=g)
+    if dtype == torch.bfloat16:
+        x = x.bfloat16()
+    noise = None
+    if bias_blocks is not None:
+        # config-4 style additive logit bias: per (b, 128-token tile) a few
+        # favoured blocks, through the additive noise hook of the router
+        noise = torch.zeros(B, T, E)
+        for b in range(B):
+            for t0 in range(0, T, 128):
+                n = int(torch.randint(bias_blocks[0], bias_blocks[1] + 1, (1,), generator=g))
+                blk = torch.randperm(E, generator=g)[:n]
+                noise[b, t0:t0 + 128, blk] = 1.0
+    return x, w_down, w_up, noise
+
+
+def fp64_margin(x, w_down, w_up, k, noise, scale):
+    logits64, _, _, _, _ = oracle.router(x.double(), w_down.double(), w_up.double(), k,
+                                         noise=None if noise is None else noise.double(), noise_scale=scale)
+    noisy = logits64 if noise is None else logits64 + scale * noise.double()
+    srt = noisy.sort(-1, descending=True).values
+    return (srt[..., k - 1] - srt[..., k]), noisy.abs().max()
+
+
+CASES = [
+    (2, 64, 32, 8, 4, 2, torch.float32),      # reference suite shapes (router rank 8)
+    (2, 512, 1024, 32, 8, 2, torch.float32),  # config 1
+    (2, 300, 1024, 32, 8, 2, torch.bfloat16), # ragged T
+    (8, 2048, 1024, 32, 8, 2, torch.bfloat16),# config 2
+    (1, 256, 96, 16, 8, 3, torch.bfloat16),   # top-3, D not a multiple of 256
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}T{c[1]}D{c[2]}R{c[3]}E{c[4]}k{c[5]}{str(c[6])[6:]}" for c in CASES])
+def test_router_forward(case, dev):
+    from naylis_amd import mom_kernels
+    B, T, D, R, E, k, dtype = case
+    x, w_down, w_up, _ = make(B, T, D, R, E, dtype)
+    logits, probs, idx, gates, h = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), k, return_h=True)
+    torch.cuda.synchronize()
+    r_logits, r_probs, r_idx, r_gates, r_h = oracle.router(x, w_down, w_up, k)
+    # bit-exact prefix mean
+    assert torch.equal(h.cpu(), r_h), f"prefix mean differs: max {float((h.cpu() - r_h).abs().max())}"
+    assert torch.equal(h[:, 0].cpu(), x[:, 0].float())
+    # indices: exact outside near-ties
+    margin, scale = fp64_margin(x, w_down, w_up, k, None, 1.0)
+    tau = 1e-5 * float(scale)
+    clear = margin > tau
+    mism = (idx.cpu().long() != r_idx).any(-1)
+    assert not (mism & clear).any(), f"{int((mism & clear).sum())} clear-margin tokens route differently"
+    # near-ties (fp64 margin below tau) may go either way; they stay rare
+    assert int(mism.sum()) <= max(2, B * T // 1000), f"{int(mism.sum())} near-tie tokens route differently"
+    print(f"near-tie tokens: {int((~clear).sum())}, of which routed differently: {int(mism.sum())}")
+    same = ~mism
+    assert_close(logits.cpu(), r_logits, "logits", rtol=1e-4, atol=1e-6)
+    assert_close(probs.cpu(), r_probs, "probs", rtol=1e-4, atol=1e-6)
+    assert_close(gates.cpu()[same], r_gates[same], "gates", rtol=1e-4, atol=1e-6)
+
+
+def test_router_noise_hook_and_config4_bias(dev):
+    """Additive noise (Gumbel / logit bias) re-ranks top-k only; probs stay
+    the clean softmax (model.py:209-220)."""
+    from naylis_amd import mom_kernels
+    B, T, D, R, E, k = 2, 512, 256, 32, 32, 2
+    x, w_down, w_up, noise = make(B, T, D, R, E, torch.bfloat16, seed=3, bias_blocks=(3, 6))
+    noise = noise * 10.0
+    logits, probs, idx, gates = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), k,
+                                                      noise=noise.to(dev), noise_scale=0.5)
+    r_logits, r_probs, r_idx, r_gates, _ = oracle.router(x, w_down, w_up, k, noise=noise, noise_scale=0.5)
+    margin, scale = fp64_margin(x, w_down, w_up, k, noise, 0.5)
+    clear = margin > 1e-5 * float(scale)
+    mism = (idx.cpu().long() != r_idx).any(-1)
+    assert not (mism & clear).any()
+    assert_close(probs.cpu(), r_probs, "probs", rtol=1e-4, atol=1e-6)
+    assert_close(gates.cpu()[~mism], r_gates[~mism], "gates", rtol=1e-4, atol=1e-6)
+    # every selected block is among the biased ones for this tile
+    assert bool((noise.gather(-1, idx.cpu().long()) > 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 64, 32, 8, 4, 2), (2, 384, 1024, 32, 8, 2), (1, 200, 96, 16, 8, 3)])
+def test_router_backward(shape, dtype, dev):
+    from naylis_amd import mom_kernels
+    B, T, D, R, E, k = shape
+    x, w_down, w_up, _ = make(B, T, D, R, E, dtype, seed=5)
+    g = torch.Generator().manual_seed(9)
+    dg = torch.randn(B, T, k, generator=g)
+    dp = torch.randn(B, T, E, generator=g) * 0.1
+    dlg = torch.randn(B, T, E, generator=g) * 0.1
+
+    xd = x.to(dev).requires_grad_(True)
+    wdd = w_down.to(dev).requires_grad_(True)
+    wud = w_up.to(dev).requires_grad_(True)
+    logits, probs, idx, gates = mom_kernels.mom_route(xd, wdd, wud, k)
+    (gates * dg.to(dev)).sum().add((probs * dp.to(dev)).sum()).add((logits * dlg.to(dev)).sum()).backward()
+
+    xr = x.float().requires_grad_(True)
+    wdr = w_down.clone().requires_grad_(True)
+    wur = w_up.clone().requires_grad_(True)
+    r_logits, r_probs, r_idx, r_gates, _ = oracle.router(xr, wdr, wur, k)
+    assert torch.equal(idx.cpu().long(), r_idx), "routing differs; pick another seed for this check"
+    (r_gates * dg).sum().add((r_probs * dp).sum()).add((r_logits * dlg).sum()).backward()
+
+    assert_close(xd.grad, xr.grad.to(x.dtype) if dtype == torch.bfloat16 else xr.grad, "dx")
+    smax = float(wdr.grad.abs().max())
+    assert_close(wdd.grad, wdr.grad, "dW_down", rtol=1e-3, atol=1e-4 * smax)
+    umax = float(wur.grad.abs().max())
+    assert_close(wud.grad, wur.grad, "dW_up", rtol=1e-3, atol=1e-4 * umax)
+
+
+def test_router_causal(dev):
+    """Routing of tokens <= t ignores tokens > t (test_parity.py §3a)."""
+    from naylis_amd import mom_kernels
+    x, w_down, w_up, _ = make(2, 512, 256, 32, 8, torch.bfloat16, seed=11)
+    a = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), 2, return_h=True)
+    x2 = x.clone()
+    x2[:, 301:] += 1.0
+    b = mom_kernels.mom_route(x2.to(dev), w_down.to(dev), w_up.to(dev), 2, return_h=True)
+    for ta, tb in zip(a, b):
+        assert torch.equal(ta[:, :301], tb[:, :301])
