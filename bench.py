@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""MoM layer forward+backward throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config4]
+
+Workload ("config2"): one Naylis MoM layer in bf16,
+forward + backward at the training shape B=8, T=2048, d=1024, 16 heads x 64,
+bank 8 blocks x 128 slots x 1024 rescaled to Frobenius norm 63, router
+d -> 32 -> 8 with top-2, ReZero scale 1.0, Gumbel noise off.  x is RMS-normed
+N(0,1) in bf16, dy ~ N(0,1); router weights, prefix mean and routing in fp32.
+Random-init weights, synthetic data.  A step is y = layer(x, M); y.backward(dy)
+with all parameter gradients.
+
+Prints ONE JSON line: tokens/s (value), per-step time, the roofline of the
+dominant kernel (average duration from HIP events recorded by the library on
+its launch stream over the timed region), the read's own MFMA fraction on the
+tile-active basis, and a CPU baseline (the eager fp32 oracle on the host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "MoM layer fwd+bwd tokens/s at d=1024, 8x128 slots; % bf16 MFMA peak"
+
+WORKLOADS = {
+    # B, T, d, heads, blocks, block_size, top_k, rank
+    "config2": dict(B=8, T=2048, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, tile_bias=None),
+    "config4": dict(B=4, T=4096, D=1536, H=24, E=32, BS=128, K=2, R=32, bank_fro=None, tile_bias=(3, 6)),
+}
+
+
+def build(cfg, device):
+    import torch
+
+    from naylis_amd.layer import MoMLayer
+    B, T, D, H, E, BS, K, R = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS", "K", "R"))
+    gw = torch.Generator().manual_seed(0)
+    layer = MoMLayer(d_model=D, n_heads=H, mem_size=E * BS, block_size=BS, top_blocks=K, router_rank=R)
+    with torch.no_grad():
+        for lin in (layer.router_down, layer.router_up, layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=gw) * 0.02)
+        layer.mom_scale.fill_(1.0)
+    layer = layer.to(device)
+    for lin in (layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+        lin.to(torch.bfloat16)
+    layer.train()
+    layer.noise_scale = 0.0
+    gb = torch.Generator().manual_seed(3)
+    M = torch.randn(E, BS * D, generator=gb) * 0.02
+    if cfg["bank_fro"]:
+        M = M * (cfg["bank_fro"] / float(M.norm()))
+    M = M.bfloat16().to(device).requires_grad_(True)
+    gx = torch.Generator().manual_seed(1)
+    x = torch.randn(B, T, D, generator=gx)
+    x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+    x = x.bfloat16().to(device).requires_grad_(True)
+    gd = torch.Generator().manual_seed(2)
+    dy = torch.randn(B, T, D, generator=gd).bfloat16().to(device)
+    if cfg["tile_bias"]:
+        lo, hi = cfg["tile_bias"]
+        bias = torch.zeros(B, T, E)
+        for b in range(B):
+            for t0 in range(0, T, 128):
+                n = int(torch.randint(lo, hi + 1, (1,), generator=gb))
+                bias[b, t0:t0 + 128, torch.randperm(E, generator=gb)[:n]] = 1.0
+        # the additive logit hook of the router: +10 x logit std on the favoured blocks
+        layer._bench_bias = (bias * 10.0 * 0.02).to(device)
+    return layer, M, x, dy
+
+
+def layer_step(layer, M, x, dy):
+    bias = getattr(layer, "_bench_bias", None)
+    if bias is None:
+        y = layer(x, M)
+    else:
+        y = _forward_with_bias(layer, x, M, bias)
+    y.backward(dy)
+    for p in layer.parameters():
+        p.grad = None
+    M.grad = None
+    x.grad = None
+
+
+def _forward_with_bias(layer, x, M, bias):
+    """Layer forward with an additive router-logit bias (config 4's sparsity)."""
+    from naylis_amd import mom_kernels
+    if layer._kernel_mode is None:
+        layer._kernel_mode = layer._resolve_kernel(x)
+    _, probs, idx, gates = mom_kernels.mom_route(x, layer.router_down.weight, layer.router_up.weight,
+                                                 layer.top_blocks, noise=bias, noise_scale=1.0)
+    return layer.mom_scale * layer._read(x, idx, gates, M)
+
+
+def routing(layer, M, x):
+    import torch
+
+    from naylis_amd import mom_kernels
+    with torch.no_grad():
+        bias = getattr(layer, "_bench_bias", None)
+        _, _, idx, _ = mom_kernels.mom_route(x, layer.router_down.weight, layer.router_up.weight,
+                                             layer.top_blocks, noise=bias, noise_scale=1.0)
+    return idx
+
+
+def active_tiles(idx, E, tile=128):
+    import torch
+    B, T, K = idx.shape
+    n_tiles = (T + tile - 1) // tile
+    oh = torch.zeros(B, n_tiles * tile, E, dtype=torch.bool, device=idx.device)
+    oh[:, :T].scatter_(2, idx.long(), True)
+    return int(oh.view(B, n_tiles, tile, E).any(2).sum())
+
+
+def cpu_baseline(cfg, sample_b):
+    """Eager fp32 oracle layer fwd+bwd on the host cores, on `sample_b` of the
+    B sequences at the full T (1 warmup + median of 3)."""
+    import torch
+
+    import oracle
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    B, T, D, H, E, BS, K, R = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS", "K", "R"))
+    b = min(sample_b, B)
+    torch.manual_seed(0)
+    layer = oracle.OracleMoMLayer(D, H, E * BS, BS, K, R)
+    with torch.no_grad():
+        for lin in (layer.router_down, layer.router_up, layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+            lin.weight.normal_(0, 0.02)
+        layer.mom_scale.fill_(1.0)
+    layer.noise_scale = 0.0
+    M = (torch.randn(E, BS * D) * 0.02).requires_grad_(True)
+    x = torch.randn(b, T, D)
+    x = (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)).requires_grad_(True)
+    dy = torch.randn(b, T, D)
+    times = []
+    for i in range(4):
+        t0 = time.perf_counter()
+        y = layer(x, M)
+        y.backward(dy)
+        times.append(time.perf_counter() - t0)
+        layer.zero_grad(set_to_none=True)
+        M.grad = None
+        x.grad = None
+    med = statistics.median(times[1:])
+    return {"value": round(b * T / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle.OracleMoMLayer fp32 fwd+bwd, {b} of {B} sequences x T={T} "
+                      f"(1 warmup, median of 3 runs: {med:.3f} s), torch {torch.__version__}"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-batch", type=int, default=2)
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+              "(the sharding design is in DESIGN.md).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from naylis_amd import _lib
+    dev = torch.device("cuda:0")
+    cfg = WORKLOADS[args.workload]
+    layer, M, x, dy = build(cfg, dev)
+    B, T, D, H, E, BS = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS"))
+    ntok = B * T
+
+    for _ in range(args.warmup):
+        layer_step(layer, M, x, dy)
+    torch.cuda.synchronize()
+    with _lib.KernelTimer():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            layer_step(layer, M, x, dy)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    kernels = _lib.KernelTimer.results()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+
+    # algorithmic work on the tile-active basis (128-token tiles, the
+    # reference's BLOCK_M): per (b, tile, active block) d*bs*128 MACs per GEMM
+    idx = routing(layer, M, x)
+    A = active_tiles(idx, E)
+    unit = 2.0 * D * BS * 128 * A          # FLOP of one GEMM-shaped product
+    alg = {"read_fwd": 2 * unit, "read_bwd_dq": 3 * unit, "read_bwd_dkdv": 4 * unit}
+    per = {k: (v[0] / v[1], v[1] / args.steps) for k, v in kernels.items() if v[1]}  # avg ms, launches/step
+    dominant = max(kernels, key=lambda k: kernels[k][0])
+    dom_ms = per[dominant][0]
+    if dominant in alg:
+        ach = alg[dominant] / (dom_ms * 1e-3) / 1e12
+        roof = {"kernel": dominant, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "avg_us": round(dom_ms * 1e3, 2), "alg_flop_per_launch": alg[dominant]}
+    else:
+        roof = {"kernel": dominant, "bound": "hbm", "achieved": None, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": None, "traffic": None, "avg_us": round(dom_ms * 1e3, 2)}
+    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            roof["traffic"] = json.load(f).get(f"{args.workload}:{dominant}")
+
+    read_names = ("bank_relayout", "read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce_kv",
+                  "read_bwd_reduce_gates")
+    read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
+    read_flop = 14.0 * D * BS * 128 * A
+    read_tf = read_flop / (read_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(ntok / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, RMS-normed N(0,1) x, N(0,1) dy)",
+        "config": {"workload": f"{args.workload}: MoM layer fwd+bwd B={B} T={T} d={D} heads={H}x{D // H} "
+                               f"bank {E}x{BS} top-{cfg['K']} rank {cfg['R']}",
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "read": {"active_tile_blocks": A, "active_per_tile": round(A / (B * ((T + 127) // 128)), 3),
+                 "alg_flop": read_flop, "ms": round(read_ms, 4), "tflops": round(read_tf, 2),
+                 "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
+        "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_sample_batch)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -139,6 +139,18 @@ int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, 
                            void* d_slots, int slots_grad_dtype, void* dw_k, void* dw_v, int w_grad_dtype, int64_t L,
                            int64_t D_in, int64_t D_out, void* stream);
 
+/* -------------------------------------------------------------- timing ---
+ * Optional instrumentation (no counterpart in the reference; for benchmarks):
+ * when enabled, each kernel launch of this library is bracketed by hipEvents
+ * on its stream.  naylis_mom_timing_get() waits for the recorded events and
+ * returns the summed duration (ms) and launch count of one kernel name
+ * (names: naylis_mom_timing_names(), comma-separated).  Off by default;
+ * enabling it adds two event records per launch. */
+void naylis_mom_timing_enable(int on);
+void naylis_mom_timing_reset(void);
+int naylis_mom_timing_get(const char* name, double* total_ms, int64_t* count);
+int naylis_mom_timing_names(char* buf, size_t buf_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,11 @@ SIGNATURES = {
     "naylis_mom_bank_kv_fwd": (_int, [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
+    "naylis_mom_timing_enable": (None, [_int]),
+    "naylis_mom_timing_reset": (None, []),
+    "naylis_mom_timing_get": (_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                     ctypes.POINTER(ctypes.c_int64)]),
+    "naylis_mom_timing_names": (_int, [ctypes.c_char_p, _size_t]),
 }
 
 _lock = threading.Lock()
@@ -86,6 +91,34 @@ def check(rc):
         msg = load().naylis_mom_last_error()
         msg = msg.decode() if msg else "unknown error"
         raise NaylisError(rc, msg)
+
+
+class KernelTimer:
+    """Per-kernel HIP-event totals collected by the library while enabled."""
+
+    def __enter__(self):
+        lib = load()
+        lib.naylis_mom_timing_reset()
+        lib.naylis_mom_timing_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        load().naylis_mom_timing_enable(0)
+        return False
+
+    @staticmethod
+    def results():
+        """{kernel name: (total_ms, launches)} (waits for the recorded events)."""
+        lib = load()
+        buf = ctypes.create_string_buffer(8192)
+        check(lib.naylis_mom_timing_names(buf, len(buf)))
+        out = {}
+        for name in filter(None, buf.value.decode().split(",")):
+            ms = ctypes.c_double()
+            n = ctypes.c_int64()
+            check(lib.naylis_mom_timing_get(name.encode(), ctypes.byref(ms), ctypes.byref(n)))
+            out[name] = (ms.value, n.value)
+        return out
 
 
 def available():

@@ -12,6 +12,7 @@
 // along K at K1 into two tensors (A1|A2, B1;B2), which is how the two terms of
 // d_slots become one product.
 #include "common.h"
+#include "timing.h"
 #include "launch_bank.h"
 
 namespace naylis {
@@ -127,7 +128,7 @@ hipError_t launch_bank_kv_fwd(const void* slots, const void* w_k, const void* w_
     P.ldc = D_out;
   }
   const dim3 grid((D_out + GBN - 1) / GBN, (L + GBM - 1) / GBM, 2);
-  hipLaunchKernelGGL((bank_gemm_kernel<true, true, false>), grid, dim3(256), 0, st, bt, L, D_out, D_in, D_in);
+  NAYLIS_TIMED("bank_kv_fwd", st, hipLaunchKernelGGL((bank_gemm_kernel<true, true, false>), grid, dim3(256), 0, st, bt, L, D_out, D_in, D_in));
   return hipGetLastError();
 }
 
@@ -142,9 +143,9 @@ hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_
   b1.prob[0].ldc = D_in;
   const dim3 g1((D_in + GBN - 1) / GBN, (L + GBM - 1) / GBM, 1);
   if (slots_f32)
-    hipLaunchKernelGGL((bank_gemm_kernel<true, false, true>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out);
+    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, true>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
   else
-    hipLaunchKernelGGL((bank_gemm_kernel<true, false, false>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out);
+    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, false>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
   // dW (D_out x D_in) = dK^T (D_out x L) . slots (L x D_in)
   GemmBatch b2{};
   for (int z = 0; z < 2; ++z) {
@@ -157,9 +158,9 @@ hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_
   }
   const dim3 g2((D_in + GBN - 1) / GBN, (D_out + GBM - 1) / GBM, 2);
   if (w_f32)
-    hipLaunchKernelGGL((bank_gemm_kernel<false, false, true>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L);
+    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, true>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L));
   else
-    hipLaunchKernelGGL((bank_gemm_kernel<false, false, false>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L);
+    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, false>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L));
   return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@
 //     d(top_gates) through log(max(g, 1e-9)).
 #include "launch.h"
 #include "read_common.h"
+#include "timing.h"
 
 namespace naylis {
 
@@ -577,10 +578,10 @@ static void dq_inst(const void* q, const void* k, const void* v, const void* kt,
                     const ReadDims& d, hipStream_t st) {
   const int n_tiles = (d.S + 127) / 128;
   const float scale = read_scale(HD);
-  hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+  NAYLIS_TIMED("read_bwd_dq", st, hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
                      (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)kt, ti, tg,
                      (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.B, d.S, d.H, d.L,
-                     read_lp(d.L), d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles);
+                     read_lp(d.L), d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
 }
 
 template <int HD, int TK>
@@ -638,9 +639,9 @@ static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t
   const int tpc = (n_ttiles + nc - 1) / nc;
   const int Lq = read_lq(d.L);
   const float alpha = read_scale(HD) * kLog2e;
-  hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(256), 0, st,
+  NAYLIS_TIMED("read_bwd_dkdv", st, hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(256), 0, st,
                      (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)dout, lse, delta,
-                     dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc, tpc);
+                     dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc, tpc));
 }
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
@@ -680,14 +681,14 @@ hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, co
   const long stride = (long)read_lq(d.L) * D;
   long blocks = (n / 4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
-                     (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD));
+  NAYLIS_TIMED("read_bwd_reduce_kv", st, hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
+                     (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD)));
   const long ng = (long)d.B * d.S * d.topk;
   if (ng > 0) {
     long gb = (ng + 255) / 256;
     if (gb > 8192) gb = 8192;
-    hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates, dgates,
-                       ng, d.H);
+    NAYLIS_TIMED("read_bwd_reduce_gates", st, hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates, dgates,
+                       ng, d.H));
   }
   return hipGetLastError();
 }

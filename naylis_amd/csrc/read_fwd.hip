@@ -15,6 +15,7 @@
 // with P^T taken straight from the accumulator registers.
 #include "launch.h"
 #include "read_common.h"
+#include "timing.h"
 
 namespace naylis {
 
@@ -279,8 +280,8 @@ hipError_t launch_bank_relayout(const void* src, void* dst, const ReadDims& d, h
   const int HDP = read_hdp(d.HD), Lp = read_lp(d.L);
   const long n = (long)d.H * HDP * Lp;
   const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-  hipLaunchKernelGGL(bank_relayout_kernel, dim3(blocks), dim3(256), 0, st, (const bf16_t*)src, (bf16_t*)dst, d.L, Lp,
-                     d.H, d.HD, HDP);
+  NAYLIS_TIMED("bank_relayout", st, hipLaunchKernelGGL(bank_relayout_kernel, dim3(blocks), dim3(256), 0, st, (const bf16_t*)src, (bf16_t*)dst, d.L, Lp,
+                     d.H, d.HD, HDP));
   return hipGetLastError();
 }
 
@@ -289,9 +290,9 @@ static void fwd_inst(const void* q, const void* k, const void* vt, const int32_t
                      float* lse, const ReadDims& d, hipStream_t st) {
   const int n_tiles = (d.S + 127) / 128;
   const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
-  hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st, (const bf16_t*)q,
+  NAYLIS_TIMED("read_fwd", st, hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st, (const bf16_t*)q,
                      (const bf16_t*)k, (const bf16_t*)vt, ti, tg, (bf16_t*)out, lse, d.B, d.S, d.H, d.L,
-                     read_lp(d.L), d.E, d.block_size, d.topk, alpha, n_tiles);
+                     read_lp(d.L), d.E, d.block_size, d.topk, alpha, n_tiles));
 }
 
 template <int HD, int TK>

@@ -23,6 +23,7 @@
 // reverse scan and the recomputation of h fold into W~).
 #include "launch_router.h"
 #include "common.h"
+#include "timing.h"
 
 namespace naylis {
 
@@ -403,12 +404,12 @@ static void fwd_launch(const void* x, const float* w_down, const float* w_up, co
   const int n_chunks = (d.T + kRouterChunk - 1) / kRouterChunk;
   double* carry = (double*)(ws + w.carry);
   const int dblk = (d.D + 255) / 256;
-  hipLaunchKernelGGL((router_chunk_sums_kernel<XT>), dim3(dblk, n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
-                     d.T, d.D, n_chunks);
-  hipLaunchKernelGGL(router_chunk_carry_kernel, dim3(dblk, d.B), dim3(256), 0, st, carry, d.D, n_chunks);
-  hipLaunchKernelGGL((router_fwd_kernel<XT, EMAX, TK>), dim3(n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
+  NAYLIS_TIMED("router_chunk_sums", st, hipLaunchKernelGGL((router_chunk_sums_kernel<XT>), dim3(dblk, n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
+                     d.T, d.D, n_chunks));
+  NAYLIS_TIMED("router_chunk_carry", st, hipLaunchKernelGGL(router_chunk_carry_kernel, dim3(dblk, d.B), dim3(256), 0, st, carry, d.D, n_chunks));
+  NAYLIS_TIMED("router_fwd", st, hipLaunchKernelGGL((router_fwd_kernel<XT, EMAX, TK>), dim3(n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
                      w_down, w_up, noise, ns, logits, probs, idx, gates, act, h_out, d.T, d.D, d.R, d.E, d.topk,
-                     n_chunks);
+                     n_chunks));
 }
 
 template <typename XT>
@@ -443,8 +444,8 @@ static void bwd_token(const float* act, const float* probs, const int32_t* idx, 
                       const float* dp, const float* dl, const float* w_up, float* w_out, float* dwup_part,
                       const RouterDims& d, hipStream_t st) {
   const long ntok = (long)d.B * d.T;
-  hipLaunchKernelGGL((router_bwd_token_kernel<EMAX, TK>), dim3((int)((ntok + 63) / 64)), dim3(64), 0, st, act, probs,
-                     idx, gates, dg, dp, dl, w_up, w_out, dwup_part, d.T, d.R, d.E, d.topk, ntok);
+  NAYLIS_TIMED("router_bwd_token", st, hipLaunchKernelGGL((router_bwd_token_kernel<EMAX, TK>), dim3((int)((ntok + 63) / 64)), dim3(64), 0, st, act, probs,
+                     idx, gates, dg, dp, dl, w_up, w_out, dwup_part, d.T, d.R, d.E, d.topk, ntok));
 }
 
 template <typename XT>
@@ -453,11 +454,11 @@ static void bwd_dx(const void* x, const float* wt, const float* w_down, void* dx
   const long ntok = (long)d.B * d.T;
   const dim3 grid((int)((ntok + kDxChunk - 1) / kDxChunk), (d.D + 255) / 256);
   if (d.R <= 32)
-    hipLaunchKernelGGL((router_bwd_dx_kernel<XT, 32>), grid, dim3(256), 0, st, (const XT*)x, wt, w_down, (XT*)dx,
-                       dwd_part, d.D, d.R, ntok);
+    NAYLIS_TIMED("router_bwd_dx", st, hipLaunchKernelGGL((router_bwd_dx_kernel<XT, 32>), grid, dim3(256), 0, st, (const XT*)x, wt, w_down, (XT*)dx,
+                       dwd_part, d.D, d.R, ntok));
   else
-    hipLaunchKernelGGL((router_bwd_dx_kernel<XT, 64>), grid, dim3(256), 0, st, (const XT*)x, wt, w_down, (XT*)dx,
-                       dwd_part, d.D, d.R, ntok);
+    NAYLIS_TIMED("router_bwd_dx", st, hipLaunchKernelGGL((router_bwd_dx_kernel<XT, 64>), grid, dim3(256), 0, st, (const XT*)x, wt, w_down, (XT*)dx,
+                       dwd_part, d.D, d.R, ntok));
 }
 
 hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, const float* w_up, const float* act,
@@ -475,10 +476,10 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
   const long nwd = (long)d.R * d.D;
   const long nwu = (long)d.E * d.R;
   if (ntok == 0) {  // no tokens: the weight gradients are zero
-    hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)),
-                       dim3(256), 0, st, dwd_part, dw_down, nwd, 0);
-    hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
-                       0);
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)),
+                       dim3(256), 0, st, dwd_part, dw_down, nwd, 0));
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
+                       0));
     return hipGetLastError();
   }
   if (d.E <= 8 && d.topk <= 2)
@@ -489,16 +490,16 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
     bwd_token<32, 8>(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf, dwup_part, d, st);
   else
     bwd_token<64, 8>(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf, dwup_part, d, st);
-  hipLaunchKernelGGL(router_bwd_scan_kernel, dim3(d.B, (d.R + 31) / 32), dim3(256), 0, st, wbuf, wt, d.T, d.R);
+  NAYLIS_TIMED("router_bwd_scan", st, hipLaunchKernelGGL(router_bwd_scan_kernel, dim3(d.B, (d.R + 31) / 32), dim3(256), 0, st, wbuf, wt, d.T, d.R));
   if (x_bf16)
     bwd_dx<bf16_t>(x, wt, w_down, dx, dwd_part, d, st);
   else
     bwd_dx<float>(x, wt, w_down, dx, dwd_part, d, st);
   const int n_dx_chunks = (int)((ntok + kDxChunk - 1) / kDxChunk);
-  hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)), dim3(256),
-                     0, st, dwd_part, dw_down, nwd, n_dx_chunks);
-  hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
-                     n_tok_blocks);
+  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)), dim3(256),
+                     0, st, dwd_part, dw_down, nwd, n_dx_chunks));
+  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
+                     n_tok_blocks));
   return hipGetLastError();
 }
 
