@@ -61,7 +61,8 @@ const char* naylis_mom_last_error(void);
  *   lse      (B, H, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
  * Constraints: head_dim a power of two in [16, 128]; 1 <= k <= min(8, E);
- * E <= 1024; L <= 16384.
+ * E <= 1024; L <= 16384.  The forward needs no workspace (pass NULL, 0); the
+ * backward needs naylis_mom_read_workspace_bytes() bytes.
  */
 size_t naylis_mom_read_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks,
                                        int64_t block_size, int64_t top_k);

@@ -73,23 +73,29 @@ int check_read_dims(int64_t B, int64_t S, int64_t H, int64_t hd, int64_t num_blo
 }
 
 struct ReadWs {
-  size_t relayout, delta, dlg, part;  // byte offsets
+  size_t delta, dlg, tile_flags, list, count, part;  // byte offsets
   size_t total;
   int n_chunks;
 };
 
+// The forward needs no workspace; the backward's layout is below.
 ReadWs plan_read_ws(const ReadDims& d) {
   ReadWs w{};
-  const size_t relay = (size_t)d.H * read_hdp(d.HD) * read_lp(d.L) * 2;
   const size_t ntok = (size_t)d.B * d.S;
+  const size_t n_tt = (size_t)read_bwd_n_ttiles(d);
+  const size_t n_sg = (size_t)read_lq(d.L) / 128;
   w.n_chunks = read_bwd_chunks(d);
   size_t off = 0;
-  w.relayout = off;
-  off += align256(relay);
   w.delta = off;
   off += align256(ntok * d.H * 4);
   w.dlg = off;
   off += align256(ntok * d.H * d.topk * 4);
+  w.tile_flags = off;
+  off += align256(n_tt * d.E);
+  w.list = off;
+  off += align256(n_sg * n_tt * 4);
+  w.count = off;
+  off += align256(n_sg * 4);
   w.part = off;
   off += 2 * align256((size_t)w.n_chunks * read_lq(d.L) * d.H * d.HD * 4);
   w.total = off;
@@ -145,20 +151,15 @@ int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32
                         void* out, float* lse, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
                         int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
                         void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   ReadDims d;
   int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
   if (rc) return rc;
   if (B * S == 0) return NAYLIS_OK;
-  if (!q || !k || !v || !top_idx || !top_gates || !out || !lse || !workspace)
+  if (!q || !k || !v || !top_idx || !top_gates || !out || !lse)
     return fail(NAYLIS_ERR_ARG, "mom_read_fwd: null pointer argument");
-  const ReadWs w = plan_read_ws(d);
-  if (workspace_bytes < w.relayout + align256((size_t)d.H * read_hdp(d.HD) * read_lp(d.L) * 2))
-    return fail(NAYLIS_ERR_WORKSPACE, "mom_read_fwd: workspace of %zu bytes is too small", workspace_bytes);
-  hipStream_t st = (hipStream_t)stream;
-  char* ws = (char*)workspace;
-  rc = hip_status(launch_bank_relayout(v, ws + w.relayout, d, st), "mom_read_fwd relayout");
-  if (rc) return rc;
-  return hip_status(launch_read_fwd(q, k, ws + w.relayout, top_idx, top_gates, out, lse, d, st), "mom_read_fwd");
+  return hip_status(launch_read_fwd(q, k, v, top_idx, top_gates, out, lse, d, (hipStream_t)stream), "mom_read_fwd");
 }
 
 int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32_t* top_idx, const float* top_gates,
@@ -179,18 +180,21 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   char* ws = (char*)workspace;
   float* delta = (float*)(ws + w.delta);
   float* dlg = (float*)(ws + w.dlg);
+  uint8_t* tflags = (uint8_t*)(ws + w.tile_flags);
+  int32_t* list = (int32_t*)(ws + w.list);
+  int32_t* count = (int32_t*)(ws + w.count);
   const size_t part_bytes = align256((size_t)w.n_chunks * read_lq(d.L) * d.H * d.HD * 4);
   float* dkp = (float*)(ws + w.part);
   float* dvp = (float*)(ws + w.part + part_bytes);
   if (B * S > 0) {
-    rc = hip_status(launch_bank_relayout(k, ws + w.relayout, d, st), "mom_read_bwd relayout");
-    if (rc) return rc;
-    rc = hip_status(launch_read_bwd_dq(q, k, v, ws + w.relayout, top_idx, top_gates, out, dout, lse, dq, delta, dlg,
-                                       d, st),
+    rc = hip_status(launch_read_bwd_dq(q, k, v, top_idx, top_gates, out, dout, lse, dq, delta, dlg, d, st),
                     "mom_read_bwd dq");
     if (rc) return rc;
   }
-  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, dkp, dvp, w.n_chunks, d, st),
+  rc = hip_status(launch_read_tile_lists(top_idx, tflags, list, count, d, st), "mom_read_bwd tile lists");
+  if (rc) return rc;
+  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dkp, dvp,
+                                       w.n_chunks, d, st),
                   "mom_read_bwd dkdv");
   if (rc) return rc;
   return hip_status(launch_read_bwd_reduce(dkp, dvp, dlg, top_gates, dk, dv, dgates, w.n_chunks, d, st),

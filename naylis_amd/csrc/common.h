@@ -29,6 +29,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t bf16_t;  // bf16 storage in global memory
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -65,6 +66,35 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& acc, int lo) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) r[e] = (__bf16)acc[lo + e];
   return r;
+}
+
+// ds_read_b64_tr_b16 (gfx950 transposing LDS read), checked on MI355X: within
+// each 16-lane group the 16 lanes x 4 halfwords read form a 16x4 matrix;
+// output lane i, element e is input lane (4e + i/4)'s halfword (i % 4).
+__device__ __forceinline__ v4i16 lds_read_tr16(const bf16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)p);
+}
+
+// MFMA A (or B) fragment of X^T from a natural-layout LDS tile X[k][m]
+// (rows = the product's K index, contiguous along M), pitch in elements.
+// Returns, for lane l, X[k0 + kpos(8*(l/32) + e)][m0 + mrow(l % 32)], e = 0..7,
+// where kpos is the identity, or slot_perm16 when PERMK (matching P / dS taken
+// from accumulator registers), and mrow is the identity, or row_perm32 when
+// PERMM (so the product's lane group g holds rows 16g .. 16g+15).
+template <bool PERMK, bool PERMM>
+__device__ __forceinline__ bf16x8 lds_frag_T(const bf16_t* tile, int pitch, int k0, int m0) {
+  const int lane = threadIdx.x & 63;
+  const int q = (lane >> 4) & 3, j = lane & 15;
+  const int g = q >> 1, mq = q & 1, c = j & 3;
+  const int col = PERMM ? (16 * (c & 1) + 8 * mq + 4 * (c >> 1)) : (16 * mq + 4 * c);
+  const int r0 = PERMK ? 4 * g : 8 * g;
+  const int r1 = PERMK ? 8 + 4 * g : 8 * g + 4;
+  const bf16_t* base = tile + (long)(k0 + (j >> 2)) * pitch + m0 + col;
+  const v4i16 lo = lds_read_tr16(base + (long)r0 * pitch);
+  const v4i16 hi = lds_read_tr16(base + (long)r1 * pitch);
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
 }
 
 __device__ __forceinline__ float wave_max_pair(float x) {

@@ -12,7 +12,7 @@ struct RouterDims {
 
 // Byte offsets into the caller's workspace.  The forward uses [0, fwd_total).
 struct RouterWs {
-  size_t carry, w, wt, dwup_part, dwd_part;
+  size_t carry, w, wt, scan_csum, dwup_part, dwd_part;
   size_t fwd_total, total;
 };
 

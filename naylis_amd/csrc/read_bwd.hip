@@ -6,16 +6,18 @@
 // token of the batch), and d(top_gates).  P is recomputed from the forward's
 // log2-domain lse; dS = P (dP - delta), delta = rowsum(o * do).
 //
-// Three launches, all deterministic (no floating-point atomics):
+// Launches, all deterministic (no floating-point atomics):
 //  1. read_bwd_dq_kernel   — one workgroup per (b, h, 128-token tile), walks
 //     the tile's active slot groups: S^T, dP^T, dS^T, dQ^T += K^T dS^T; also
-//     writes delta and the per-head partial of dlog_gates (sum of dS over
-//     each selected block).
-//  2. read_bwd_dkdv_kernel — one workgroup per (h, 128-slot group, token
-//     chunk), K/V of its slots resident in registers, walks the chunk's
-//     64-token tiles that select any block of the group: S, dP, dS,
-//     dV^T += dO^T P, dK^T += Q^T dS, written as fp32 partials per chunk.
-//  3. read_bwd_reduce kernels — partials summed over chunks in a fixed order
+//     writes the exact delta (sum_n P dP) and the per-head partial of
+//     dlog_gates (sum of dS over each selected block).
+//  2. read_tile_flags / read_tile_lists — which 64-token tiles select any
+//     block of each 128-slot group, as compact ascending lists.
+//  3. read_bwd_dkdv_kernel — one workgroup per (h, 128-slot group, share of
+//     that group's active tiles); K/V rows of its slots stay in registers;
+//     S, dP, dS per tile, dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
+//     read transposed from the natural-layout tiles; fp32 partials per share.
+//  4. read_bwd_reduce kernels — partials summed over shares in a fixed order
 //     (dk scaled), per-head dlog partials summed over heads and mapped to
 //     d(top_gates) through log(max(g, 1e-9)).
 #include "launch.h"
@@ -27,20 +29,18 @@ namespace naylis {
 template <int HD, int SG, bool ALIGNED, int TK>
 __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const bf16_t* __restrict__ kt, const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates,
-    const bf16_t* __restrict__ o, const bf16_t* __restrict__ dout, const float* __restrict__ lse,
-    bf16_t* __restrict__ dq, float* __restrict__ delta, float* __restrict__ dlg_part, int B, int S, int H,
-    int L, int Lp, int E, int block_size, int topk, float alpha, float scale, int n_tiles) {
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
+    const bf16_t* __restrict__ dout, const float* __restrict__ lse, bf16_t* __restrict__ dq,
+    float* __restrict__ delta, float* __restrict__ dlg_part, int B, int S, int H, int L, int E, int block_size,
+    int topk, float alpha, float scale, int n_tiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NS = SG / 32;
   constexpr int NO = HDP / 32;
-  constexpr int KPAD = HD + 8;
-  constexpr int VPAD = SG + 8;
+  constexpr int PITCH = HDP + 8;
 
-  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * KPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t v_lds[SG * KPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t kt_lds[HDP * VPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[SG * PITCH];
   __shared__ uint8_t flags[kMaxBlocks];
   __shared__ uint16_t groups[kMaxGroups];
   __shared__ int n_active;
@@ -64,6 +64,9 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
   TokenRoute<TK> rt;
   load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
   for (int e = tid; e < E; e += 256) flags[e] = 0;
+  if constexpr (HD < 32) {
+    for (int i = tid; i < SG * PITCH; i += 256) k_lds[i] = 0;  // K^T rows beyond HD stay zero
+  }
   __syncthreads();
   if (g == 0 && tok_ok) {
 #pragma unroll
@@ -71,10 +74,10 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
       if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
   }
   __syncthreads();
-  const int n_groups = Lp / SG;
+  const int n_groups = (L + SG - 1) / SG;
   if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
 
-  // Q^T and dO^T fragments; delta = rowsum(o * do) from the same rows
+  // Q^T and dO^T fragments; delta0 = rowsum(o * do) from the same rows
   bf16x8 qf[KS], df[KS];
   float dl = 0.f;
 #pragma unroll
@@ -111,19 +114,17 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
   __syncthreads();
   const int n_act = n_active;
 
-  constexpr int KV_VEC = SG * HD / 8;
-  constexpr int KT_VEC = HDP * SG / 8;
-  constexpr int K_PER = (KV_VEC + 255) / 256;
-  constexpr int T_PER = (KT_VEC + 255) / 256;
-  uint4 kreg[K_PER], vreg[K_PER], treg[T_PER];
+  constexpr int VEC = SG * HD / 8;
+  constexpr int PER = (VEC + 255) / 256;
+  uint4 kreg[PER], vreg[PER];
 
   auto load_group = [&](int gi) {
     const int s0 = gi * SG;
 #pragma unroll
-    for (int r = 0; r < K_PER; ++r) {
+    for (int r = 0; r < PER; ++r) {
       const int vi = tid + 256 * r;
       uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (vi < KV_VEC) {
+      if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
         if (s0 + srow < L) {
           const long off = (long)(s0 + srow) * D + (long)h * HD + 8 * c8;
@@ -134,33 +135,15 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
       kreg[r] = kv;
       vreg[r] = vv;
     }
-#pragma unroll
-    for (int r = 0; r < T_PER; ++r) {
-      const int vi = tid + 256 * r;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (vi < KT_VEC) {
-        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
-        val = *reinterpret_cast<const uint4*>(kt + ((long)h * HDP + hr) * Lp + s0 + 8 * c8);
-      }
-      treg[r] = val;
-    }
   };
   auto store_group = [&]() {
 #pragma unroll
-    for (int r = 0; r < K_PER; ++r) {
+    for (int r = 0; r < PER; ++r) {
       const int vi = tid + 256 * r;
-      if (vi < KV_VEC) {
+      if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
-        *reinterpret_cast<uint4*>(&k_lds[srow * KPAD + 8 * c8]) = kreg[r];
-        *reinterpret_cast<uint4*>(&v_lds[srow * KPAD + 8 * c8]) = vreg[r];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < T_PER; ++r) {
-      const int vi = tid + 256 * r;
-      if (vi < KT_VEC) {
-        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
-        *reinterpret_cast<uint4*>(&kt_lds[hr * VPAD + 8 * c8]) = treg[r];
+        *reinterpret_cast<uint4*>(&k_lds[srow * PITCH + 8 * c8]) = kreg[r];
+        *reinterpret_cast<uint4*>(&v_lds[srow * PITCH + 8 * c8]) = vreg[r];
       }
     }
   };
@@ -181,7 +164,7 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
       acc_p[i] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int off = (32 * i + col) * KPAD + 16 * ks + 8 * g;
+        const int off = (32 * i + col) * PITCH + 16 * ks + 8 * g;
         const bf16x8 ak = *reinterpret_cast<const bf16x8*>(&k_lds[off]);
         const bf16x8 av = *reinterpret_cast<const bf16x8*>(&v_lds[off]);
         acc_s[i] = mfma32(ak, qf[ks], acc_s[i]);
@@ -236,13 +219,13 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
         }
     }
 
-    // dQ^T += K^T . dS^T
+    // dQ^T += K^T . dS^T  (K^T read transposed from the natural K tile)
 #pragma unroll
     for (int kk = 0; kk < SG / 16; ++kk) {
       const bf16x8 bs = pack8(acc_s[kk >> 1], 8 * (kk & 1));
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kt_lds[(32 * j + col) * VPAD + 16 * kk + 8 * g]);
+        const bf16x8 a = lds_frag_T<true, true>(k_lds, PITCH, 16 * kk, 32 * j);
         acc_dq[j] = mfma32(a, bs, acc_dq[j]);
       }
     }
@@ -280,36 +263,87 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV over the shared bank.  Lanes own slots (S = Q K^T orientation), so
-// P and dS come out of the accumulators already in the B-operand layout of
-// dV^T = dO^T P and dK^T = Q^T dS; Q^T and dO^T are staged transposed (rows
-// in row_perm32 order, tokens in slot_perm16 order) in LDS.
-template <int HD, bool ALIGNED, int TK, bool SPLIT>
-__global__ __launch_bounds__(256) void read_bwd_dkdv_kernel(
+// Active 64-token tiles per 128-slot group.
+constexpr int kDkdvTile = 64;
+
+// tile_flags[tile][e] = 1 when a token of the tile selects block e
+__global__ __launch_bounds__(64) void read_tile_flags_kernel(const int32_t* __restrict__ top_idx,
+                                                             uint8_t* __restrict__ tile_flags, long ntok, int E,
+                                                             int topk) {
+  __shared__ uint8_t fl[kMaxBlocks];
+  const long tile = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 64) fl[e] = 0;
+  __syncthreads();
+  const long tk = tile * kDkdvTile + threadIdx.x;
+  if (tk < ntok)
+    for (int t = 0; t < topk; ++t) {
+      const int id = top_idx[tk * topk + t];
+      if (id >= 0 && id < E) fl[id] = 1;
+    }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 64) tile_flags[tile * E + e] = fl[e];
+}
+
+// list[sg][0 .. count[sg]) = ascending tiles with a token selecting a block
+// that overlaps slots [128 sg, 128 sg + 128)
+__global__ __launch_bounds__(256) void read_tile_lists_kernel(const uint8_t* __restrict__ tile_flags,
+                                                              int32_t* __restrict__ list, int32_t* __restrict__ count,
+                                                              int n_ttiles, int E, int L, int block_size) {
+  __shared__ int scan[256];
+  const int sg = blockIdx.x;
+  const int blk_lo = (sg * 128) / block_size;
+  const int blk_hi = min((min(sg * 128 + 128, L) - 1) / block_size, E - 1);
+  int total = 0;
+  for (int base = 0; base < n_ttiles; base += 256) {
+    const int t = base + threadIdx.x;
+    int act = 0;
+    if (t < n_ttiles)
+      for (int e = blk_lo; e <= blk_hi; ++e) act |= tile_flags[(long)t * E + e];
+    scan[threadIdx.x] = act;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int vadd = threadIdx.x >= off ? scan[threadIdx.x - off] : 0;
+      __syncthreads();
+      scan[threadIdx.x] += vadd;
+      __syncthreads();
+    }
+    if (act) list[(long)sg * n_ttiles + total + scan[threadIdx.x] - 1] = t;
+    total += scan[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) count[sg] = total;
+}
+
+// dK / dV over the shared bank.  8 waves: wave w owns slots
+// 128 sg + 32 (w & 3) + lane%32 and the token half (w >> 2) of each 64-token
+// tile.  Lanes own slots (S = Q K^T orientation), so P and dS come out of the
+// accumulators already in the B-operand layout of dV^T = dO^T P and
+// dK^T = Q^T dS, whose A operands are read transposed from the tiles.
+template <int HD, bool ALIGNED, int TK, bool SPLIT_V>
+__global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dk_part,
-    float* __restrict__ dv_part, int B, int S, int H, int L, int Lq, int E, int block_size, int topk,
-    float alpha, int n_chunks, int tiles_per_chunk) {
+    const float* __restrict__ lse, const float* __restrict__ delta, const int32_t* __restrict__ tile_list,
+    const int32_t* __restrict__ tile_count, float* __restrict__ dk_part, float* __restrict__ dv_part, int B, int S,
+    int H, int L, int Lq, int E, int block_size, int topk, float alpha, int n_chunks, int n_ttiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NO = HDP / 32;
-  constexpr int TT = 64;            // tokens per staged tile
-  constexpr int NT = TT / 32;       // 32-token accumulator tiles
-  constexpr int QPAD = HD + 8;
-  constexpr int TPAD = TT + 8;
+  constexpr int TT = kDkdvTile;
+  constexpr int PITCH = HDP + 8;
+  constexpr int VEC = TT * HD / 8;        // 16-byte vectors per staged tensor tile
+  constexpr int PER = (VEC + 511) / 512;
 
-  __shared__ __attribute__((aligned(16))) bf16_t q_lds[TT * QPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t do_lds[TT * QPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t qt_lds[HDP * TPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t dot_lds[HDP * TPAD];
-  __shared__ __attribute__((aligned(16))) float add_lds[4][TT];   // per wave-block: c2 - lse or -inf
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds[TT * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t do_lds[TT * PITCH];
+  __shared__ __attribute__((aligned(16))) float add_lds[4][TT];  // per quarter: c2 - lse, or -inf
   __shared__ __attribute__((aligned(16))) float dl_lds[TT];
   __shared__ int32_t idx_lds[TT * TK];
   __shared__ float lg_lds[TT * TK];
   __shared__ float lse_lds[TT];
+  __shared__ __attribute__((aligned(16))) float red[4 * NO * 16 * 64];  // half-1 partials for the final sum
 
-  const int n_sg = Lq / 128;  // Lq = L rounded up to 128: rows of the partials
+  const int n_sg = Lq / 128;
   const int G = H * n_sg * n_chunks;
   const int wid = xcd_remap(blockIdx.x, G);
   const int chunk = wid % n_chunks;
@@ -319,20 +353,21 @@ __global__ __launch_bounds__(256) void read_bwd_dkdv_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int quarter = wave & 3, half = wave >> 2;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const int slot = sg * 128 + wave * 32 + col;
+  const int slot = sg * 128 + quarter * 32 + col;
   const bool slot_ok = slot < L;
   const int D = H * HD;
   const long ntok = (long)B * S;
-  const int n_ttiles = (int)((ntok + TT - 1) / TT);
-
-  // blocks covered by this workgroup's 128 slots
-  const int blk_lo = (sg * 128) / block_size;
-  const int blk_hi = (min(sg * 128 + 128, L) - 1) / block_size;
   const int lane_blk = slot / block_size;
 
-  // K and V rows of this lane's slot as B fragments (K^T / V^T columns)
+  // this workgroup's share of the group's active tiles
+  const int cnt = tile_count[sg];
+  const int per = (cnt + n_chunks - 1) / n_chunks;
+  const int i_begin = min(cnt, chunk * per), i_end = min(cnt, i_begin + per);
+  const int32_t* tiles = tile_list + (long)sg * n_ttiles;
+
   bf16x8 kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -345,182 +380,195 @@ __global__ __launch_bounds__(256) void read_bwd_dkdv_kernel(
       vf[ks] = bf16x8{};
     }
   }
-
   f32x16 acc_dk[NO], acc_dv[NO];
 #pragma unroll
   for (int j = 0; j < NO; ++j) {
     acc_dk[j] = f32x16{};
     acc_dv[j] = f32x16{};
   }
+  if constexpr (HD < 32) {
+    for (int i = tid; i < TT * PITCH; i += 512) {
+      q_lds[i] = 0;
+      do_lds[i] = 0;
+    }
+  }
 
-  const int t_begin = chunk * tiles_per_chunk;
-  const int t_end = min(n_ttiles, t_begin + tiles_per_chunk);
-  for (int tt = t_begin; tt < t_end; ++tt) {
+  // prefetch registers: Q / dO vectors, per-token routing, lse, delta
+  uint4 qreg[PER], dreg[PER];
+  int pidx[TK];
+  float pg[TK], plse = 0.f, pdl = 0.f;
+  auto load_tile = [&](int tt) {
     const long tok0 = (long)tt * TT;
-    // ---- routing of the tile; is any block of this group selected?
-    bool any = false;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int vi = tid + 512 * r;
+      uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
+      if (vi < VEC) {
+        const int row = vi / (HD / 8), c8 = vi % (HD / 8);
+        const long tk = tok0 + row;
+        if (tk < ntok) {
+          const long off = tk * D + (long)h * HD + 8 * c8;
+          qv = *reinterpret_cast<const uint4*>(q + off);
+          dv4 = *reinterpret_cast<const uint4*>(dout + off);
+        }
+      }
+      qreg[r] = qv;
+      dreg[r] = dv4;
+    }
     if (tid < TT) {
       const long tk = tok0 + tid;
       const bool ok = tk < ntok;
 #pragma unroll
       for (int t = 0; t < TK; ++t) {
-        int id = -1;
-        float lg = 0.f;
-        if (t < topk && ok) {
-          id = top_idx[tk * topk + t];
-          lg = log2f(fmaxf(top_gates[tk * topk + t], 1e-9f));
-          any |= (id >= blk_lo && id <= blk_hi);
-        }
-        idx_lds[tid * TK + t] = id;
-        lg_lds[tid * TK + t] = lg;
+        pidx[t] = (ok && t < topk) ? top_idx[tk * topk + t] : -1;
+        pg[t] = (ok && t < topk) ? top_gates[tk * topk + t] : 1.f;
       }
-      float ls = 0.f, dlv = 0.f;
+      plse = 0.f;
+      pdl = 0.f;
       if (ok) {
         const long bb = tk / S, ss = tk % S;
-        ls = lse[(bb * H + h) * S + ss];
-        dlv = delta[(bb * H + h) * S + ss];
+        plse = lse[(bb * H + h) * S + ss];
+        pdl = delta[(bb * H + h) * S + ss];
       }
-      lse_lds[tid] = ls;
-      dl_lds[tid] = dlv;
     }
-    if (!__syncthreads_or(any)) continue;
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int vi = tid + 512 * r;
+      if (vi < VEC) {
+        const int row = vi / (HD / 8), c8 = vi % (HD / 8);
+        *reinterpret_cast<uint4*>(&q_lds[row * PITCH + 8 * c8]) = qreg[r];
+        *reinterpret_cast<uint4*>(&do_lds[row * PITCH + 8 * c8]) = dreg[r];
+      }
+    }
+    if (tid < TT) {
+      float lg2[TK];
+#pragma unroll
+      for (int t = 0; t < TK; ++t) {
+        lg2[t] = log2f(fmaxf(pg[t], 1e-9f));
+        idx_lds[tid * TK + t] = pidx[t];
+        lg_lds[tid * TK + t] = lg2[t];
+      }
+      lse_lds[tid] = plse;
+      dl_lds[tid] = pdl;
+      if constexpr (ALIGNED) {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int e = (sg * 128 + qq * 32) / block_size;
+          float c = 0.f;
+          bool sel = false;
+#pragma unroll
+          for (int t = 0; t < TK; ++t)
+            if (t < topk && pidx[t] == e) {
+              c += lg2[t];
+              sel = true;
+            }
+          add_lds[qq][tid] = sel ? c - plse : -INFINITY;
+        }
+      }
+    }
+  };
 
-    // ---- stage Q, dO (natural) and Q^T, dO^T (transposed) for the tile
-    for (int vi = tid; vi < TT * HD / 8; vi += 256) {
-      const int r = vi / (HD / 8), c8 = vi % (HD / 8);
-      const long tk = tok0 + r;
-      uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
-      if (tk < ntok) {
-        const long off = tk * D + (long)h * HD + 8 * c8;
-        qv = *reinterpret_cast<const uint4*>(q + off);
-        dv4 = *reinterpret_cast<const uint4*>(dout + off);
-      }
-      *reinterpret_cast<uint4*>(&q_lds[r * QPAD + 8 * c8]) = qv;
-      *reinterpret_cast<uint4*>(&do_lds[r * QPAD + 8 * c8]) = dv4;
-      const bf16_t* qs = reinterpret_cast<const bf16_t*>(&qv);
-      const bf16_t* ds = reinterpret_cast<const bf16_t*>(&dv4);
-      const int tp = 16 * (r / 16) + slot_perm16(r % 16);  // token position (involution)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int hd = 8 * c8 + e;
-        const int row = 32 * (hd / 32) + row_unperm32(hd % 32);
-        qt_lds[row * TPAD + tp] = qs[e];
-        dot_lds[row * TPAD + tp] = ds[e];
-      }
-    }
-    if constexpr (HD < 32) {
-      // zero the padding rows of the transposed tiles (features >= HD)
-      for (int i = tid; i < 32 * TT; i += 256) {
-        const int row = i / TT, c = i % TT;
-        if (row_perm32(row) >= HD) {
-          qt_lds[row * TPAD + c] = 0;
-          dot_lds[row * TPAD + c] = 0;
-        }
-      }
-    }
-    if constexpr (ALIGNED) {
-      // per (wave block, token) additive term of the exp2 argument
-      const int w = tid >> 6, r = tid & 63;
-      const int e = (sg * 128 + w * 32) / block_size;
-      float c = 0.f;
-      bool sel = false;
-#pragma unroll
-      for (int t = 0; t < TK; ++t)
-        if (t < topk && idx_lds[r * TK + t] == e) {
-          c += lg_lds[r * TK + t];
-          sel = true;
-        }
-      add_lds[w][r] = sel ? c - lse_lds[r] : -INFINITY;
-    }
+  if (i_begin < i_end) load_tile(tiles[i_begin]);
+  for (int it = i_begin; it < i_end; ++it) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    store_tile();
     __syncthreads();
+    if (it + 1 < i_end) load_tile(tiles[it + 1]);  // in flight during the math below
 
-    // ---- S = Q K^T and dP = dO V^T (tokens x slots, lanes = slots)
-    f32x16 acc_s[NT], acc_p[NT];
+    // ---- S = Q K^T and dP = dO V^T for this wave's 32 tokens x 32 slots
+    f32x16 acc_s = f32x16{}, acc_p = f32x16{};
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      acc_s[i] = f32x16{};
-      acc_p[i] = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int off = (32 * i + col) * QPAD + 16 * ks + 8 * g;
-        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
-        const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[off]);
-        acc_s[i] = mfma32(aq, kf[ks], acc_s[i]);
-        acc_p[i] = mfma32(ad, vf[ks], acc_p[i]);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = (32 * half + col) * PITCH + 16 * ks + 8 * g;
+      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
+      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[off]);
+      acc_s = mfma32(aq, kf[ks], acc_s);
+      acc_p = mfma32(ad, vf[ks], acc_p);
     }
-
     // ---- P and dS, registers indexed by token
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const int r0 = 32 * i + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
-        const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&dl_lds[r0]);
-        f32x4 ad4;
-        if constexpr (ALIGNED) {
-          ad4 = *reinterpret_cast<const f32x4*>(&add_lds[wave][r0]);
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            float c = 0.f;
-            bool sel = false;
-#pragma unroll
-            for (int t = 0; t < TK; ++t)
-              if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
-                c += lg_lds[(r0 + u) * TK + t];
-                sel = true;
-              }
-            ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
-          }
-        }
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const int r0 = 32 * half + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
+      const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&dl_lds[r0]);
+      f32x4 ad4;
+      if constexpr (ALIGNED) {
+        ad4 = *reinterpret_cast<const f32x4*>(&add_lds[quarter][r0]);
+      } else {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int vv = 4 * j4 + u;
-          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, ad4[u]));
-          acc_s[i][vv] = p;
-          acc_p[i][vv] = p * (acc_p[i][vv] - dl4[u]);
+          float c = 0.f;
+          bool sel = false;
+#pragma unroll
+          for (int t = 0; t < TK; ++t)
+            if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
+              c += lg_lds[(r0 + u) * TK + t];
+              sel = true;
+            }
+          ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
         }
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vv = 4 * j4 + u;
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, ad4[u]));
+        acc_s[vv] = p;
+        acc_p[vv] = p * (acc_p[vv] - dl4[u]);
+      }
     }
-
-    // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = tokens)
-    // These two products sum over every token of the batch (thousands of
-    // terms), so P and dS enter as a compensated pair hi + lo of bf16
-    // values (hi = bf16(x), lo = bf16(x - hi)): the bf16 rounding of P/dS
-    // would otherwise dominate the error of small dK/dV entries.
+    // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = this wave's 32 tokens)
+    // dV sums P over thousands of tokens, so P enters as hi + lo bf16 parts
+    // (hi = bf16(P), lo = bf16(P - hi)); bf16 rounding of P would otherwise
+    // dominate the error of small dV entries.
 #pragma unroll
-    for (int kk = 0; kk < TT / 16; ++kk) {
-      const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
-      const bf16x8 bd = pack8(acc_p[kk >> 1], 8 * (kk & 1));
-      bf16x8 bp_lo, bd_lo;
-      if constexpr (SPLIT) {
+    for (int kk = 0; kk < 2; ++kk) {
+      const bf16x8 bp = pack8(acc_s, 8 * kk);
+      const bf16x8 bd = pack8(acc_p, 8 * kk);
+      bf16x8 bp_lo;
+      if constexpr (SPLIT_V) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bp_lo[e] = (__bf16)(acc_s[kk >> 1][8 * (kk & 1) + e] - (float)bp[e]);
-          bd_lo[e] = (__bf16)(acc_p[kk >> 1][8 * (kk & 1) + e] - (float)bd[e]);
-        }
+        for (int e = 0; e < 8; ++e) bp_lo[e] = (__bf16)(acc_s[8 * kk + e] - (float)bp[e]);
       }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
-        const int off = (32 * j + col) * TPAD + 16 * kk + 8 * g;
-        const bf16x8 a_do = *reinterpret_cast<const bf16x8*>(&dot_lds[off]);
-        const bf16x8 a_q = *reinterpret_cast<const bf16x8*>(&qt_lds[off]);
+        const bf16x8 a_do = lds_frag_T<true, true>(do_lds, PITCH, 32 * half + 16 * kk, 32 * j);
+        const bf16x8 a_q = lds_frag_T<true, true>(q_lds, PITCH, 32 * half + 16 * kk, 32 * j);
         acc_dv[j] = mfma32(a_do, bp, acc_dv[j]);
+        if constexpr (SPLIT_V) acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
         acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
-        if constexpr (SPLIT) {
-          acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
-          acc_dk[j] = mfma32(a_q, bd_lo, acc_dk[j]);
-        }
       }
     }
-    __syncthreads();  // LDS tiles are rewritten by the next iteration
   }
 
-  // ---- fp32 partials of this chunk: part[chunk][slot][h*HD + f]
-  if (slot_ok) {
+  // ---- sum the two token halves (fixed order), write this share's partials
+  __syncthreads();
+  if (half == 1) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dk[j][vv];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) acc_dk[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
+  }
+  __syncthreads();
+  if (half == 1) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dv[j][vv];
+  }
+  __syncthreads();
+  if (half == 0 && slot_ok) {
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) acc_dv[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
       const int f0 = 32 * j + 16 * g;
       if (f0 < HD) {
         const long base = ((long)chunk * Lq + slot) * D + (long)h * HD + f0;
@@ -536,7 +584,7 @@ __global__ __launch_bounds__(256) void read_bwd_dkdv_kernel(
   }
 }
 
-// dk/dv = sum over chunks (fixed order) of the fp32 partials; dk scaled.
+// dk/dv = sum over shares (fixed order) of the fp32 partials; dk scaled.
 __global__ void read_bwd_reduce_kv_kernel(const float* __restrict__ dk_part, const float* __restrict__ dv_part,
                                           bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long n, long stride,
                                           int n_chunks, float scale) {
@@ -573,93 +621,110 @@ __global__ void read_bwd_reduce_gates_kernel(const float* __restrict__ dlg_part,
 static float read_scale(int HD) { return (float)(1.0 / __builtin_sqrt((double)HD)); }
 
 template <int HD, int SG, bool AL, int TK>
-static void dq_inst(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
-                    const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
-                    const ReadDims& d, hipStream_t st) {
+static void dq_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
+                    const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
+                    hipStream_t st) {
   const int n_tiles = (d.S + 127) / 128;
   const float scale = read_scale(HD);
-  NAYLIS_TIMED("read_bwd_dq", st, hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
-                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)kt, ti, tg,
-                     (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.B, d.S, d.H, d.L,
-                     read_lp(d.L), d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
+  NAYLIS_TIMED("read_bwd_dq", st,
+               hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+                                  (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)o,
+                                  (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.B, d.S, d.H, d.L, d.E,
+                                  d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
 }
 
 template <int HD, int TK>
-static void dq_hdk(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
-                  const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
-                  const ReadDims& d, hipStream_t st) {
+static void dq_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
+                   const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
+                   hipStream_t st) {
   constexpr int SGMAX = HD <= 64 ? 64 : 32;
   if (d.block_size % SGMAX == 0)
-    dq_inst<HD, SGMAX, true, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_inst<HD, SGMAX, true, TK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
   else if (d.block_size % 32 == 0)
-    dq_inst<HD, 32, true, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_inst<HD, 32, true, TK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
   else
-    dq_inst<HD, 32, false, TK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_inst<HD, 32, false, TK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
 }
 
 template <int HD>
-static void dq_hd(const void* q, const void* k, const void* v, const void* kt, const int32_t* ti, const float* tg,
-                  const void* o, const void* dout, const float* lse, void* dq, float* delta, float* dlg,
-                  const ReadDims& d, hipStream_t st) {
+static void dq_hd(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
+                  const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
+                  hipStream_t st) {
   if (d.topk <= 2)
-    dq_hdk<HD, 2>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_hdk<HD, 2>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
   else
-    dq_hdk<HD, kMaxTopK>(q, k, v, kt, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_hdk<HD, kMaxTopK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
 }
 
-hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const void* kt, const int32_t* top_idx,
+hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const int32_t* top_idx,
                               const float* top_gates, const void* o, const void* dout, const float* lse, void* dq,
                               float* delta, float* dlg_part, const ReadDims& d, hipStream_t st) {
   switch (d.HD) {
-    case 16: dq_hd<16>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 32: dq_hd<32>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 64: dq_hd<64>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 128: dq_hd<128>(q, k, v, kt, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 16: dq_hd<16>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 32: dq_hd<32>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 64: dq_hd<64>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 128: dq_hd<128>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+int read_bwd_n_ttiles(const ReadDims& d) { return (int)(((long)d.B * d.S + kDkdvTile - 1) / kDkdvTile); }
+
 int read_bwd_chunks(const ReadDims& d) {
-  const long ntok = (long)d.B * d.S;
-  const int n_ttiles = (int)((ntok + 63) / 64);
+  // shares per 128-slot group: enough workgroups to cover the chip twice
+  const int n_tt = read_bwd_n_ttiles(d);
   const int per_chunk_wgs = d.H * (read_lq(d.L) / 128);
   int nc = (512 + per_chunk_wgs - 1) / per_chunk_wgs;
-  if (nc > n_ttiles) nc = n_ttiles;
+  if (nc > n_tt) nc = n_tt;
   if (nc < 1) nc = 1;
   return nc;
 }
 
+hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, int32_t* list, int32_t* count,
+                                  const ReadDims& d, hipStream_t st) {
+  const long ntok = (long)d.B * d.S;
+  const int n_tt = read_bwd_n_ttiles(d);
+  if (n_tt > 0)
+    NAYLIS_TIMED("read_tile_lists", st,
+                 hipLaunchKernelGGL(read_tile_flags_kernel, dim3(n_tt), dim3(64), 0, st, top_idx, tile_flags, ntok, d.E,
+                                    d.topk));
+  NAYLIS_TIMED("read_tile_lists", st,
+               hipLaunchKernelGGL(read_tile_lists_kernel, dim3(read_lq(d.L) / 128), dim3(256), 0, st, tile_flags, list,
+                                  count, n_tt, d.E, d.L, d.block_size));
+  return hipGetLastError();
+}
+
 template <int HD, bool AL, int TK>
 static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg,
-                      const void* dout, const float* lse, const float* delta, float* dkp, float* dvp, int nc,
-                      const ReadDims& d, hipStream_t st) {
-  const long ntok = (long)d.B * d.S;
-  const int n_ttiles = (int)((ntok + 63) / 64);
-  const int tpc = (n_ttiles + nc - 1) / nc;
+                      const void* dout, const float* lse, const float* delta, const int32_t* list,
+                      const int32_t* count, float* dkp, float* dvp, int nc, const ReadDims& d, hipStream_t st) {
   const int Lq = read_lq(d.L);
   const float alpha = read_scale(HD) * kLog2e;
-  NAYLIS_TIMED("read_bwd_dkdv", st, hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(256), 0, st,
-                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)dout, lse, delta,
-                     dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc, tpc));
+  NAYLIS_TIMED("read_bwd_dkdv", st,
+               hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(512), 0,
+                                  st, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
+                                  (const bf16_t*)dout, lse, delta, list, count, dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E,
+                                  d.block_size, d.topk, alpha, nc, read_bwd_n_ttiles(d)));
 }
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const void* dout, const float* lse, const float* delta,
-                                float* dk_part, float* dv_part, int n_chunks, const ReadDims& d, hipStream_t st) {
+                                const int32_t* list, const int32_t* count, float* dk_part, float* dv_part,
+                                int n_chunks, const ReadDims& d, hipStream_t st) {
   const bool al = d.block_size % 32 == 0;
-#define NAYLIS_DKDV2(HDV, TKV)                                                                                \
-  if (al)                                                                                                     \
-    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, dk_part, dv_part, n_chunks, d,   \
-                              st);                                                                            \
-  else                                                                                                        \
-    dkdv_inst<HDV, false, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, dk_part, dv_part, n_chunks, d,  \
-                               st);
-#define NAYLIS_DKDV(HDV)          \
-  if (d.topk <= 2) {              \
-    NAYLIS_DKDV2(HDV, 2)          \
-  } else {                        \
-    NAYLIS_DKDV2(HDV, kMaxTopK)   \
+#define NAYLIS_DKDV2(HDV, TKV)                                                                                 \
+  if (al)                                                                                                      \
+    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part,    \
+                              n_chunks, d, st);                                                                \
+  else                                                                                                         \
+    dkdv_inst<HDV, false, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part,   \
+                               n_chunks, d, st);
+#define NAYLIS_DKDV(HDV)        \
+  if (d.topk <= 2) {            \
+    NAYLIS_DKDV2(HDV, 2)        \
+  } else {                      \
+    NAYLIS_DKDV2(HDV, kMaxTopK) \
   }
   switch (d.HD) {
     case 16: NAYLIS_DKDV(16) break;
@@ -681,14 +746,16 @@ hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, co
   const long stride = (long)read_lq(d.L) * D;
   long blocks = (n / 4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  NAYLIS_TIMED("read_bwd_reduce_kv", st, hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
-                     (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD)));
+  NAYLIS_TIMED("read_bwd_reduce_kv", st,
+               hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
+                                  (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD)));
   const long ng = (long)d.B * d.S * d.topk;
   if (ng > 0) {
     long gb = (ng + 255) / 256;
     if (gb > 8192) gb = 8192;
-    NAYLIS_TIMED("read_bwd_reduce_gates", st, hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates, dgates,
-                       ng, d.H));
+    NAYLIS_TIMED("read_bwd_reduce_gates", st,
+                 hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates,
+                                    dgates, ng, d.H));
   }
   return hipGetLastError();
 }

@@ -12,47 +12,30 @@
 // which bank blocks any of its tokens selects and then walks only those
 // blocks' slot groups (SG slots): S^T = K_g Q^T (slots x tokens, K from LDS,
 // Q^T resident in registers), online softmax per token column, O^T += V_g^T P^T
-// with P^T taken straight from the accumulator registers.
+// with P^T taken straight from the accumulator registers and V^T read from
+// the natural-layout V tile with the transposing LDS read.  K and V tiles
+// are plain 16-byte copies of the bank rows; the next group's copy is in
+// flight while the current group is computed.
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
 
 namespace naylis {
 
-// Relayout of a (L, H*HD) bank projection into (H, HDP, Lp): per head, rows
-// are features in row_perm32 order (padded to HDP = max(HD, 32)), columns are
-// slots in slot_perm16 order (padded to Lp = L rounded up to 32), zero fill.
-// This is the A operand of every "X^T . P^T" product of the read.
-__global__ void bank_relayout_kernel(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, int L,
-                                     int Lp, int H, int HD, int HDP) {
-  const long n = (long)H * HDP * Lp;
-  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
-    const int sp = (int)(i % Lp);
-    const int hr = (int)((i / Lp) % HDP);
-    const int h = (int)(i / ((long)Lp * HDP));
-    const int hd = 32 * (hr / 32) + row_perm32(hr % 32);
-    const int slot = 16 * (sp / 16) + slot_perm16(sp % 16);
-    bf16_t v = 0;
-    if (hd < HD && slot < L) v = src[(long)slot * H * HD + (long)h * HD + hd];
-    dst[i] = v;
-  }
-}
-
 template <int HD, int SG, bool ALIGNED, int TK>
 __global__ __launch_bounds__(256) void read_fwd_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
-    float* __restrict__ lse, int B, int S, int H, int L, int Lp, int E, int block_size, int topk,
-    float alpha, int n_tiles) {
+    float* __restrict__ lse, int B, int S, int H, int L, int E, int block_size, int topk, float alpha,
+    int n_tiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;       // K-steps over features for Q.K^T
   constexpr int NS = SG / 32;       // 32-slot accumulator tiles per group
   constexpr int NO = HDP / 32;      // 32-feature output tiles
-  constexpr int KPAD = HD + 8;      // LDS row pitch (bf16) of the K tile
-  constexpr int VPAD = SG + 8;      // LDS row pitch (bf16) of the V^T tile
+  constexpr int PITCH = HDP + 8;    // LDS row pitch (bf16) of the K and V tiles
 
-  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * KPAD];
-  __shared__ __attribute__((aligned(16))) bf16_t vt_lds[HDP * VPAD];
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[SG * PITCH];
   __shared__ uint8_t flags[kMaxBlocks];
   __shared__ uint16_t groups[kMaxGroups];
   __shared__ int n_active;
@@ -77,6 +60,10 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
   TokenRoute<TK> rt;
   load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
   for (int e = tid; e < E; e += 256) flags[e] = 0;
+  if constexpr (HD < 32) {
+    // feature columns HD..31 of the V tile stay zero (V^T rows beyond HD)
+    for (int i = tid; i < SG * PITCH; i += 256) v_lds[i] = 0;
+  }
   __syncthreads();
   if (g == 0 && tok_ok) {
 #pragma unroll
@@ -84,7 +71,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
       if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
   }
   __syncthreads();
-  const int n_groups = Lp / SG;
+  const int n_groups = (L + SG - 1) / SG;
   if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
 
   // ---- Q^T fragments (B operand): lane holds q[token][16*ks + 8*g .. +8]
@@ -105,52 +92,37 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
   __syncthreads();
   const int n_act = n_active;
 
-  // staging: K group (SG x HD) and V^T group (HDP x SG) as 16-byte vectors
-  constexpr int KV_VEC = SG * HD / 8;
-  constexpr int VT_VEC = HDP * SG / 8;
-  constexpr int K_PER = (KV_VEC + 255) / 256;
-  constexpr int V_PER = (VT_VEC + 255) / 256;
-  uint4 kreg[K_PER], vreg[V_PER];
+  // staging: K and V rows of the group (SG x HD) as 16-byte vectors
+  constexpr int VEC = SG * HD / 8;
+  constexpr int PER = (VEC + 255) / 256;
+  uint4 kreg[PER], vreg[PER];
 
   auto load_group = [&](int gi) {
     const int s0 = gi * SG;
 #pragma unroll
-    for (int r = 0; r < K_PER; ++r) {
+    for (int r = 0; r < PER; ++r) {
       const int vi = tid + 256 * r;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (vi < KV_VEC) {
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
-        if (s0 + srow < L)
-          val = *reinterpret_cast<const uint4*>(k + (long)(s0 + srow) * D + (long)h * HD + 8 * c8);
+        if (s0 + srow < L) {
+          const long off = (long)(s0 + srow) * D + (long)h * HD + 8 * c8;
+          kv = *reinterpret_cast<const uint4*>(k + off);
+          vv = *reinterpret_cast<const uint4*>(v + off);
+        }
       }
-      kreg[r] = val;
-    }
-#pragma unroll
-    for (int r = 0; r < V_PER; ++r) {
-      const int vi = tid + 256 * r;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (vi < VT_VEC) {
-        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
-        val = *reinterpret_cast<const uint4*>(vt + ((long)h * HDP + hr) * Lp + s0 + 8 * c8);
-      }
-      vreg[r] = val;
+      kreg[r] = kv;
+      vreg[r] = vv;
     }
   };
   auto store_group = [&]() {
 #pragma unroll
-    for (int r = 0; r < K_PER; ++r) {
+    for (int r = 0; r < PER; ++r) {
       const int vi = tid + 256 * r;
-      if (vi < KV_VEC) {
+      if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
-        *reinterpret_cast<uint4*>(&k_lds[srow * KPAD + 8 * c8]) = kreg[r];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < V_PER; ++r) {
-      const int vi = tid + 256 * r;
-      if (vi < VT_VEC) {
-        const int hr = vi / (SG / 8), c8 = vi % (SG / 8);
-        *reinterpret_cast<uint4*>(&vt_lds[hr * VPAD + 8 * c8]) = vreg[r];
+        *reinterpret_cast<uint4*>(&k_lds[srow * PITCH + 8 * c8]) = kreg[r];
+        *reinterpret_cast<uint4*>(&v_lds[srow * PITCH + 8 * c8]) = vreg[r];
       }
     }
   };
@@ -171,7 +143,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
       acc_s[i] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * i + col) * KPAD + 16 * ks + 8 * g]);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * i + col) * PITCH + 16 * ks + 8 * g]);
         acc_s[i] = mfma32(a, qf[ks], acc_s[i]);
       }
     }
@@ -180,12 +152,12 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
     float m_new = m_run;
     if constexpr (ALIGNED) {
       bool sel;
-      const float c2 = route_bias(rt, (gi * SG) / block_size, topk, sel);
+      const float c2 = route_bias<TK>(rt, (gi * SG) / block_size, topk, sel);
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc_s[i][v]);
+        for (int vv = 0; vv < 16; ++vv) mx = fmaxf(mx, acc_s[i][vv]);
       mx = wave_max_pair(mx);
       if (sel) m_new = fmaxf(m_run, fmaf(mx, alpha, c2));
       const float add = sel ? c2 - m_new : -INFINITY;
@@ -193,31 +165,33 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
 #pragma unroll
       for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][v], alpha, add));
-          acc_s[i][v] = p;
+        for (int vv = 0; vv < 16; ++vv) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, add));
+          acc_s[i][vv] = p;
           rs += p;
         }
       rs = wave_sum_pair(rs);
       const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run = fmaf(l_run, corr, rs);
+      if (__any(corr != 1.f)) {
 #pragma unroll
-      for (int j = 0; j < NO; ++j)
+        for (int j = 0; j < NO; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc_o[j][v] *= corr;
+          for (int vv = 0; vv < 16; ++vv) acc_o[j][vv] *= corr;
+      }
     } else {
       // generic slot->block lookup per element (block_size not a multiple of SG)
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int slot = gi * SG + 32 * i + acc_row(g, v);
+        for (int vv = 0; vv < 16; ++vv) {
+          const int slot = gi * SG + 32 * i + acc_row(g, vv);
           bool sel = false;
           float c2 = 0.f;
-          if (slot < L) c2 = route_bias(rt, slot / block_size, topk, sel);
-          const float t = sel ? fmaf(acc_s[i][v], alpha, c2) : -INFINITY;
-          acc_s[i][v] = t;
+          if (slot < L) c2 = route_bias<TK>(rt, slot / block_size, topk, sel);
+          const float t = sel ? fmaf(acc_s[i][vv], alpha, c2) : -INFINITY;
+          acc_s[i][vv] = t;
           mx = fmaxf(mx, t);
         }
       mx = wave_max_pair(mx);
@@ -226,9 +200,9 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
 #pragma unroll
       for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = __builtin_amdgcn_exp2f(acc_s[i][v] - m_new);
-          acc_s[i][v] = p;
+        for (int vv = 0; vv < 16; ++vv) {
+          const float p = __builtin_amdgcn_exp2f(acc_s[i][vv] - m_new);
+          acc_s[i][vv] = p;
           rs += p;
         }
       rs = wave_sum_pair(rs);
@@ -237,7 +211,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
 #pragma unroll
       for (int j = 0; j < NO; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc_o[j][v] *= corr;
+        for (int vv = 0; vv < 16; ++vv) acc_o[j][vv] *= corr;
     }
     m_run = m_new;
 
@@ -247,7 +221,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
       const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&vt_lds[(32 * j + col) * VPAD + 16 * kk + 8 * g]);
+        const bf16x8 a = lds_frag_T<true, true>(v_lds, PITCH, 16 * kk, 32 * j);
         acc_o[j] = mfma32(a, bp, acc_o[j]);
       }
     }
@@ -276,55 +250,47 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-hipError_t launch_bank_relayout(const void* src, void* dst, const ReadDims& d, hipStream_t st) {
-  const int HDP = read_hdp(d.HD), Lp = read_lp(d.L);
-  const long n = (long)d.H * HDP * Lp;
-  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-  NAYLIS_TIMED("bank_relayout", st, hipLaunchKernelGGL(bank_relayout_kernel, dim3(blocks), dim3(256), 0, st, (const bf16_t*)src, (bf16_t*)dst, d.L, Lp,
-                     d.H, d.HD, HDP));
-  return hipGetLastError();
-}
-
 template <int HD, int SG, bool AL, int TK>
-static void fwd_inst(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
+static void fwd_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                      float* lse, const ReadDims& d, hipStream_t st) {
   const int n_tiles = (d.S + 127) / 128;
   const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
-  NAYLIS_TIMED("read_fwd", st, hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st, (const bf16_t*)q,
-                     (const bf16_t*)k, (const bf16_t*)vt, ti, tg, (bf16_t*)out, lse, d.B, d.S, d.H, d.L,
-                     read_lp(d.L), d.E, d.block_size, d.topk, alpha, n_tiles));
+  NAYLIS_TIMED("read_fwd", st,
+               hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+                                  (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (bf16_t*)out, lse,
+                                  d.B, d.S, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
 }
 
 template <int HD, int TK>
-static void fwd_hdk(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
-                   float* lse, const ReadDims& d, hipStream_t st) {
+static void fwd_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
+                    float* lse, const ReadDims& d, hipStream_t st) {
   constexpr int SGMAX = HD <= 64 ? 128 : 64;
   if (d.block_size % SGMAX == 0)
-    fwd_inst<HD, SGMAX, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_inst<HD, SGMAX, true, TK>(q, k, v, ti, tg, out, lse, d, st);
   else if (d.block_size % 64 == 0)
-    fwd_inst<HD, 64, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_inst<HD, 64, true, TK>(q, k, v, ti, tg, out, lse, d, st);
   else if (d.block_size % 32 == 0)
-    fwd_inst<HD, 32, true, TK>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_inst<HD, 32, true, TK>(q, k, v, ti, tg, out, lse, d, st);
   else
-    fwd_inst<HD, 32, false, TK>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_inst<HD, 32, false, TK>(q, k, v, ti, tg, out, lse, d, st);
 }
 
 template <int HD>
-static void fwd_hd(const void* q, const void* k, const void* vt, const int32_t* ti, const float* tg, void* out,
+static void fwd_hd(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                    float* lse, const ReadDims& d, hipStream_t st) {
   if (d.topk <= 2)
-    fwd_hdk<HD, 2>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_hdk<HD, 2>(q, k, v, ti, tg, out, lse, d, st);
   else
-    fwd_hdk<HD, kMaxTopK>(q, k, vt, ti, tg, out, lse, d, st);
+    fwd_hdk<HD, kMaxTopK>(q, k, v, ti, tg, out, lse, d, st);
 }
 
-hipError_t launch_read_fwd(const void* q, const void* k, const void* vt, const int32_t* top_idx,
+hipError_t launch_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
                            const float* top_gates, void* out, float* lse, const ReadDims& d, hipStream_t st) {
   switch (d.HD) {
-    case 16: fwd_hd<16>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
-    case 32: fwd_hd<32>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
-    case 64: fwd_hd<64>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
-    case 128: fwd_hd<128>(q, k, vt, top_idx, top_gates, out, lse, d, st); break;
+    case 16: fwd_hd<16>(q, k, v, top_idx, top_gates, out, lse, d, st); break;
+    case 32: fwd_hd<32>(q, k, v, top_idx, top_gates, out, lse, d, st); break;
+    case 64: fwd_hd<64>(q, k, v, top_idx, top_gates, out, lse, d, st); break;
+    case 128: fwd_hd<128>(q, k, v, top_idx, top_gates, out, lse, d, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

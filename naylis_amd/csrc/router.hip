@@ -11,8 +11,8 @@
 // which is exactly what the CPU reference's torch.cumsum produces for fp32
 // input; the divide is IEEE fp32 (correctly rounded), so h is bit-exact.
 //
-// Launch plan: (1) per 64-token chunk fp64 column sums, (2) exclusive carry
-// over chunks, (3) one workgroup per (b, chunk): scan its 64 tokens column by
+// Launch plan: (1) per 32-token chunk fp64 column sums, (2) exclusive carry
+// over chunks, (3) one workgroup per (b, chunk): scan its 32 tokens column by
 // column from the carry, stage h in LDS slab by slab (256 features), and
 // accumulate the rank-R projection z; then tanh, W_up, softmax, top-k.
 //
@@ -27,7 +27,7 @@
 
 namespace naylis {
 
-constexpr int kRouterChunk = 64;  // tokens per scan chunk / workgroup
+constexpr int kRouterChunk = 32;  // tokens per scan chunk / workgroup
 constexpr int kRouterSlab = 256;  // features per LDS slab (one per thread)
 
 template <typename XT>
@@ -44,114 +44,150 @@ __device__ __forceinline__ float load_x32<float>(const float* p) { return *p; }
 template <>
 __device__ __forceinline__ float load_x32<bf16_t>(const bf16_t* p) { return bf16_to_f32(*p); }
 
-// (1) chunk column sums, fp64: csum[b][c][d]
+// (1) chunk column sums, fp64: csum[b][c][d] (exact for bf16 input).
+// Thread = 8 consecutive features (one 16-byte load of bf16, two of fp32).
 template <typename XT>
 __global__ __launch_bounds__(256) void router_chunk_sums_kernel(const XT* __restrict__ x, double* __restrict__ csum,
                                                                 int T, int D, int n_chunks) {
-  const int d = blockIdx.x * 256 + threadIdx.x;
+  const int d = (blockIdx.x * 256 + threadIdx.x) * 8;
   const int c = blockIdx.y;
   const int b = blockIdx.z;
   if (d >= D) return;
   const int t0 = c * kRouterChunk, t1 = min(T, t0 + kRouterChunk);
-  double s = 0.0;
-  for (int t = t0; t < t1; ++t) s += load_x64<XT>(x + ((long)b * T + t) * D + d);
-  csum[((long)b * n_chunks + c) * D + d] = s;
+  double s[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = 0.0;
+  const bool full = d + 8 <= D;
+  for (int t = t0; t < t1; ++t) {
+    const XT* p = x + ((long)b * T + t) * D + d;
+    if (full) {
+      if constexpr (sizeof(XT) == 2) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const bf16_t* e8 = reinterpret_cast<const bf16_t*>(&v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] += (double)bf16_to_f32(e8[e]);
+      } else {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(p);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] += (double)v0[e];
+          s[4 + e] += (double)v1[e];
+        }
+      }
+    } else {
+      for (int e = 0; e < 8; ++e)
+        if (d + e < D) s[e] += load_x64<XT>(p + e);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (d + e < D) csum[((long)b * n_chunks + c) * D + d + e] = s[e];
 }
 
-// (2) exclusive carry over chunks, in place: carry[b][c][d] = sum_{c'<c} csum
+// (2) exclusive carry over chunks, in place: carry[b][c][d] = sum_{c'<c} csum,
+// added in ascending chunk order.  Loads go out 16 at a time so their
+// latencies overlap.
 __global__ __launch_bounds__(256) void router_chunk_carry_kernel(double* __restrict__ csum, int D, int n_chunks) {
   const int d = blockIdx.x * 256 + threadIdx.x;
   const int b = blockIdx.y;
   if (d >= D) return;
   double run = 0.0;
-  for (int c = 0; c < n_chunks; ++c) {
-    double* p = csum + ((long)b * n_chunks + c) * D + d;
-    const double v = *p;
-    *p = run;
-    run += v;
+  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = c0 + i < n_chunks ? csum[((long)b * n_chunks + c0 + i) * D + d] : 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (c0 + i < n_chunks) {
+        csum[((long)b * n_chunks + c0 + i) * D + d] = run;
+        run += v[i];
+      }
   }
 }
 
-// (3) main router kernel, one workgroup per (b, 64-token chunk)
+// (3) main router kernel, one workgroup per (b, kRouterChunk-token chunk).
+// For each 256-feature slab: thread f scans its feature over the chunk from
+// the fp64 carry and writes h[t][f] to LDS; the 4 waves then each take 64 of
+// the slab's features and accumulate z = h W_down^T with fp32 MFMA
+// (v_mfma_f32_32x32x2f32: lane l holds A[l%32][l/32] and B[l/32][l%32]).
+// The 4 per-wave partial z tiles are summed in LDS in a fixed order.
 template <typename XT, int EMAX, int TK>
 __global__ __launch_bounds__(256) void router_fwd_kernel(
     const XT* __restrict__ x, const double* __restrict__ carry, const float* __restrict__ w_down,
     const float* __restrict__ w_up, const float* __restrict__ noise, float noise_scale, float* __restrict__ logits,
     float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_gates,
     float* __restrict__ act, float* __restrict__ h_out, int T, int D, int R, int E, int topk, int n_chunks) {
-  constexpr int CT = kRouterChunk;
-  constexpr int HP = CT + 4;  // pitch of the transposed h slab (floats)
-  __shared__ __attribute__((aligned(16))) float h_lds[kRouterSlab * HP];  // [feature][token]
-  __shared__ __attribute__((aligned(16))) float wd_lds[kRouterSlab * 33];  // [feature][r], r < 32 per pass
-  __shared__ float a_lds[CT * 65];  // tanh activations [token][r], R <= 64
+  constexpr int CT = kRouterChunk;   // 32 tokens: one MFMA row tile
+  constexpr int HP = kRouterSlab + 1;
+  __shared__ float h_lds[CT * HP];                 // [token][feature] of the slab
+  __shared__ float wz_lds[kRouterSlab * 33];       // W_down slab [feature][rank]; then the wave partials of z
+  __shared__ float a_lds[CT * 65];                 // tanh activations [token][rank], R <= 64
+  __shared__ float wu_lds[EMAX * 65];              // W_up [block][rank]
+  float* wd_lds = wz_lds;
+  float (*z_lds)[CT * 33] = reinterpret_cast<float (*)[CT * 33]>(wz_lds);
+  static_assert(4 * CT * 33 <= kRouterSlab * 33, "z partials must fit in the W_down slab buffer");
 
   const int c = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = c * CT;
   const int nt = min(CT, T - t0);
-
-  // GEMM mapping: thread -> 4 tokens x 2 rank outputs (per 32-wide rank pass)
-  const int tq = tid >> 4;         // token quad 0..15
-  const int rp = tid & 15;         // rank pair 0..15
+  for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
 
   for (int r0 = 0; r0 < R; r0 += 32) {
-    float z[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) z[i][0] = z[i][1] = 0.f;
-
+    f32x16 acc = f32x16{};
     for (int d0 = 0; d0 < D; d0 += kRouterSlab) {
       const int d = d0 + tid;
       __syncthreads();
-      // ---- scan this thread's feature column over the chunk (fp64)
+      // ---- scan this thread's feature over the chunk (fp64, rounded once)
       if (d < D) {
         double run = carry[((long)b * n_chunks + c) * D + d];
         const XT* xp = x + ((long)b * T + t0) * D + d;
+        float xv[CT];
+#pragma unroll
+        for (int t = 0; t < CT; ++t) xv[t] = t < nt ? load_x32<XT>(xp + (long)t * D) : 0.f;
+#pragma unroll
         for (int t = 0; t < CT; ++t) {
           float hv = 0.f;
           if (t < nt) {
-            run += load_x64<XT>(xp + (long)t * D);
+            run += (double)xv[t];
             const float cs = (float)run;
             hv = cs / (float)(t0 + t + 1);
             if (h_out != nullptr && r0 == 0) h_out[((long)b * T + t0 + t) * D + d] = hv;
           }
-          h_lds[tid * HP + t] = hv;
+          h_lds[t * HP + tid] = hv;
         }
       } else {
-        for (int t = 0; t < CT; ++t) h_lds[tid * HP + t] = 0.f;
+#pragma unroll
+        for (int t = 0; t < CT; ++t) h_lds[t * HP + tid] = 0.f;
       }
-      // W_down slab for ranks r0 .. r0+31, transposed to [feature][r]
       for (int i = tid; i < kRouterSlab * 32; i += 256) {
-        const int f = i / 32, r = i % 32;
-        float w = 0.f;
-        if (d0 + f < D && r0 + r < R) w = w_down[(long)(r0 + r) * D + d0 + f];
-        wd_lds[f * 33 + r] = w;
+        const int r = i / kRouterSlab, f = i % kRouterSlab;  // consecutive threads: consecutive features
+        wd_lds[f * 33 + r] = (d0 + f < D && r0 + r < R) ? w_down[(long)(r0 + r) * D + d0 + f] : 0.f;
       }
       __syncthreads();
-      // ---- z[tokens][r] += h[tokens][f] * Wd[r][f]
-      const int fmax = min(kRouterSlab, D - d0);
-      for (int f = 0; f < fmax; ++f) {
-        const f32x4 h4 = *reinterpret_cast<const f32x4*>(&h_lds[f * HP + 4 * tq]);
-        const float w0 = wd_lds[f * 33 + 2 * rp];
-        const float w1 = wd_lds[f * 33 + 2 * rp + 1];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          z[i][0] = fmaf(h4[i], w0, z[i][0]);
-          z[i][1] = fmaf(h4[i], w1, z[i][1]);
-        }
+      // ---- z[t][r] += sum_f h[t][f] Wd[r][f] over this wave's 64 features
+      const int fw = wave * 64;
+#pragma unroll 8
+      for (int k = 0; k < 64; k += 2) {
+        const int f = fw + k + (lane >> 5);
+        const float av = h_lds[(lane & 31) * HP + f];
+        const float bv = wd_lds[f * 33 + (lane & 31)];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
       }
     }
-    // ---- tanh, stash activations (global for the backward, LDS for W_up)
+    // ---- sum the 4 wave partials in a fixed order, tanh, stash
+    __syncthreads();  // every wave is done reading the W_down slab
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 4 * tq + i;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = r0 + 2 * rp + j;
-        if (r < R && t < nt) {
-          const float a = tanhf(z[i][j]);
-          act[((long)b * T + t0 + t) * R + r] = a;
-          a_lds[t * 65 + r] = a;
-        }
+    for (int v = 0; v < 16; ++v) z_lds[wave][acc_row(lane >> 5, v) * 33 + (lane & 31)] = acc[v];
+    __syncthreads();
+    for (int i = tid; i < CT * 32; i += 256) {
+      const int t = i >> 5, r = i & 31;
+      const float z = ((z_lds[0][t * 33 + r] + z_lds[1][t * 33 + r]) + z_lds[2][t * 33 + r]) + z_lds[3][t * 33 + r];
+      if (t < nt && r0 + r < R) {
+        const float a = tanhf(z);
+        act[((long)b * T + t0 + t) * R + r0 + r] = a;
+        a_lds[t * 65 + r0 + r] = a;
       }
     }
   }
@@ -166,7 +202,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
       const float a = a_lds[tid * 65 + r];
 #pragma unroll
       for (int e = 0; e < EMAX; ++e)
-        if (e < E) lg[e] = fmaf(a, w_up[(long)e * R + r], lg[e]);
+        if (e < E) lg[e] = fmaf(a, wu_lds[e * 65 + r], lg[e]);
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -234,8 +270,15 @@ __global__ __launch_bounds__(64) void router_bwd_token_kernel(
     float* __restrict__ dwup_part, int T, int R, int E, int topk, long ntok) {
   __shared__ float dl_lds[64 * (EMAX + 1)];
   __shared__ float a_lds[64 * 65];
+  __shared__ float wu_lds[EMAX * 65];
   const long tok = (long)blockIdx.x * 64 + threadIdx.x;
   const bool ok = tok < ntok;
+  for (int i = threadIdx.x; i < E * R; i += 64) wu_lds[(i / R) * 65 + i % R] = w_up[i];
+  for (int i = threadIdx.x; i < 64 * R; i += 64) {
+    const long tk = (long)blockIdx.x * 64 + i / R;
+    a_lds[(i / R) * 65 + i % R] = tk < ntok ? act[tk * R + i % R] : 0.f;
+  }
+  __syncthreads();
   float dl[EMAX];
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) dl[e] = 0.f;
@@ -275,10 +318,9 @@ __global__ __launch_bounds__(64) void router_bwd_token_kernel(
     float da = 0.f;
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
-      if (e < E) da = fmaf(dl[e], w_up[(long)e * R + r], da);
-    const float a = ok ? act[tok * R + r] : 0.f;
+      if (e < E) da = fmaf(dl[e], wu_lds[e * 65 + r], da);
+    const float a = a_lds[threadIdx.x * 65 + r];
     if (ok) w_out[tok * R + r] = da * (1.f - a * a) / denom;
-    a_lds[threadIdx.x * 65 + r] = a;
   }
 #pragma unroll
   for (int e = 0; e < EMAX; ++e) dl_lds[threadIdx.x * (EMAX + 1) + e] = ok ? dl[e] : 0.f;
@@ -292,29 +334,61 @@ __global__ __launch_bounds__(64) void router_bwd_token_kernel(
   }
 }
 
-// Backward (2): reverse inclusive scan over t of w (per b, r), fp64
-// accumulation.  One workgroup per b: 256 threads = 32 ranks x 8 segments.
-__global__ __launch_bounds__(256) void router_bwd_scan_kernel(const float* __restrict__ w, float* __restrict__ wt,
-                                                              int T, int R) {
-  __shared__ double seg_sum[8][33];
-  const int b = blockIdx.x;
-  const int r = threadIdx.x & 31, sgi = threadIdx.x >> 5;
-  const int r_base = blockIdx.y * 32;
-  const int rr = r_base + r;
-  const int seg = (T + 7) / 8;
-  const int ta = sgi * seg, tb = min(T, ta + seg);
+// Backward (2): reverse inclusive scan over t of w (per b, r) with fp64
+// accumulation, in two passes over 64-token chunks: (2a) chunk sums,
+// (2b) suffix carry of the later chunks + in-chunk reverse scan.
+constexpr int kScanChunk = 64;
+
+__global__ __launch_bounds__(256) void router_bwd_chunk_sums_kernel(const float* __restrict__ w,
+                                                                    double* __restrict__ csum, int T, int R,
+                                                                    int n_chunks) {
+  // 256 threads = 32 ranks x 8 token groups of 8
+  __shared__ double part[8][33];
+  const int b = blockIdx.y, c = blockIdx.x, r0 = blockIdx.z * 32;
+  const int r = threadIdx.x & 31, grp = threadIdx.x >> 5;
+  const int rr = r0 + r;
   double s = 0.0;
   if (rr < R)
-    for (int t = ta; t < tb; ++t) s += (double)w[((long)b * T + t) * R + rr];
-  seg_sum[sgi][r] = s;
+    for (int i = 0; i < 8; ++i) {
+      const int t = c * kScanChunk + grp * 8 + i;
+      if (t < T) s += (double)w[((long)b * T + t) * R + rr];
+    }
+  part[grp][r] = s;
   __syncthreads();
-  double carry = 0.0;  // sum of later segments
-  for (int j = sgi + 1; j < 8; ++j) carry += seg_sum[j][r];
+  if (grp == 0 && rr < R) {
+    double tot = 0.0;
+    for (int j = 0; j < 8; ++j) tot += part[j][r];
+    csum[((long)b * n_chunks + c) * R + rr] = tot;
+  }
+}
+
+__global__ __launch_bounds__(256) void router_bwd_scan_kernel(const float* __restrict__ w,
+                                                              const double* __restrict__ csum,
+                                                              float* __restrict__ wt, int T, int R, int n_chunks) {
+  // 256 threads = 32 ranks x 8 token groups of 8; groups scanned in reverse
+  __shared__ double part[8][33];
+  const int b = blockIdx.y, c = blockIdx.x, r0 = blockIdx.z * 32;
+  const int r = threadIdx.x & 31, grp = threadIdx.x >> 5;
+  const int rr = r0 + r;
+  double s = 0.0;
   if (rr < R)
-    for (int t = tb - 1; t >= ta; --t) {
+    for (int i = 0; i < 8; ++i) {
+      const int t = c * kScanChunk + grp * 8 + i;
+      if (t < T) s += (double)w[((long)b * T + t) * R + rr];
+    }
+  part[grp][r] = s;
+  __syncthreads();
+  if (rr >= R) return;
+  double carry = 0.0;
+  for (int cc = c + 1; cc < n_chunks; ++cc) carry += csum[((long)b * n_chunks + cc) * R + rr];
+  for (int j = grp + 1; j < 8; ++j) carry += part[j][r];
+  for (int i = 7; i >= 0; --i) {
+    const int t = c * kScanChunk + grp * 8 + i;
+    if (t < T) {
       carry += (double)w[((long)b * T + t) * R + rr];
       wt[((long)b * T + t) * R + rr] = (float)carry;
     }
+  }
 }
 
 // Backward (3): dx = W~ W_down and per-chunk partials of dW_down = W~^T x.
@@ -344,34 +418,48 @@ __global__ __launch_bounds__(256) void router_bwd_dx_kernel(const XT* __restrict
     acc[r] = 0.f;
   }
   const int nt = (int)(ntok - tok0 < CT ? ntok - tok0 : CT);
-  for (int t = 0; t < nt; ++t) {
-    const long tk = tok0 + t;
-    const float xv = dok ? load_x32<XT>(x + tk * D + d) : 0.f;
-    float s = 0.f;
+  for (int t8 = 0; t8 < nt; t8 += 8) {
+    float xv[8];
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-      const float w = wt_lds[t * RMAX + r];
-      s = fmaf(w, wd[r], s);
-      acc[r] = fmaf(w, xv, acc[r]);
-    }
-    if (dok) {
-      if constexpr (sizeof(XT) == 2)
-        dx[tk * D + d] = f32_to_bf16(s);
-      else
-        dx[tk * D + d] = s;
+    for (int u = 0; u < 8; ++u) xv[u] = (dok && t8 + u < nt) ? load_x32<XT>(x + (tok0 + t8 + u) * D + d) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t8 + u;
+      if (t >= nt) break;
+      const long tk = tok0 + t;
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < RMAX; ++r) {
+        const float w = wt_lds[t * RMAX + r];
+        s = fmaf(w, wd[r], s);
+        acc[r] = fmaf(w, xv[u], acc[r]);
+      }
+      if (dok) {
+        if constexpr (sizeof(XT) == 2)
+          dx[tk * D + d] = f32_to_bf16(s);
+        else
+          dx[tk * D + d] = s;
+      }
     }
   }
   if (dok)
     for (int r = 0; r < R; ++r) dwd_part[((long)blockIdx.x * R + r) * D + d] = acc[r];
 }
 
-// Fixed-order reduction of per-chunk partials: out[i] = sum_c part[c][i]
-__global__ void router_reduce_kernel(const float* __restrict__ part, float* __restrict__ out, long n, int n_parts) {
-  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int c = 0; c < n_parts; ++c) s += part[(long)c * n + i];
-    out[i] = s;
-  }
+// Fixed-order reduction of per-chunk partials: out[i] = sum_c part[c][i].
+// Block = 64 outputs x 4 interleaved partial groups; each group sums its
+// partials in order, then the 4 group sums are added in a fixed order.
+__global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                            long n, int n_parts) {
+  __shared__ float grp_sum[4][64];
+  const int o = threadIdx.x & 63, gq = threadIdx.x >> 6;
+  const long i = (long)blockIdx.x * 64 + o;
+  float s = 0.f;
+  if (i < n)
+    for (int c = gq; c < n_parts; c += 4) s += part[(long)c * n + i];
+  grp_sum[gq][o] = s;
+  __syncthreads();
+  if (gq == 0 && i < n) out[i] = ((grp_sum[0][o] + grp_sum[1][o]) + grp_sum[2][o]) + grp_sum[3][o];
 }
 
 // ---------------------------------------------------------------------------
@@ -388,6 +476,8 @@ RouterWs plan_router_ws(const RouterDims& d) {
   off += a256((size_t)ntok * d.R * 4);
   w.wt = off;
   off += a256((size_t)ntok * d.R * 4);
+  w.scan_csum = off;
+  off += a256((size_t)d.B * ((d.T + kScanChunk - 1) / kScanChunk) * d.R * 8);
   w.dwup_part = off;
   off += a256((size_t)n_tok_blocks * d.E * d.R * 4);
   w.dwd_part = off;
@@ -403,10 +493,13 @@ static void fwd_launch(const void* x, const float* w_down, const float* w_up, co
                        const RouterWs& w, const RouterDims& d, hipStream_t st) {
   const int n_chunks = (d.T + kRouterChunk - 1) / kRouterChunk;
   double* carry = (double*)(ws + w.carry);
-  const int dblk = (d.D + 255) / 256;
+  const int dblk = (d.D + 2047) / 2048;
   NAYLIS_TIMED("router_chunk_sums", st, hipLaunchKernelGGL((router_chunk_sums_kernel<XT>), dim3(dblk, n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
                      d.T, d.D, n_chunks));
-  NAYLIS_TIMED("router_chunk_carry", st, hipLaunchKernelGGL(router_chunk_carry_kernel, dim3(dblk, d.B), dim3(256), 0, st, carry, d.D, n_chunks));
+
+  NAYLIS_TIMED("router_chunk_carry", st,
+               hipLaunchKernelGGL(router_chunk_carry_kernel, dim3((d.D + 255) / 256, d.B), dim3(256), 0, st, carry,
+                                  d.D, n_chunks));
   NAYLIS_TIMED("router_fwd", st, hipLaunchKernelGGL((router_fwd_kernel<XT, EMAX, TK>), dim3(n_chunks, d.B), dim3(256), 0, st, (const XT*)x, carry,
                      w_down, w_up, noise, ns, logits, probs, idx, gates, act, h_out, d.T, d.D, d.R, d.E, d.topk,
                      n_chunks));
@@ -476,9 +569,9 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
   const long nwd = (long)d.R * d.D;
   const long nwu = (long)d.E * d.R;
   if (ntok == 0) {  // no tokens: the weight gradients are zero
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)),
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)),
                        dim3(256), 0, st, dwd_part, dw_down, nwd, 0));
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,
                        0));
     return hipGetLastError();
   }
@@ -490,15 +583,23 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
     bwd_token<32, 8>(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf, dwup_part, d, st);
   else
     bwd_token<64, 8>(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf, dwup_part, d, st);
-  NAYLIS_TIMED("router_bwd_scan", st, hipLaunchKernelGGL(router_bwd_scan_kernel, dim3(d.B, (d.R + 31) / 32), dim3(256), 0, st, wbuf, wt, d.T, d.R));
+  {
+    const int n_sc = (d.T + kScanChunk - 1) / kScanChunk;
+    double* csum = (double*)(base + w.scan_csum);
+    const dim3 grid(n_sc, d.B, (d.R + 31) / 32);
+    NAYLIS_TIMED("router_bwd_scan", st,
+                 hipLaunchKernelGGL(router_bwd_chunk_sums_kernel, grid, dim3(256), 0, st, wbuf, csum, d.T, d.R, n_sc));
+    NAYLIS_TIMED("router_bwd_scan", st,
+                 hipLaunchKernelGGL(router_bwd_scan_kernel, grid, dim3(256), 0, st, wbuf, csum, wt, d.T, d.R, n_sc));
+  }
   if (x_bf16)
     bwd_dx<bf16_t>(x, wt, w_down, dx, dwd_part, d, st);
   else
     bwd_dx<float>(x, wt, w_down, dx, dwd_part, d, st);
   const int n_dx_chunks = (int)((ntok + kDxChunk - 1) / kDxChunk);
-  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 255) / 256 < 4096 ? (nwd + 255) / 256 : 4096)), dim3(256),
+  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)), dim3(256),
                      0, st, dwd_part, dw_down, nwd, n_dx_chunks));
-  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 255) / 256)), dim3(256), 0, st, dwup_part, dw_up, nwu,
+  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,
                      n_tok_blocks));
   return hipGetLastError();
 }

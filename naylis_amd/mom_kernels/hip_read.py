@@ -33,14 +33,10 @@ class MomReadFunction(torch.autograd.Function):
         dev = q_sh.device
         out = torch.empty_like(q_sh)
         lse = torch.empty((B, H, S), device=dev, dtype=torch.float32)
-        nbytes = lib.naylis_mom_read_workspace_bytes(B, S, H, HD, num_blocks, block_size, topk)
-        if nbytes == 0:
-            _lib.check(_lib.NAYLIS_ERR_ARG)
-        ws = _workspace(nbytes, dev)
         with torch.cuda.device(dev):
             rc = lib.naylis_mom_read_fwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
+                out.data_ptr(), lse.data_ptr(), None, 0,
                 B, S, H, HD, num_blocks, block_size, topk, _stream(dev))
         _lib.check(rc)
         ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, out, lse)
@@ -63,6 +59,8 @@ class MomReadFunction(torch.autograd.Function):
         dv = torch.empty_like(v)
         dgates = torch.empty_like(top_gates)
         nbytes = lib.naylis_mom_read_workspace_bytes(B, S, H, HD, num_blocks, block_size, topk)
+        if nbytes == 0:
+            _lib.check(_lib.NAYLIS_ERR_ARG)
         ws = _workspace(nbytes, dev)
         with torch.cuda.device(dev):
             rc = lib.naylis_mom_read_bwd(
