@@ -58,7 +58,7 @@ const char* naylis_mom_last_error(void);
  *                                          log(max(g, 1e-9)) on each selected
  *                                          block (duplicate ids add up)
  *   out      (B, S, H, head_dim) bf16
- *   lse      (B, H, S) fp32                log2-domain log-sum-exp per row,
+ *   lse      (H, B, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
  * Constraints: head_dim a power of two in [16, 128]; 1 <= k <= min(8, E);
  * E <= 1024; L <= 16384.  The forward needs no workspace (pass NULL, 0); the

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     }
   }
   dl = wave_sum_pair(dl);
-  const float lse_t = tok_ok ? lse[((long)b * H + h) * S + s_tok] : 0.f;
+  const float lse_t = tok_ok ? lse[(long)h * B * S + tok] : 0.f;
 
   f32x16 acc_dq[NO];
 #pragma unroll
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     }
     if (g == 0) {
       const long ntok = (long)B * S;
-      delta[((long)b * H + h) * S + s_tok] = dx;
+      delta[(long)h * B * S + tok] = dx;
 #pragma unroll
       for (int t = 0; t < TK; ++t)
         if (t < topk) dlg_part[((long)h * ntok + tok) * topk + t] = dlg[t];
@@ -397,20 +397,25 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   uint4 qreg[PER], dreg[PER];
   int pidx[TK];
   float pg[TK], plse = 0.f, pdl = 0.f;
+  // per-thread constant part of the tile copy: row (token in tile) and column
+  int cp_row[PER], cp_off[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int vi = tid + 512 * r;
+    cp_row[r] = vi < VEC ? vi / (HD / 8) : TT;
+    cp_off[r] = cp_row[r] * D + h * HD + 8 * (vi % (HD / 8));
+  }
   auto load_tile = [&](int tt) {
     const long tok0 = (long)tt * TT;
+    const bf16_t* qb = q + tok0 * D;
+    const bf16_t* db = dout + tok0 * D;
+    const int rows = (int)min((long)TT, ntok - tok0);
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int vi = tid + 512 * r;
       uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
-      if (vi < VEC) {
-        const int row = vi / (HD / 8), c8 = vi % (HD / 8);
-        const long tk = tok0 + row;
-        if (tk < ntok) {
-          const long off = tk * D + (long)h * HD + 8 * c8;
-          qv = *reinterpret_cast<const uint4*>(q + off);
-          dv4 = *reinterpret_cast<const uint4*>(dout + off);
-        }
+      if (cp_row[r] < rows) {
+        qv = *reinterpret_cast<const uint4*>(qb + cp_off[r]);
+        dv4 = *reinterpret_cast<const uint4*>(db + cp_off[r]);
       }
       qreg[r] = qv;
       dreg[r] = dv4;
@@ -423,13 +428,8 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
         pidx[t] = (ok && t < topk) ? top_idx[tk * topk + t] : -1;
         pg[t] = (ok && t < topk) ? top_gates[tk * topk + t] : 1.f;
       }
-      plse = 0.f;
-      pdl = 0.f;
-      if (ok) {
-        const long bb = tk / S, ss = tk % S;
-        plse = lse[(bb * H + h) * S + ss];
-        pdl = delta[(bb * H + h) * S + ss];
-      }
+      plse = ok ? lse[(long)h * ntok + tk] : 0.f;
+      pdl = ok ? delta[(long)h * ntok + tk] : 0.f;
     }
   };
   auto store_tile = [&]() {

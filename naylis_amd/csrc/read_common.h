@@ -8,6 +8,7 @@ namespace naylis {
 constexpr int kMaxTopK = 8;       // selections per token supported in registers
 constexpr int kMaxBlocks = 1024;  // bank blocks (flags live in LDS)
 constexpr int kMaxGroups = 512;   // slot groups of 32 over the whole bank (L <= 16384)
+constexpr int kReadWaves = 8;     // waves (x 32 tokens) per forward / dQ workgroup
 
 // Contiguous logical work ranges land on one XCD: the hardware deals
 // workgroup i to XCD i % 8, so logical id (i % 8) * (G / 8) + i / 8 keeps

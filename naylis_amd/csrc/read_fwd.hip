@@ -7,15 +7,17 @@
 // never materialised: it is one scalar per (token, bank block), folded into
 // the exp2 argument together with the running max.
 //
-// Work decomposition: one workgroup = (b, h, tile of 128 tokens), 4 waves,
-// each wave owns 32 tokens (one MFMA column each).  The tile first marks
-// which bank blocks any of its tokens selects and then walks only those
-// blocks' slot groups (SG slots): S^T = K_g Q^T (slots x tokens, K from LDS,
-// Q^T resident in registers), online softmax per token column, O^T += V_g^T P^T
-// with P^T taken straight from the accumulator registers and V^T read from
-// the natural-layout V tile with the transposing LDS read.  K and V tiles
-// are plain 16-byte copies of the bank rows; the next group's copy is in
-// flight while the current group is computed.
+// Work decomposition: one workgroup = (b, h, 256 tokens), 8 waves, each wave
+// owns 32 tokens (one MFMA column each).  The workgroup walks the slot groups
+// (SG slots) of the bank blocks any of its tokens selects, streaming K and V
+// rows through double-buffered LDS (one barrier per group, the next group's
+// copy in flight during the math); a wave computes a group only when one of
+// its own 32 tokens selects it.  Per group: S^T = K_g Q^T (slots x tokens, K
+// from LDS, Q^T resident in registers), online softmax per token column,
+// O^T += V_g^T P^T with P^T taken straight from the accumulator registers and
+// V^T read from the natural-layout V tile with the transposing LDS read.
+#include <stdlib.h>
+
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
@@ -23,19 +25,23 @@
 namespace naylis {
 
 template <int HD, int SG, bool ALIGNED, int TK>
-__global__ __launch_bounds__(256) void read_fwd_kernel(
+__global__ __launch_bounds__(512) void read_fwd_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
     float* __restrict__ lse, int B, int S, int H, int L, int E, int block_size, int topk, float alpha,
     int n_tiles) {
+  constexpr int NW = kReadWaves;
+  constexpr int NT = 64 * NW;
+  constexpr int TM = 32 * NW;       // tokens per workgroup
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;       // K-steps over features for Q.K^T
   constexpr int NS = SG / 32;       // 32-slot accumulator tiles per group
   constexpr int NO = HDP / 32;      // 32-feature output tiles
   constexpr int PITCH = HDP + 8;    // LDS row pitch (bf16) of the K and V tiles
+  constexpr int TILE = SG * PITCH;
 
-  __shared__ __attribute__((aligned(16))) bf16_t k_lds[SG * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t v_lds[SG * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[2 * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[2 * TILE];
   __shared__ uint8_t flags[kMaxBlocks];
   __shared__ uint16_t groups[kMaxGroups];
   __shared__ int n_active;
@@ -51,18 +57,18 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
   const int wave = tid >> 6;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const int s_tok = tile * 128 + wave * 32 + col;
+  const int s_tok = tile * TM + wave * 32 + col;
   const bool tok_ok = s_tok < S;
   const long tok = (long)b * S + s_tok;
   const int D = H * HD;
 
-  // ---- routing of this lane's token; active-block flags of the tile
+  // ---- routing of this lane's token; active-block flags of the workgroup
   TokenRoute<TK> rt;
   load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
-  for (int e = tid; e < E; e += 256) flags[e] = 0;
+  for (int e = tid; e < E; e += NT) flags[e] = 0;
   if constexpr (HD < 32) {
-    // feature columns HD..31 of the V tile stay zero (V^T rows beyond HD)
-    for (int i = tid; i < SG * PITCH; i += 256) v_lds[i] = 0;
+    // feature columns HD..31 of the V tiles stay zero (V^T rows beyond HD)
+    for (int i = tid; i < 2 * TILE; i += NT) v_lds[i] = 0;
   }
   __syncthreads();
   if (g == 0 && tok_ok) {
@@ -92,16 +98,15 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
   __syncthreads();
   const int n_act = n_active;
 
-  // staging: K and V rows of the group (SG x HD) as 16-byte vectors
+  // staging: K and V rows of a group (SG x HD) as 16-byte vectors
   constexpr int VEC = SG * HD / 8;
-  constexpr int PER = (VEC + 255) / 256;
+  constexpr int PER = (VEC + NT - 1) / NT;
   uint4 kreg[PER], vreg[PER];
-
   auto load_group = [&](int gi) {
     const int s0 = gi * SG;
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int vi = tid + 256 * r;
+      const int vi = tid + NT * r;
       uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
       if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
@@ -115,116 +120,143 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
       vreg[r] = vv;
     }
   };
-  auto store_group = [&]() {
+  auto store_group = [&](int buf) {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int vi = tid + 256 * r;
+      const int vi = tid + NT * r;
       if (vi < VEC) {
         const int srow = vi / (HD / 8), c8 = vi % (HD / 8);
-        *reinterpret_cast<uint4*>(&k_lds[srow * PITCH + 8 * c8]) = kreg[r];
-        *reinterpret_cast<uint4*>(&v_lds[srow * PITCH + 8 * c8]) = vreg[r];
+        *reinterpret_cast<uint4*>(&k_lds[buf * TILE + srow * PITCH + 8 * c8]) = kreg[r];
+        *reinterpret_cast<uint4*>(&v_lds[buf * TILE + srow * PITCH + 8 * c8]) = vreg[r];
       }
     }
   };
 
-  if (n_act > 0) load_group(groups[0]);
+  if (n_act > 0) {
+    load_group(groups[0]);
+    store_group(0);
+  }
+  __syncthreads();
 
   for (int it = 0; it < n_act; ++it) {
     const int gi = groups[it];
-    __syncthreads();  // previous group's LDS reads are done
-    store_group();
-    __syncthreads();
+    const int buf = it & 1;
     if (it + 1 < n_act) load_group(groups[it + 1]);  // in flight during the math below
+    const bf16_t* kt = k_lds + buf * TILE;
+    const bf16_t* vt = v_lds + buf * TILE;
 
-    // ---- S^T = K_g . Q^T  (SG slots x 32 tokens per wave)
-    f32x16 acc_s[NS];
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-      acc_s[i] = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * i + col) * PITCH + 16 * ks + 8 * g]);
-        acc_s[i] = mfma32(a, qf[ks], acc_s[i]);
-      }
-    }
-
-    // ---- online softmax over this group, per token column
-    float m_new = m_run;
+    // does any token of this wave select a block of the group?
+    bool mine = false;
     if constexpr (ALIGNED) {
-      bool sel;
-      const float c2 = route_bias<TK>(rt, (gi * SG) / block_size, topk, sel);
-      float mx = -INFINITY;
+      const int e = (gi * SG) / block_size;
 #pragma unroll
-      for (int i = 0; i < NS; ++i)
+      for (int t = 0; t < TK; ++t) mine |= (t < topk && rt.idx[t] == e);
+    } else {
+      const int b0 = (gi * SG) / block_size, b1 = (min(gi * SG + SG, L) - 1) / block_size;
 #pragma unroll
-        for (int vv = 0; vv < 16; ++vv) mx = fmaxf(mx, acc_s[i][vv]);
-      mx = wave_max_pair(mx);
-      if (sel) m_new = fmaxf(m_run, fmaf(mx, alpha, c2));
-      const float add = sel ? c2 - m_new : -INFINITY;
-      float rs = 0.f;
+      for (int t = 0; t < TK; ++t) mine |= (t < topk && rt.idx[t] >= b0 && rt.idx[t] <= b1);
+    }
+    if (__any(mine)) {
+      // ---- S^T = K_g . Q^T  (SG slots x 32 tokens per wave)
+      f32x16 acc_s[NS];
 #pragma unroll
-      for (int i = 0; i < NS; ++i)
+      for (int i = 0; i < NS; ++i) {
+        acc_s[i] = f32x16{};
 #pragma unroll
-        for (int vv = 0; vv < 16; ++vv) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, add));
-          acc_s[i][vv] = p;
-          rs += p;
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kt[(32 * i + col) * PITCH + 16 * ks + 8 * g]);
+          acc_s[i] = mfma32(a, qf[ks], acc_s[i]);
         }
-      rs = wave_sum_pair(rs);
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run = fmaf(l_run, corr, rs);
-      if (__any(corr != 1.f)) {
+      }
+
+      // ---- online softmax over this group, per token column
+      float m_new = m_run;
+      if constexpr (ALIGNED) {
+        bool sel;
+        const float c2 = route_bias<TK>(rt, (gi * SG) / block_size, topk, sel);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int vv = 0; vv < 16; ++vv) mx = fmaxf(mx, acc_s[i][vv]);
+        mx = wave_max_pair(mx);
+        // Lazy rescaling: the running max only moves when the group's max
+        // exceeds it by more than 8 (log2 units) — p stays <= 2^8, exact in
+        // fp32 and in range for bf16 — or on the token's first selected group
+        // (its accumulators are still zero then), so O is rarely rescaled.
+        if (sel) {
+          const float cand = fmaf(mx, alpha, c2);
+          if (cand > m_run + 8.f) m_new = cand;
+        }
+        const float add = sel ? c2 - m_new : -INFINITY;
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int vv = 0; vv < 16; ++vv) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[i][vv], alpha, add));
+            acc_s[i][vv] = p;
+            rs += p;
+          }
+        rs = wave_sum_pair(rs);
+        const bool moved = m_new != m_run;
+        const float corr = moved ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+        l_run = fmaf(l_run, corr, rs);
+        if (__any(moved && m_run != kNegBig)) {
+#pragma unroll
+          for (int j = 0; j < NO; ++j)
+#pragma unroll
+            for (int vv = 0; vv < 16; ++vv) acc_o[j][vv] *= corr;
+        }
+      } else {
+        // generic slot->block lookup per element (block_size not a multiple of SG)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int vv = 0; vv < 16; ++vv) {
+            const int slot = gi * SG + 32 * i + acc_row(g, vv);
+            bool sel = false;
+            float c2 = 0.f;
+            if (slot < L) c2 = route_bias<TK>(rt, slot / block_size, topk, sel);
+            const float t = sel ? fmaf(acc_s[i][vv], alpha, c2) : -INFINITY;
+            acc_s[i][vv] = t;
+            mx = fmaxf(mx, t);
+          }
+        mx = wave_max_pair(mx);
+        m_new = fmaxf(m_run, mx);
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int vv = 0; vv < 16; ++vv) {
+            const float p = __builtin_amdgcn_exp2f(acc_s[i][vv] - m_new);
+            acc_s[i][vv] = p;
+            rs += p;
+          }
+        rs = wave_sum_pair(rs);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run = fmaf(l_run, corr, rs);
 #pragma unroll
         for (int j = 0; j < NO; ++j)
 #pragma unroll
           for (int vv = 0; vv < 16; ++vv) acc_o[j][vv] *= corr;
       }
-    } else {
-      // generic slot->block lookup per element (block_size not a multiple of SG)
-      float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < NS; ++i)
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) {
-          const int slot = gi * SG + 32 * i + acc_row(g, vv);
-          bool sel = false;
-          float c2 = 0.f;
-          if (slot < L) c2 = route_bias<TK>(rt, slot / block_size, topk, sel);
-          const float t = sel ? fmaf(acc_s[i][vv], alpha, c2) : -INFINITY;
-          acc_s[i][vv] = t;
-          mx = fmaxf(mx, t);
-        }
-      mx = wave_max_pair(mx);
-      m_new = fmaxf(m_run, mx);
-      float rs = 0.f;
-#pragma unroll
-      for (int i = 0; i < NS; ++i)
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) {
-          const float p = __builtin_amdgcn_exp2f(acc_s[i][vv] - m_new);
-          acc_s[i][vv] = p;
-          rs += p;
-        }
-      rs = wave_sum_pair(rs);
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run = fmaf(l_run, corr, rs);
-#pragma unroll
-      for (int j = 0; j < NO; ++j)
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) acc_o[j][vv] *= corr;
-    }
-    m_run = m_new;
+      m_run = m_new;
 
-    // ---- O^T += V_g^T . P^T   (P^T fragments come straight from acc_s)
+      // ---- O^T += V_g^T . P^T   (P^T fragments come straight from acc_s)
 #pragma unroll
-    for (int kk = 0; kk < SG / 16; ++kk) {
-      const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
+      for (int kk = 0; kk < SG / 16; ++kk) {
+        const bf16x8 bp = pack8(acc_s[kk >> 1], 8 * (kk & 1));
 #pragma unroll
-      for (int j = 0; j < NO; ++j) {
-        const bf16x8 a = lds_frag_T<true, true>(v_lds, PITCH, 16 * kk, 32 * j);
-        acc_o[j] = mfma32(a, bp, acc_o[j]);
+        for (int j = 0; j < NO; ++j) {
+          const bf16x8 a = lds_frag_T<true, true>(vt, PITCH, 16 * kk, 32 * j);
+          acc_o[j] = mfma32(a, bp, acc_o[j]);
+        }
       }
     }
+    if (it + 1 < n_act) store_group(buf ^ 1);  // that buffer was last read before the previous barrier
+    __syncthreads();
   }
 
   // ---- epilogue: normalise, store o (bf16) and the log2-domain lse
@@ -245,7 +277,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
         *reinterpret_cast<bf16x8*>(dst + 8) = hi;
       }
     }
-    if (g == 0) lse[((long)b * H + h) * S + s_tok] = m_run + log2f(l_run);
+    if (g == 0) lse[(long)h * B * S + tok] = m_run + log2f(l_run);
   }
 }
 
@@ -253,19 +285,32 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(
 template <int HD, int SG, bool AL, int TK>
 static void fwd_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                      float* lse, const ReadDims& d, hipStream_t st) {
-  const int n_tiles = (d.S + 127) / 128;
+  const int n_tiles = (d.S + 32 * kReadWaves - 1) / (32 * kReadWaves);
   const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+               hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(64 * kReadWaves), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (bf16_t*)out, lse,
                                   d.B, d.S, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
+}
+
+// Slot-group size of the forward: NAYLIS_READ_FWD_SG=128 selects 128-slot
+// groups instead of the default 64 (read once per process; a tuning knob like
+// the reference's NAYLIS_TRITON_BLOCK_N, mom_kernels/triton_gpu.py:48-55).
+static int fwd_sg_override() {
+  static const int v = [] {
+    const char* e = getenv("NAYLIS_READ_FWD_SG");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
 }
 
 template <int HD, int TK>
 static void fwd_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                     float* lse, const ReadDims& d, hipStream_t st) {
-  constexpr int SGMAX = HD <= 64 ? 128 : 64;
-  if (d.block_size % SGMAX == 0)
+  constexpr int SGMAX = 64;  // measured faster than 128 on MI355X (fewer registers, 2 workgroups per CU)
+  if (fwd_sg_override() == 128 && HD <= 64 && d.block_size % 128 == 0)
+    fwd_inst<HD, (HD <= 64 ? 128 : 64), true, TK>(q, k, v, ti, tg, out, lse, d, st);
+  else if (d.block_size % SGMAX == 0)
     fwd_inst<HD, SGMAX, true, TK>(q, k, v, ti, tg, out, lse, d, st);
   else if (d.block_size % 64 == 0)
     fwd_inst<HD, 64, true, TK>(q, k, v, ti, tg, out, lse, d, st);

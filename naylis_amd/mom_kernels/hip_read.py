@@ -32,7 +32,7 @@ class MomReadFunction(torch.autograd.Function):
         topk = top_idx.shape[-1]
         dev = q_sh.device
         out = torch.empty_like(q_sh)
-        lse = torch.empty((B, H, S), device=dev, dtype=torch.float32)
+        lse = torch.empty((H, B, S), device=dev, dtype=torch.float32)
         with torch.cuda.device(dev):
             rc = lib.naylis_mom_read_fwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),

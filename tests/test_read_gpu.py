@@ -122,7 +122,9 @@ def test_read_empty_sequence(dev):
 
 def test_read_single_block_gate_independence(dev):
     """A token whose k selections all name one block attends to that block
-    alone, whatever the gate values (the bias is constant over the block)."""
+    alone, whatever the gate values (the bias is constant over the block).
+    The gate enters the exp2 argument through two fp32 roundings, so the two
+    outputs agree to one bf16 ulp rather than bitwise."""
     from naylis_amd import mom_kernels
     B, S, H, HD, NB, BS = 1, 128, 2, 64, 4, 64
     q, k, v, _, gates, _ = make_inputs(B, S, H, HD, NB, BS, 2, "random")
@@ -132,7 +134,7 @@ def test_read_single_block_gate_independence(dev):
                               num_blocks=NB, block_size=BS, mode="hip")
     o2 = mom_kernels.mom_read(q.to(dev), k.to(dev), v.to(dev), top.to(dev), g2.to(dev),
                               num_blocks=NB, block_size=BS, mode="hip")
-    assert torch.equal(o1, o2)
+    assert torch.allclose(o1.float(), o2.float(), rtol=2.0 ** -7, atol=1e-6)
 
 
 def test_read_full_config2_vs_torch_fp32(dev):
