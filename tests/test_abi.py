@@ -1,0 +1,152 @@
+"""CPU checks of the C-ABI library (no GPU calls): it loads, exports every
+function include/naylis_mom.h declares, and rejects bad arguments with the
+reference's fail-loud rules (mom_kernels/triton_gpu.py:420-429,
+mom_kernels/__init__.py:69-79) as status codes — before touching a device.
+Also the Python-side contracts of resolve_mode / preflight / mom_read
+(tests/test_parity.py §7-8) and the layer constructor (model.py:125-133).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from naylis_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "naylis_mom.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(naylis_mom_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), f"{n} declared in include/naylis_mom.h but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_abi_version(lib):
+    assert lib.naylis_mom_abi_version() == _lib.ABI_VERSION
+
+
+READ_OK = dict(B=2, S=64, H=2, hd=16, nb=4, bs=16, k=2)
+
+
+def read_fwd(lib, **kw):
+    a = dict(READ_OK, **kw)
+    return lib.naylis_mom_read_fwd(1, 1, 1, 1, 1, 1, 1, None, 0, a["B"], a["S"], a["H"], a["hd"], a["nb"], a["bs"],
+                                   a["k"], None)
+
+
+@pytest.mark.parametrize("bad", [dict(hd=96), dict(hd=256), dict(hd=8), dict(k=0), dict(k=9), dict(k=5, nb=4),
+                                 dict(nb=0), dict(bs=0), dict(nb=2048), dict(B=-1), dict(H=0)])
+def test_read_rejects_bad_arguments(lib, bad):
+    rc = read_fwd(lib, **bad)
+    assert rc == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_last_error()
+    assert lib.naylis_mom_read_workspace_bytes(*[dict(READ_OK, **bad)[n] for n in ("B", "S", "H", "hd", "nb", "bs",
+                                                                                     "k")]) == 0
+
+
+def test_read_null_pointers_and_workspace(lib):
+    rc = lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, 0, 2, 64, 2, 16, 4, 16, 2, None)
+    assert rc == _lib.NAYLIS_ERR_ARG and b"null" in lib.naylis_mom_last_error()
+    ws = lib.naylis_mom_read_workspace_bytes(8, 2048, 16, 64, 8, 128, 2)
+    assert ws > 0
+    rc = lib.naylis_mom_read_bwd(*([1] * 12), 1, ws - 1, 8, 2048, 16, 64, 8, 128, 2, None)
+    assert rc == _lib.NAYLIS_ERR_WORKSPACE
+    # empty sequences are a valid no-op for the forward
+    assert lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, 0, 2, 0, 2, 16, 4, 16, 2,
+                                   None) == _lib.NAYLIS_OK
+
+
+def test_router_and_bank_reject_bad_arguments(lib):
+    assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 65, 8, 2) == 0     # rank > 64
+    assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 65, 2) == 0     # blocks > 64
+    assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 4, 5) == 0      # top_k > blocks
+    assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 4, 2) > 0
+    rc = lib.naylis_mom_router_fwd(1, 7, 1, 1, None, 1.0, 1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 64, 32, 8, 4, 2, None)
+    assert rc == _lib.NAYLIS_ERR_ARG                                           # unknown dtype code
+    assert lib.naylis_mom_bank_kv_fwd(1, 1, 1, 1, 1, 64, 30, 32, None) == _lib.NAYLIS_ERR_ARG   # D_in % 8
+    assert lib.naylis_mom_bank_kv_fwd(None, None, None, None, None, 0, 32, 32, None) == _lib.NAYLIS_OK
+    assert lib.naylis_mom_bank_kv_bwd(1, 1, 1, 1, 1, 1, 9, 1, 1, 0, 64, 32, 32, None) == _lib.NAYLIS_ERR_ARG
+
+
+def test_error_message_is_per_thread(lib):
+    import threading
+    read_fwd(lib, hd=96)
+    msgs = {}
+
+    def other():
+        read_fwd(lib, k=0)
+        msgs["t"] = lib.naylis_mom_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert b"head_dim" in lib.naylis_mom_last_error()
+    assert b"top_k" in msgs["t"]
+
+
+# ------------------------------------------------------- python contracts
+def test_resolve_mode_contract():
+    from naylis_amd import mom_kernels
+    with pytest.raises(RuntimeError):
+        mom_kernels.resolve_mode(torch.device("cpu"), torch.float32)               # §7a
+    with pytest.raises(RuntimeError):
+        mom_kernels.resolve_mode("cuda", torch.float32, head_dim=64)               # §7b
+    with pytest.raises(RuntimeError):
+        mom_kernels.resolve_mode("cuda", torch.bfloat16, head_dim=96)              # §7c
+    with pytest.raises(RuntimeError):
+        mom_kernels.resolve_mode("xla", torch.float32, head_dim=64)                # no XLA backend here
+    if torch.version.hip is not None and _lib.available():
+        assert mom_kernels.resolve_mode("cuda", torch.bfloat16, head_dim=64) == "hip"   # §7d
+    with pytest.raises(RuntimeError):
+        mom_kernels.preflight("cpu")                                             # §8a
+    with pytest.raises(RuntimeError):
+        mom_kernels.mom_read(None, None, None, None, None, num_blocks=1, block_size=1, mode="triton")
+
+
+def test_mom_read_preconditions_raise_before_device_work():
+    from naylis_amd import mom_kernels
+    q = torch.zeros(2, 8, 2, 16, dtype=torch.bfloat16)
+    k = torch.zeros(64, 32, dtype=torch.bfloat16)
+    top = torch.zeros(2, 8, 2, dtype=torch.long)
+    g = torch.full((2, 8, 2), 0.5)
+    with pytest.raises(RuntimeError, match="shared K/V"):
+        mom_kernels.mom_read(q, k.unsqueeze(0), k, top, g, num_blocks=4, block_size=16, mode="hip")
+    with pytest.raises(RuntimeError, match="bf16"):
+        mom_kernels.mom_read(q.float(), k, k, top, g, num_blocks=4, block_size=16, mode="hip")
+    with pytest.raises(RuntimeError, match="slots"):
+        mom_kernels.mom_read(q, k, k, top, g, num_blocks=3, block_size=16, mode="hip")
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mom_kernels.mom_read(q, k, k, top, g, num_blocks=4, block_size=16, mode="hip")
+
+
+def test_layer_constructor_contract():
+    from naylis_amd.layer import MoMLayer
+    with pytest.raises(ValueError):
+        MoMLayer(d_model=30, n_heads=4, mem_size=64, block_size=16, top_blocks=2, router_rank=8)
+    with pytest.raises(ValueError):
+        MoMLayer(d_model=32, n_heads=2, mem_size=60, block_size=16, top_blocks=2, router_rank=8)
+    with pytest.raises(ValueError):
+        MoMLayer(d_model=32, n_heads=2, mem_size=64, block_size=16, top_blocks=5, router_rank=8)
+    layer = MoMLayer(d_model=32, n_heads=2, mem_size=64, block_size=16, top_blocks=2, router_rank=8)
+    names = {n for n, _ in layer.named_parameters()}
+    assert names == {"router_down.weight", "router_up.weight", "q_proj.weight", "k_proj.weight", "v_proj.weight",
+                     "o_proj.weight", "mom_scale"}                               # checkpoint-compatible names
+    with pytest.raises(RuntimeError):
+        layer(torch.zeros(1, 4, 32), torch.zeros(4, 16 * 32))                   # CPU tensors: no fallback
