@@ -287,3 +287,25 @@ def test_active_tile_blocks_brute_force():
         for t0 in range(0, 300, 128):
             want += len({int(e) for e in top[b, t0:t0 + 128].flatten()})
     assert oracle.active_tile_blocks(top, 6, 128) == want
+
+
+def test_decode_step_equals_full_sequence_rows():
+    """Stepping the running prefix-sum state token by token gives, at every
+    position, the router decision and read output of the full-sequence
+    oracle (model.py:172-173 vs the O(1) decode form)."""
+    g = torch.Generator().manual_seed(13)
+    B, S, H, HD, NB, BS, K, R = 2, 24, 2, 16, 4, 16, 2, 8
+    D = H * HD
+    x = torch.randn(B, S, D, generator=g)
+    wd, wu = torch.randn(R, D, generator=g) * 0.3, torch.randn(NB, R, generator=g)
+    q = torch.randn(B, S, H, HD, generator=g)
+    k, v = torch.randn(NB * BS, D, generator=g), torch.randn(NB * BS, D, generator=g)
+    _, _, idx_full, gates_full, _ = oracle.router(x, wd, wu, K)
+    out_full = oracle.mom_read(q, k, v, idx_full, gates_full, num_blocks=NB, block_size=BS)
+    state = torch.zeros(B, D, dtype=torch.float64)
+    for t in range(S):
+        tp = torch.full((B,), t, dtype=torch.int64)
+        out, state, idx, gates = oracle.decode_step(state, tp, x[:, t], wd, wu, K, q[:, t], k, v, NB, BS)
+        assert torch.equal(idx, idx_full[:, t])
+        torch.testing.assert_close(gates, gates_full[:, t], rtol=0, atol=0)
+        torch.testing.assert_close(out, out_full[:, t].float(), rtol=1e-5, atol=1e-6)
