@@ -165,6 +165,9 @@ def main(argv=None):
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=2)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the timed region, run 3 plain device copies of this many MiB (a known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
@@ -241,6 +244,14 @@ def main(argv=None):
                  "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
     }
+    if args.copy_probe_mib > 0:
+        src = torch.ones(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_probe_bytes"] = src.numel()
+        del src, dst
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_sample_batch)
     print(json.dumps(line), flush=True)
