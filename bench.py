@@ -200,7 +200,11 @@ def main(argv=None):
     idx = routing(layer, M, x)
     A = active_tiles(idx, E)
     unit = 2.0 * D * BS * 128 * A          # FLOP of one GEMM-shaped product
-    alg = {"read_fwd": 2 * unit, "read_bwd_dq": 3 * unit, "read_bwd_dkdv": 4 * unit}
+    L = E * BS
+    alg = {"read_fwd": 2 * unit, "read_bwd_dq": 3 * unit, "read_bwd_dkdv": 4 * unit,
+           # GEMMs: 2 flop per multiply-add; bank K/V (two products), d_slots, dW_k/dW_v; q/o weight grads
+           "bank_kv_fwd": 2 * 2.0 * L * D * D, "bank_kv_bwd_dslots": 2.0 * L * 2 * D * D,
+           "bank_kv_bwd_dw": 2 * 2.0 * D * D * L, "linear_wgrad": 2.0 * ntok * D * D}
     per = {k: (v[0] / v[1], v[1] / args.steps) for k, v in kernels.items() if v[1]}  # avg ms, launches/step
     dominant = max(kernels, key=lambda k: kernels[k][0])
     dom_ms = per[dominant][0]

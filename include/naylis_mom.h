@@ -140,6 +140,22 @@ int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, 
                            void* d_slots, int slots_grad_dtype, void* dw_k, void* dw_v, int w_grad_dtype, int64_t L,
                            int64_t D_in, int64_t D_out, void* stream);
 
+/* ------------------------------------------------- projection weight grad ---
+ * Weight gradient of the layer's bias-free query / output projections
+ * (model.py:239 `q_proj`, model.py:251 `o_proj`, both nn.Linear(d, d,
+ * bias=False)), which the reference gets from autograd as dy^T x summed over
+ * all B*T tokens:
+ *   dw[o][i] = sum_t dy[t][o] * x[t][i]      (fp32 accumulation)
+ *   x  (N, D_in) bf16, dy (N, D_out) bf16, dw (D_out, D_in) in dw_dtype.
+ * The token reduction is split over workgroups; the fp32 partials live in the
+ * caller's workspace (naylis_mom_linear_wgrad_workspace_bytes) and are summed
+ * in a fixed order, so the result is deterministic.
+ * Constraints: N, D_in, D_out multiples of 8; pointers 16-byte aligned;
+ * N * max(D_in, D_out) below 2^30. */
+size_t naylis_mom_linear_wgrad_workspace_bytes(int64_t N, int64_t D_in, int64_t D_out);
+int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtype, void* workspace,
+                            size_t workspace_bytes, int64_t N, int64_t D_in, int64_t D_out, void* stream);
+
 /* -------------------------------------------------------------- timing ---
  * Optional instrumentation (no counterpart in the reference; for benchmarks):
  * when enabled, each kernel launch of this library is bracketed by hipEvents

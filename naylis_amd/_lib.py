@@ -39,6 +39,8 @@ SIGNATURES = {
     "naylis_mom_router_bwd": (_int, [_c_void_p, _int] + [_c_void_p] * 12 + [_c_void_p, _size_t] + [_i64] * 6
                               + [_c_void_p]),
     "naylis_mom_bank_kv_fwd": (_int, [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p]),
+    "naylis_mom_linear_wgrad_workspace_bytes": (_size_t, [_i64] * 3),
+    "naylis_mom_linear_wgrad": (_int, [_c_void_p] * 3 + [_int, _c_void_p, _size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
     "naylis_mom_timing_enable": (None, [_int]),

@@ -14,6 +14,7 @@
 #include "common.h"
 #include "timing.h"
 #include "launch_bank.h"
+#include "launch_gemm.h"
 
 namespace naylis {
 
@@ -118,6 +119,21 @@ __global__ __launch_bounds__(256) void bank_gemm_kernel(GemmBatch batch, int M, 
 // ---------------------------------------------------------------------------
 hipError_t launch_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, void* k_out, void* v_out, int L,
                               int D_in, int D_out, hipStream_t st) {
+  GemmLaunch g{};
+  g.njobs = 2;
+  g.M = L;
+  g.N = D_out;
+  g.K = g.K1 = D_in;
+  g.out = kGemmOutBF16;
+  g.splits = 1;
+  for (int z = 0; z < 2; ++z) {
+    g.job[z].a = GemmOp{slots, nullptr, D_in, true};                   // A(l, i) = slots[l][i]
+    g.job[z].b = GemmOp{z == 0 ? w_k : w_v, nullptr, D_in, true};      // B(i, o) = W[o][i]
+    g.job[z].c = z == 0 ? k_out : v_out;
+    g.job[z].ldc = D_out;
+  }
+  if (gemm_supported(g)) return launch_gemm(g, "bank_kv_fwd", st);
+  // small or unaligned shapes: the simple 64 x 64 tile kernel
   GemmBatch bt{};
   for (int z = 0; z < 2; ++z) {
     GemmProblem& P = bt.prob[z];
@@ -136,16 +152,47 @@ hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_
                               void* d_slots, bool slots_f32, void* dw_k, void* dw_v, bool w_f32, int L, int D_in,
                               int D_out, hipStream_t st) {
   // d_slots (L x D_in) = [dK | dV] (L x 2D_out) . [W_k ; W_v] (2D_out x D_in)
+  GemmLaunch g1{};
+  g1.njobs = 1;
+  g1.M = L;
+  g1.N = D_in;
+  g1.K = 2 * D_out;
+  g1.K1 = D_out;
+  g1.out = slots_f32 ? kGemmOutF32 : kGemmOutBF16;
+  g1.splits = 1;
+  g1.job[0].a = GemmOp{dk, dv, D_out, true};      // A(l, o) = [dK | dV][l][o]
+  g1.job[0].b = GemmOp{w_k, w_v, D_in, false};    // B(o, i) = [W_k ; W_v][o][i]
+  g1.job[0].c = d_slots;
+  g1.job[0].ldc = D_in;
+  // dW (D_out x D_in) = dK^T (D_out x L) . slots (L x D_in)
+  GemmLaunch g2{};
+  g2.njobs = 2;
+  g2.M = D_out;
+  g2.N = D_in;
+  g2.K = g2.K1 = L;
+  g2.out = w_f32 ? kGemmOutF32 : kGemmOutBF16;
+  g2.splits = 1;
+  for (int z = 0; z < 2; ++z) {
+    g2.job[z].a = GemmOp{z == 0 ? dk : dv, nullptr, D_out, false};   // A(o, l) = dK[l][o]
+    g2.job[z].b = GemmOp{slots, nullptr, D_in, false};               // B(l, i) = slots[l][i]
+    g2.job[z].c = z == 0 ? dw_k : dw_v;
+    g2.job[z].ldc = D_in;
+  }
+  if (gemm_supported(g1) && gemm_supported(g2)) {
+    hipError_t e = launch_gemm(g1, "bank_kv_bwd_dslots", st);
+    if (e != hipSuccess) return e;
+    return launch_gemm(g2, "bank_kv_bwd_dw", st);
+  }
   GemmBatch b1{};
   b1.prob[0].a = {(const bf16_t*)dk, (const bf16_t*)dv, D_out};      // A(m=l, k=o): K-major
   b1.prob[0].b = {(const bf16_t*)w_k, (const bf16_t*)w_v, D_in};     // B(k=o, n=j) = W[o][j]: N-contiguous
   b1.prob[0].c = d_slots;
   b1.prob[0].ldc = D_in;
-  const dim3 g1((D_in + GBN - 1) / GBN, (L + GBM - 1) / GBM, 1);
+  const dim3 grid1((D_in + GBN - 1) / GBN, (L + GBM - 1) / GBM, 1);
   if (slots_f32)
-    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, true>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
+    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, true>), grid1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
   else
-    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, false>), g1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
+    NAYLIS_TIMED("bank_kv_bwd_dslots", st, hipLaunchKernelGGL((bank_gemm_kernel<true, false, false>), grid1, dim3(256), 0, st, b1, L, D_in, 2 * D_out, D_out));
   // dW (D_out x D_in) = dK^T (D_out x L) . slots (L x D_in)
   GemmBatch b2{};
   for (int z = 0; z < 2; ++z) {
@@ -156,11 +203,11 @@ hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_
     P.c = z == 0 ? dw_k : dw_v;
     P.ldc = D_in;
   }
-  const dim3 g2((D_in + GBN - 1) / GBN, (D_out + GBM - 1) / GBM, 2);
+  const dim3 grid2((D_in + GBN - 1) / GBN, (D_out + GBM - 1) / GBM, 2);
   if (w_f32)
-    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, true>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L));
+    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, true>), grid2, dim3(256), 0, st, b2, D_out, D_in, L, L));
   else
-    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, false>), g2, dim3(256), 0, st, b2, D_out, D_in, L, L));
+    NAYLIS_TIMED("bank_kv_bwd_dw", st, hipLaunchKernelGGL((bank_gemm_kernel<false, false, false>), grid2, dim3(256), 0, st, b2, D_out, D_in, L, L));
   return hipGetLastError();
 }
 

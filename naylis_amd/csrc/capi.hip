@@ -5,6 +5,7 @@
 // The library holds no tensors and no mutable global state; the last error
 // message is per calling thread (like errno).
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -14,6 +15,7 @@
 #include "launch.h"
 #include "launch_router.h"
 #include "launch_bank.h"
+#include "launch_gemm.h"
 
 using namespace naylis;
 
@@ -115,8 +117,8 @@ int check_router_dims(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int
   if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > E)
     return fail(NAYLIS_ERR_ARG, "mom_route: top_k %lld must be in [1, min(%d, num_blocks=%lld)]", (long long)top_k,
                 NAYLIS_MAX_TOPK, (long long)E);
-  if (B * T > ((int64_t)1 << 30) || D > (1 << 20))
-    return fail(NAYLIS_ERR_ARG, "mom_route: problem too large");
+  if (B * T > ((int64_t)1 << 30) || D > (1 << 20) || T > (1 << 24))
+    return fail(NAYLIS_ERR_ARG, "mom_route: problem too large (B*T <= 2^30, D <= 2^20, T <= 2^24)");
   d->B = (int)B;
   d->T = (int)T;
   d->D = (int)D;
@@ -282,6 +284,65 @@ int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, 
                                        dw_v, w_grad_dtype == NAYLIS_DTYPE_F32, (int)L, (int)D_in, (int)D_out,
                                        (hipStream_t)stream),
                     "mom_bank_kv_bwd");
+}
+
+// ---------------------------------------------------- projection weight grad
+static int wgrad_splits(int64_t N, int64_t D_in, int64_t D_out) {
+  // enough workgroups for two per CU, each reducing at least 1024 tokens
+  const int64_t tiles = ((D_out + 127) / 128) * ((D_in + 127) / 128);
+  int64_t s = (512 + tiles - 1) / tiles;
+  const int64_t smax = N / 1024 > 1 ? N / 1024 : 1;
+  if (s > smax) s = smax;
+  if (s > 64) s = 64;
+  return (int)(s < 1 ? 1 : s);
+}
+
+static int check_wgrad_dims(int64_t N, int64_t D_in, int64_t D_out) {
+  if (N < 0 || D_in <= 0 || D_out <= 0 || N > ((int64_t)1 << 30) || D_in > 65536 || D_out > 65536)
+    return fail(NAYLIS_ERR_ARG, "linear_wgrad: bad shape N=%lld D_in=%lld D_out=%lld", (long long)N, (long long)D_in,
+                (long long)D_out);
+  if (N % 8 || D_in % 8 || D_out % 8)
+    return fail(NAYLIS_ERR_ARG, "linear_wgrad: N (%lld), D_in (%lld) and D_out (%lld) must be multiples of 8",
+                (long long)N, (long long)D_in, (long long)D_out);
+  return NAYLIS_OK;
+}
+
+size_t naylis_mom_linear_wgrad_workspace_bytes(int64_t N, int64_t D_in, int64_t D_out) {
+  if (check_wgrad_dims(N, D_in, D_out) != NAYLIS_OK) return 0;
+  const size_t b = gemm_ws_bytes(1, (int)D_out, (int)D_in, wgrad_splits(N, D_in, D_out));
+  return b ? b : 256;
+}
+
+int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtype, void* workspace,
+                            size_t workspace_bytes, int64_t N, int64_t D_in, int64_t D_out, void* stream) {
+  int rc = check_wgrad_dims(N, D_in, D_out);
+  if (rc) return rc;
+  if ((rc = check_dtype(dw_dtype, "linear_wgrad"))) return rc;
+  if (!dw || (N > 0 && (!x || !dy))) return fail(NAYLIS_ERR_ARG, "linear_wgrad: null pointer argument");
+  const int splits = wgrad_splits(N, D_in, D_out);
+  const size_t need = gemm_ws_bytes(1, (int)D_out, (int)D_in, splits);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(NAYLIS_ERR_WORKSPACE, "linear_wgrad: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  if (N == 0)  // no tokens: the gradient is zero
+    return hip_status(hipMemsetAsync(dw, 0, (size_t)D_out * D_in * (dw_dtype == NAYLIS_DTYPE_F32 ? 4 : 2),
+                                     (hipStream_t)stream),
+                      "linear_wgrad");
+  GemmLaunch g{};
+  g.njobs = 1;
+  g.M = (int)D_out;
+  g.N = (int)D_in;
+  g.K = g.K1 = (int)N;
+  g.out = dw_dtype == NAYLIS_DTYPE_F32 ? kGemmOutF32 : kGemmOutBF16;
+  g.splits = splits;
+  g.ws = workspace;
+  g.job[0].a = GemmOp{dy, nullptr, D_out, false};  // A(o, t) = dy[t][o]
+  g.job[0].b = GemmOp{x, nullptr, D_in, false};    // B(t, i) = x[t][i]
+  g.job[0].c = dw;
+  g.job[0].ldc = D_in;
+  if (!gemm_supported(g))
+    return fail(NAYLIS_ERR_ARG, "linear_wgrad: needs 16-byte aligned pointers and N * max(D_in, D_out) < 2^30");
+  return hip_status(launch_gemm(g, "linear_wgrad", (hipStream_t)stream), "linear_wgrad");
 }
 
 }  // extern "C"

@@ -51,6 +51,13 @@ __host__ __device__ constexpr int row_unperm32(int f) {
 // Row of the 32x32 accumulator held by (lane group g, register v).
 __device__ __forceinline__ int acc_row(int g, int v) { return 8 * (v >> 2) + 4 * g + (v & 3); }
 
+// Raw buffer resource over [base, base + bytes): buffer loads take a per-lane
+// VGPR byte offset plus a wave-uniform SGPR byte offset, so a run of loads at
+// uniform strides needs no per-load 64-bit address registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 __device__ __forceinline__ float bf16_to_f32(bf16_t u) {
   return __uint_as_float(((uint32_t)u) << 16);
 }
@@ -95,6 +102,14 @@ __device__ __forceinline__ bf16x8 lds_frag_T(const bf16_t* tile, int pitch, int 
   typedef short v8i16 __attribute__((ext_vector_type(8)));
   const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);
+}
+
+// Contiguous logical work ranges land on one XCD: the hardware deals
+// workgroup i to XCD i % 8, so logical id (i % 8) * (G / 8) + i / 8 keeps
+// neighbouring logical ids (the same operand working set) in one L2.
+__device__ __forceinline__ int xcd_remap(int i, int G) {
+  if (G & 7) return i;
+  return (i & 7) * (G >> 3) + (i >> 3);
 }
 
 __device__ __forceinline__ float wave_max_pair(float x) {

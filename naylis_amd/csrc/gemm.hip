@@ -1,0 +1,359 @@
+// General bf16 GEMM for gfx950 on v_mfma_f32_32x32x16_bf16, fp32 accumulate:
+//     C(m, n) = sum_k A(m, k) B(k, n)
+// Used for the bank K/V projection and its gradients (model.py:253-256) and
+// for the weight gradients of the layer's q/o projections (model.py:239,251),
+// whose reduction runs over all tokens.
+//
+// Workgroup tile 128 x 128, K step 64; 4 waves in 2 x 2, each wave 64 x 64 =
+// 2 x 2 MFMA tiles.  Each operand is staged into LDS in its global layout by
+// plain 16-byte copies: a K-contiguous operand as [row][k] (an MFMA fragment
+// is one 16-byte LDS read), an M- or N-contiguous one as [k][row] (a fragment
+// is two gfx950 transposing reads, ds_read_b64_tr_b16).  LDS is double
+// buffered with one barrier per K step; the next step's global loads are in
+// flight during the current step's MFMAs.  With splits > 1 the K range is
+// divided over workgroups, fp32 partials go to a workspace and a fixed-order
+// reduction writes C (deterministic, independent of scheduling).
+#include "common.h"
+#include "launch_gemm.h"
+#include "timing.h"
+
+namespace naylis {
+
+constexpr int kGK = 64;  // K step
+
+struct DevOp {
+  const bf16_t* p1;
+  const bf16_t* p2;
+  long ld;
+};
+struct DevJob {
+  DevOp a, b;
+  void* c;
+  long ldc;
+};
+struct DevJobs {
+  DevJob j[2];
+};
+
+// Tile configuration: WAVES_M x WAVES_N waves, each owning TM x TN MFMA tiles
+// of 32 x 32 (a (32 TM) x (32 TN) block of C).
+template <int WAVES_M_, int WAVES_N_, int TM_, int TN_>
+struct GemmCfg {
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, TM = TM_, TN = TN_;
+  static constexpr int NT = 64 * WAVES_M * WAVES_N;   // threads
+  static constexpr int BM = 32 * TM * WAVES_M;        // workgroup tile rows
+  static constexpr int BN = 32 * TN * WAVES_N;        // workgroup tile columns
+};
+// 128 x 128, 4 waves of 64 x 64.  (256 x 256 tiles with 8 waves of 128 x 64
+// or 4 of 128 x 128 measured no faster on MI355X for these shapes: with one
+// stage of prefetch the K loop waits on load latency, not on MFMA or LDS.)
+using CfgSmall = GemmCfg<2, 2, 2, 2>;
+
+// LDS pitches: a [row][k] tile row is 64 + 8 elements (36 dwords: eight
+// consecutive rows' 16-byte reads hit distinct banks); a [k][row] tile row
+// is ROWS + 16 elements (== 8 dwords mod 64: the 4 rows of a transposing
+// read hit distinct banks).
+template <bool KC, int ROWS>
+struct TileShape {
+  static constexpr int PITCH = KC ? kGK + 8 : ROWS + 16;
+  static constexpr int ELEMS = KC ? ROWS * PITCH : kGK * PITCH;
+};
+
+// One operand's share of a ROWS x 64 stage, loaded through a buffer
+// resource: the per-chunk byte offsets are fixed per thread, a K step only
+// moves the wave-uniform SGPR offset.  KC: [row][k], 8 chunks of 8 per row;
+// else [k][row], ROWS/8 chunks per k.  Rows past the operand's end read a
+// clamped (valid) row; they only feed C rows/columns that are not stored.
+template <bool KC, int ROWS, int NT>
+struct Stage {
+  static constexpr int CPR = KC ? kGK / 8 : ROWS / 8;   // chunks per LDS row
+  static constexpr int N = ROWS * kGK / 8 / NT;         // chunks per thread
+  using Shape = TileShape<KC, ROWS>;
+  uint4 v[N];
+  int voff[N];   // byte offset of the chunk within a stage (k relative to the stage start)
+  int lds[N];    // element offset in the LDS tile
+  int kk[N];     // k of the chunk within the stage
+
+  __device__ __forceinline__ void init(long ld, int nrows, int row0, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int i = tid + NT * j;
+      const int r = KC ? i / CPR : (i % CPR) * 8;
+      const int k = KC ? (i % CPR) * 8 : i / CPR;
+      const int rr = min(row0 + r, nrows - (KC ? 1 : 8)) - row0;  // clamped row (relative)
+      voff[j] = (int)(KC ? ((long)rr * ld + k) * 2 : ((long)k * ld + rr) * 2);
+      lds[j] = KC ? r * Shape::PITCH + k : k * Shape::PITCH + r;
+      kk[j] = k;
+    }
+  }
+  // soff: byte offset of the stage start; klim: valid k within the stage
+  // (wave-uniform; only a split's last stage can be partial)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int soff, int klim) {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      v[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j], soff, 0));
+    if (klim < kGK) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const uint32_t m = kk[j] < klim ? 0xffffffffu : 0u;
+        v[j].x &= m;
+        v[j].y &= m;
+        v[j].z &= m;
+        v[j].w &= m;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16_t* tile) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) *reinterpret_cast<uint4*>(&tile[lds[j]]) = v[j];
+  }
+};
+
+// MFMA fragment of rows row0 .. row0+31, K sub-step ks (16 k): lane l gets
+// X(row0 + l%32, 16 ks + 8 (l/32) + e), e = 0..7 (the A layout; the B layout
+// is the same with rows = n).
+template <bool KC, int ROWS>
+__device__ __forceinline__ bf16x8 gemm_frag(const bf16_t* tile, int row0, int ks) {
+  constexpr int P = TileShape<KC, ROWS>::PITCH;
+  const int lane = threadIdx.x & 63;
+  if constexpr (KC) {
+    return *reinterpret_cast<const bf16x8*>(&tile[(row0 + (lane & 31)) * P + ks * 16 + 8 * (lane >> 5)]);
+  } else {
+    return lds_frag_T<false, false>(tile, P, ks * 16, row0);
+  }
+}
+
+// OUT: 0 = fp32 C, 1 = bf16 C, 2 = fp32 partial into ws[job][split][M][N]
+template <class C, bool AKC, bool BKC, int OUT>
+__global__ __launch_bounds__(C::NT) void gemm_kernel(DevJobs jobs, int M, int N, int K1, int kper, int tiles_m,
+                                                     int tiles_n, int splits, int njobs, int K,
+                                                     float* __restrict__ ws) {
+  using SA = Stage<AKC, C::BM, C::NT>;
+  using SB = Stage<BKC, C::BN, C::NT>;
+  __shared__ __align__(16) bf16_t a_lds[2][SA::Shape::ELEMS];
+  __shared__ __align__(16) bf16_t b_lds[2][SB::Shape::ELEMS];
+  const int tiles = tiles_m * tiles_n;
+  const int G = tiles * splits * njobs;
+  const int lid = xcd_remap(blockIdx.x, G);
+  const int tile = lid % tiles;
+  const int split = (lid / tiles) % splits;
+  const int jb = lid / (tiles * splits);
+  const int m0 = (tile / tiles_n) * C::BM, n0 = (tile % tiles_n) * C::BN;
+  const int kbeg = split * kper;
+  const int kend = min(K, kbeg + kper);
+  const int nk = kend > kbeg ? (kend - kbeg + kGK - 1) / kGK : 0;
+  const DevJob& job = jobs.j[jb];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, held in an SGPR
+  const int wm = (wave % C::WAVES_M) * 32 * C::TM, wn = (wave / C::WAVES_M) * 32 * C::TN;
+
+  // buffer resources over each operand segment, based at this tile's first
+  // row (or column) and the segment's first k
+  auto rsrc = [&](const bf16_t* p, long ld, bool kc, int row0) {
+    return make_rsrc(kc ? p + (long)row0 * ld : p + row0, 0x7fffffff);
+  };
+  const __amdgpu_buffer_rsrc_t ra1 = rsrc(job.a.p1, job.a.ld, AKC, m0), ra2 = rsrc(job.a.p2, job.a.ld, AKC, m0);
+  const __amdgpu_buffer_rsrc_t rb1 = rsrc(job.b.p1, job.b.ld, BKC, n0), rb2 = rsrc(job.b.p2, job.b.ld, BKC, n0);
+  // byte offset of k inside its segment
+  auto koff = [&](int k, long ld, bool kc) { return (int)(kc ? (long)k * 2 : (long)k * ld * 2); };
+
+  SA sa;
+  SB sb;
+  sa.init(job.a.ld, M, m0, tid);
+  sb.init(job.b.ld, N, n0, tid);
+  auto load_stage = [&](int k0) {
+    const bool seg2 = k0 >= K1;
+    const int kseg = seg2 ? k0 - K1 : k0;
+    sa.load(seg2 ? ra2 : ra1, koff(kseg, job.a.ld, AKC), kend - k0);
+    sb.load(seg2 ? rb2 : rb1, koff(kseg, job.b.ld, BKC), kend - k0);
+  };
+
+  f32x16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = f32x16{};
+
+  if (nk > 0) {
+    load_stage(kbeg);
+    sa.store(a_lds[0]);
+    sb.store(b_lds[0]);
+  }
+  __syncthreads();
+  for (int s = 0; s < nk; ++s) {
+    const int cur = s & 1;
+    const bool more = s + 1 < nk;
+    if (more) load_stage(kbeg + (s + 1) * kGK);
+#pragma unroll
+    for (int ks = 0; ks < kGK / 16; ++ks) {
+      bf16x8 af[C::TM], bfr[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) af[i] = gemm_frag<AKC, C::BM>(a_lds[cur], wm + 32 * i, ks);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) bfr[j] = gemm_frag<BKC, C::BN>(b_lds[cur], wn + 32 * j, ks);
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      sa.store(a_lds[cur ^ 1]);
+      sb.store(b_lds[cur ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: acc[i][j][v] = C(m0 + wm + 32i + acc_row(l/32, v), n0 + wn + 32j + l%32)
+  const int g = lane >> 5, col = lane & 31;
+  const long ldo = OUT == 2 ? (long)N : job.ldc;
+  auto put = [&](int m, int n, float x) {
+    if constexpr (OUT == 0) {
+      reinterpret_cast<float*>(job.c)[(long)m * ldo + n] = x;
+    } else if constexpr (OUT == 1) {
+      reinterpret_cast<bf16_t*>(job.c)[(long)m * ldo + n] = f32_to_bf16(x);
+    } else {
+      ws[((long)jb * splits + split) * M * (long)N + (long)m * ldo + n] = x;
+    }
+  };
+  const bool full = m0 + wm + 32 * C::TM <= M && n0 + wn + 32 * C::TN <= N;  // wave-uniform
+  if (full) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) put(m0 + wm + 32 * i + acc_row(g, v), n0 + wn + 32 * j + col, acc[i][j][v]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        const int n = n0 + wn + 32 * j + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = m0 + wm + 32 * i + acc_row(g, v);
+          if (m < M && n < N) put(m, n, acc[i][j][v]);
+        }
+      }
+  }
+}
+
+// C = sum over splits (ascending) of the partials; 4 consecutive n per thread.
+template <int OUT>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(DevJobs jobs, const float* __restrict__ ws, int M, int N,
+                                                          int splits) {
+  const int jb = blockIdx.y;
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  const long mn = (long)M * N;
+  if (i >= mn) return;
+  const float* p = ws + (long)jb * splits * mn + i;
+  f32x4 s = *reinterpret_cast<const f32x4*>(p);
+  for (int sp = 1; sp < splits; ++sp) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + sp * mn);
+    s[0] += v[0];
+    s[1] += v[1];
+    s[2] += v[2];
+    s[3] += v[3];
+  }
+  const long m = i / N, n = i % N;
+  const DevJob& job = jobs.j[jb];
+  if constexpr (OUT == 0) {
+    float* c = reinterpret_cast<float*>(job.c) + m * job.ldc + n;
+    c[0] = s[0];
+    c[1] = s[1];
+    c[2] = s[2];
+    c[3] = s[3];
+  } else {
+    bf16_t* c = reinterpret_cast<bf16_t*>(job.c) + m * job.ldc + n;
+    c[0] = f32_to_bf16(s[0]);
+    c[1] = f32_to_bf16(s[1]);
+    c[2] = f32_to_bf16(s[2]);
+    c[3] = f32_to_bf16(s[3]);
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool gemm_supported(const GemmLaunch& g) {
+  if (g.njobs < 1 || g.njobs > 2 || g.M <= 0 || g.N <= 0 || g.K <= 0) return false;
+  if (g.M % 8 || g.N % 8 || g.K % 8) return false;
+  if (g.K1 < g.K && g.K1 % kGK) return false;
+  for (int j = 0; j < g.njobs; ++j) {
+    const GemmOp* ops[2] = {&g.job[j].a, &g.job[j].b};
+    for (const GemmOp* o : ops) {
+      if (o->ld % 8 || !aligned16(o->p1)) return false;
+      if (g.K1 < g.K && !aligned16(o->p2)) return false;
+      // buffer byte offsets (from a tile's first row and the segment's first k) fit in 31 bits
+      const long span = o->kcontig ? (256L * o->ld + g.K) * 2 : ((long)g.K * o->ld + 256) * 2;
+      if (span >= 0x7fffffffL) return false;
+    }
+  }
+  return true;
+}
+
+size_t gemm_ws_bytes(int njobs, int M, int N, int splits) {
+  return splits > 1 ? (size_t)njobs * splits * M * N * sizeof(float) : 0;
+}
+
+template <class C, bool AKC, bool BKC>
+static void gemm_dispatch(const DevJobs& dj, const GemmLaunch& g, int kper, int splits, const char* name,
+                          hipStream_t st) {
+  const int tiles_m = (g.M + C::BM - 1) / C::BM, tiles_n = (g.N + C::BN - 1) / C::BN;
+  const dim3 grid(tiles_m * tiles_n * splits * g.njobs);
+  float* ws = (float*)g.ws;
+  if (splits > 1) {
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 2>), grid, dim3(C::NT), 0, st, dj, g.M, g.N, g.K1, kper,
+                                    tiles_m, tiles_n, splits, g.njobs, g.K, ws));
+    const dim3 rg((unsigned)(((long)g.M * g.N / 4 + 255) / 256), g.njobs);
+    if (g.out == kGemmOutF32)
+      NAYLIS_TIMED("gemm_reduce", st,
+                   hipLaunchKernelGGL((gemm_reduce_kernel<0>), rg, dim3(256), 0, st, dj, ws, g.M, g.N, splits));
+    else
+      NAYLIS_TIMED("gemm_reduce", st,
+                   hipLaunchKernelGGL((gemm_reduce_kernel<1>), rg, dim3(256), 0, st, dj, ws, g.M, g.N, splits));
+  } else if (g.out == kGemmOutF32) {
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 0>), grid, dim3(C::NT), 0, st, dj, g.M, g.N, g.K1, kper,
+                                    tiles_m, tiles_n, 1, g.njobs, g.K, ws));
+  } else {
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 1>), grid, dim3(C::NT), 0, st, dj, g.M, g.N, g.K1, kper,
+                                    tiles_m, tiles_n, 1, g.njobs, g.K, ws));
+  }
+}
+
+template <class C>
+static void gemm_layouts(const DevJobs& dj, const GemmLaunch& g, int kper, int splits, const char* name,
+                         hipStream_t st) {
+  const bool ak = g.job[0].a.kcontig, bk = g.job[0].b.kcontig;
+  if (ak && bk)
+    gemm_dispatch<C, true, true>(dj, g, kper, splits, name, st);
+  else if (ak)
+    gemm_dispatch<C, true, false>(dj, g, kper, splits, name, st);
+  else if (bk)
+    gemm_dispatch<C, false, true>(dj, g, kper, splits, name, st);
+  else
+    gemm_dispatch<C, false, false>(dj, g, kper, splits, name, st);
+}
+
+hipError_t launch_gemm(const GemmLaunch& g, const char* name, hipStream_t st) {
+  DevJobs dj{};
+  for (int j = 0; j < g.njobs; ++j) {
+    const GemmJob& s = g.job[j];
+    dj.j[j].a = DevOp{(const bf16_t*)s.a.p1, (const bf16_t*)(s.a.p2 ? s.a.p2 : s.a.p1), s.a.ld};
+    dj.j[j].b = DevOp{(const bf16_t*)s.b.p1, (const bf16_t*)(s.b.p2 ? s.b.p2 : s.b.p1), s.b.ld};
+    dj.j[j].c = s.c;
+    dj.j[j].ldc = s.ldc;
+  }
+  int splits = g.splits < 1 ? 1 : g.splits;
+  const int kper = ((g.K + splits - 1) / splits + kGK - 1) / kGK * kGK;
+  splits = (g.K + kper - 1) / kper;
+  GemmLaunch gl = g;
+  gl.K1 = g.K1 < g.K ? g.K1 : g.K;
+  gemm_layouts<CfgSmall>(dj, gl, kper, splits, name, st);
+  return hipGetLastError();
+}
+
+}  // namespace naylis

@@ -1,0 +1,46 @@
+// General bf16 GEMM on MFMA (gemm.hip): C(m, n) = sum_k A(m, k) B(k, n).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace naylis {
+
+// One operand.  K-contiguous: A(m, k) = p[m * ld + k] (B(k, n) = p[n * ld + k]);
+// otherwise A(m, k) = p[k * ld + m] (B(k, n) = p[k * ld + n]).  The operand may
+// be split along K into two tensors: p1 holds k < K1, p2 holds k >= K1 (then
+// indexed from k - K1); K1 must be a multiple of 64 when it is inside [0, K).
+struct GemmOp {
+  const void* p1;
+  const void* p2;
+  long ld;
+  bool kcontig;
+};
+
+enum GemmOut { kGemmOutF32 = 0, kGemmOutBF16 = 1 };
+
+struct GemmJob {
+  GemmOp a, b;
+  void* c;
+  long ldc;
+};
+
+// Up to two GEMMs of the same shape and layouts in one launch.  splits > 1
+// splits K over workgroups: fp32 partials go to `ws` (gemm_ws_bytes) and a
+// fixed-order reduction writes C, so results do not depend on the split.
+struct GemmLaunch {
+  GemmJob job[2];
+  int njobs;
+  int M, N, K, K1;
+  GemmOut out;
+  int splits;
+  void* ws;
+};
+
+// true when the fast kernel supports the shapes and layouts (M, N, K, leading
+// dimensions multiples of 8, 16-byte aligned pointers, K1 a multiple of 64)
+bool gemm_supported(const GemmLaunch& g);
+size_t gemm_ws_bytes(int njobs, int M, int N, int splits);
+hipError_t launch_gemm(const GemmLaunch& g, const char* timer_name, hipStream_t st);
+
+}  // namespace naylis

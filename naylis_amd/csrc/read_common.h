@@ -10,14 +10,6 @@ constexpr int kMaxBlocks = 1024;  // bank blocks (flags live in LDS)
 constexpr int kMaxGroups = 512;   // slot groups of 32 over the whole bank (L <= 16384)
 constexpr int kReadWaves = 8;     // waves (x 32 tokens) per forward / dQ workgroup
 
-// Contiguous logical work ranges land on one XCD: the hardware deals
-// workgroup i to XCD i % 8, so logical id (i % 8) * (G / 8) + i / 8 keeps
-// neighbouring logical ids (same head -> same K/V working set) in one L2.
-__device__ __forceinline__ int xcd_remap(int i, int G) {
-  if (G & 7) return i;
-  return (i & 7) * (G >> 3) + (i >> 3);
-}
-
 // Per-token routing held in registers: block ids and log2 of the clamped
 // gates, as mom_kernels/reference.py:23 builds them (log(max(g, 1e-9))).
 // TK is the compiled maximum of selections per token (>= the runtime topk).

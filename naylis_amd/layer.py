@@ -11,7 +11,8 @@ between the two unchanged.  The forward is
     out   = mom_read(q_proj(x), K, V, idx, gates)       # gated flash read
     y     = mom_scale * o_proj(out)
 
-q_proj / o_proj stay torch linears (hipBLASLt).  There is one backend: the
+q_proj / o_proj run their forward and input gradient as torch GEMMs
+(hipBLASLt) and their weight gradient on the library's split-K GEMM.  There is one backend: the
 HIP kernels (``use_kernel`` is accepted for signature compatibility).  The
 eager SDPA path of model.py:262-275 is the parity oracle and lives in
 ``oracle/``, outside the product.
@@ -98,11 +99,11 @@ class MoMLayer(nn.Module):
     def _read(self, x, top_idx, top_gates, M_blocks):
         """q projection, bank K/V, gated flash read, o projection (model.py:241-276)."""
         B, S, D = x.shape
-        q_sh = self.q_proj(x).view(B, S, self.n_heads, self.head_dim)
+        q_sh = mom_kernels.mom_linear(x, self.q_proj.weight).view(B, S, self.n_heads, self.head_dim)
         k, v = mom_kernels.mom_bank_kv(M_blocks, self.k_proj.weight, self.v_proj.weight, mem_slots=self.mem_slots)
         out = mom_kernels.mom_read(q_sh, k, v, top_idx, top_gates, num_blocks=self.num_blocks,
                                    block_size=self.block_size, mode=self._kernel_mode)
-        return self.o_proj(out.reshape(B, S, D))
+        return mom_kernels.mom_linear(out.reshape(B, S, D), self.o_proj.weight)
 
 
 def mom_aux_loss(layers):

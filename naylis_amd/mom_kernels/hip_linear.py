@@ -1,0 +1,61 @@
+"""Autograd binding of the layer's bias-free q/o projections with the weight
+gradient on the library's split-K MFMA GEMM (C ABI: naylis_mom_linear_wgrad).
+
+model.py:239 (`q_proj`) and model.py:251 (`o_proj`) are nn.Linear(d, d,
+bias=False); the reference takes their weight gradient from autograd, a
+dy^T x reduction over all B*T tokens.  Here the forward product and the input
+gradient stay torch GEMMs (hipBLASLt); the weight gradient is
+naylis_mom_linear_wgrad, deterministic (fixed-order split-K reduction).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+
+_DT = {torch.float32: 0, torch.bfloat16: 1}
+
+
+class MomLinearFunction(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, x, weight):
+        ctx.save_for_backward(x, weight)
+        return F.linear(x, weight)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        D_out, D_in = weight.shape
+        dy2 = dy.reshape(-1, D_out).contiguous()
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(dy2, weight).view(x.shape)
+        dw = None
+        if ctx.needs_input_grad[1]:
+            lib = _lib.load()
+            x2 = x.reshape(-1, D_in).contiguous()
+            N = x2.shape[0]
+            dev = x.device
+            ws = torch.empty(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), device=dev,
+                             dtype=torch.uint8)
+            dw = torch.empty((D_out, D_in), device=dev, dtype=weight.dtype)
+            with torch.cuda.device(dev):
+                rc = lib.naylis_mom_linear_wgrad(x2.data_ptr(), dy2.data_ptr(), dw.data_ptr(), _DT[weight.dtype],
+                                                 ws.data_ptr(), ws.numel(), N, D_in, D_out,
+                                                 torch.cuda.current_stream(dev).cuda_stream)
+            _lib.check(rc)
+        return dx, dw
+
+
+def mom_linear(x, weight):
+    """y = x W^T (no bias).  For bf16 activations and weights on a ROCm device
+    with dimensions that are multiples of 8 the weight gradient runs on the
+    library's GEMM; any other combination is the plain torch linear."""
+    D_out, D_in = weight.shape
+    if (x.is_cuda and torch.version.hip is not None and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and D_in % 8 == 0 and D_out % 8 == 0 and (x.numel() // D_in) % 8 == 0 and torch.is_grad_enabled()
+            and weight.requires_grad):
+        return MomLinearFunction.apply(x, weight)
+    return F.linear(x, weight)

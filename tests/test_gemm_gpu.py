@@ -1,0 +1,75 @@
+"""GPU checks of the split-K MFMA GEMM behind the q/o projection weight
+gradient (C ABI naylis_mom_linear_wgrad; model.py:239,251 take it from
+autograd as dy^T x over all tokens) against an fp64 product of the same bf16
+inputs, plus the autograd binding against torch's own linear.
+
+Tolerance: |got - ref| <= 2e-2 |ref| + 2e-3 max(1, max|ref|) (a sum over up to
+16384 tokens has magnitudes >> 1; the atol scales with it as for the other
+parameter gradients); results must be bitwise reproducible.
+"""
+import pytest
+import torch
+
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def wgrad(x, dy, out_dtype):
+    from naylis_amd import _lib
+    lib = _lib.load()
+    N, D_in = x.shape
+    D_out = dy.shape[1]
+    ws = torch.empty(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), device=x.device, dtype=torch.uint8)
+    dw = torch.full((D_out, D_in), float("nan"), device=x.device, dtype=out_dtype)
+    rc = lib.naylis_mom_linear_wgrad(x.data_ptr(), dy.data_ptr(), dw.data_ptr(), 0 if out_dtype == torch.float32 else 1,
+                                     ws.data_ptr(), ws.numel(), N, D_in, D_out,
+                                     torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    return dw
+
+
+@pytest.mark.parametrize("N,D_in,D_out,out_dtype", [
+    (16384, 1024, 1024, torch.bfloat16),   # config 2: B*T tokens, d x d
+    (16384, 1024, 1024, torch.float32),
+    (16384, 1536, 1536, torch.bfloat16),   # config 4 width
+    (1000, 64, 192, torch.float32),        # ragged token count, rectangular
+    (8, 24, 40, torch.float32),            # below one tile in every dimension
+])
+def test_linear_wgrad_matches_fp64(N, D_in, D_out, out_dtype, dev):
+    g = torch.Generator().manual_seed(N + D_in)
+    x = torch.randn(N, D_in, generator=g).bfloat16()
+    dy = torch.randn(N, D_out, generator=g).bfloat16()
+    got = wgrad(x.to(dev), dy.to(dev), out_dtype)
+    torch.cuda.synchronize()
+    ref = dy.double().T @ x.double()
+    assert_close(got, ref, "dW", atol=2e-3 * max(1.0, float(ref.abs().max())))
+
+
+def test_linear_wgrad_deterministic_and_empty(dev):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(16384, 1024, generator=g).bfloat16().to(dev)
+    dy = torch.randn(16384, 1024, generator=g).bfloat16().to(dev)
+    a = wgrad(x, dy, torch.float32)
+    b = wgrad(x, dy, torch.float32)
+    assert torch.equal(a, b)
+    z = wgrad(x[:0], dy[:0], torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(z.cpu(), torch.zeros(1024, 1024))
+
+
+def test_mom_linear_autograd_matches_torch(dev):
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4, 512, 256, generator=g).bfloat16().to(dev).requires_grad_(True)
+    w = (torch.randn(384, 256, generator=g) * 0.05).bfloat16().to(dev).requires_grad_(True)
+    dy = torch.randn(4, 512, 384, generator=g).bfloat16().to(dev)
+    y = mom_kernels.mom_linear(x, w)
+    y.backward(dy)
+    xr = x.detach().double().requires_grad_(True)
+    wr = w.detach().double().requires_grad_(True)
+    yr = torch.nn.functional.linear(xr, wr)
+    yr.backward(dy.double())
+    assert_close(y, yr, "y")
+    assert_close(x.grad, xr.grad, "dx")
+    assert_close(w.grad, wr.grad, "dW", atol=2e-3 * max(1.0, float(wr.grad.abs().max())))

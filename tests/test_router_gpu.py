@@ -56,6 +56,27 @@ CASES = [
 ]
 
 
+def test_router_prefix_mean_tiny_values(dev):
+    """Prefix means in and near the fp32 subnormal range stay bit-exact
+    (the kernel's reciprocal product hands nonzero subnormal quotients to
+    the IEEE division; the fp64 partial sums of such inputs are exact, so the
+    chunked summation order cannot matter)."""
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(5)
+    B, T, D, R, E, k = 2, 4096, 64, 8, 4, 2
+    x = torch.randn(B, T, D, generator=g) * 2.0 ** -128
+    x[:, :, :8] = 0.0                                           # exact zeros
+    x[0, :, 8:16] = torch.randint(-3, 4, (T, 8), generator=g).float() * 2.0 ** -149   # subnormal multiples
+    w_down = torch.randn(R, D, generator=g) * 0.02
+    w_up = torch.randn(E, R, generator=g) * 0.02
+    *_, h = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), k, return_h=True)
+    torch.cuda.synchronize()
+    r_h = oracle.prefix_mean(x)
+    sub = (r_h != 0) & (r_h.abs() < torch.finfo(torch.float32).tiny)
+    assert int(sub.sum()) > 1000, "the case must exercise subnormal prefix means"
+    assert torch.equal(h.cpu(), r_h), f"{int((h.cpu() != r_h).sum())} prefix-mean values differ"
+
+
 @pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}T{c[1]}D{c[2]}R{c[3]}E{c[4]}k{c[5]}{str(c[6])[6:]}" for c in CASES])
 def test_router_forward(case, dev):
     from naylis_amd import mom_kernels
