@@ -156,6 +156,19 @@ size_t naylis_mom_linear_wgrad_workspace_bytes(int64_t N, int64_t D_in, int64_t 
 int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtype, void* workspace,
                             size_t workspace_bytes, int64_t N, int64_t D_in, int64_t D_out, void* stream);
 
+/* ------------------------------------------------------------- ReZero ---
+ * The layer's output gate (model.py:151 `mom_scale`, applied at model.py:239
+ * as `self.mom_scale * out`): y = s * z with s the (1,) fp32 parameter on the
+ * device, z (n elements) in z_dtype, y fp32 (torch type promotion).
+ * Backward: dz = s * dy in z_dtype (dz may be NULL when z needs no gradient)
+ * and ds = sum(dy * z), one fp32 value reduced in a fixed order through the
+ * caller's workspace (naylis_mom_rezero_workspace_bytes).  dy in dy_dtype.
+ * No counterpart kernel in the reference (eager elementwise ops there). */
+size_t naylis_mom_rezero_workspace_bytes(int64_t n);
+int naylis_mom_rezero_fwd(const void* z, int z_dtype, const float* s, float* y, int64_t n, void* stream);
+int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dtype, const float* s, void* dz, float* ds,
+                          void* workspace, size_t workspace_bytes, int64_t n, void* stream);
+
 /* -------------------------------------------------------------- timing ---
  * Optional instrumentation (no counterpart in the reference; for benchmarks):
  * when enabled, each kernel launch of this library is bracketed by hipEvents

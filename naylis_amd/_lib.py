@@ -7,6 +7,7 @@ fallback: a missing or stale library raises ``RuntimeError``.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -40,6 +41,9 @@ SIGNATURES = {
                               + [_c_void_p]),
     "naylis_mom_bank_kv_fwd": (_int, [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_linear_wgrad_workspace_bytes": (_size_t, [_i64] * 3),
+    "naylis_mom_rezero_workspace_bytes": (_size_t, [_i64]),
+    "naylis_mom_rezero_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _c_void_p]),
+    "naylis_mom_rezero_bwd": (_int, [_c_void_p, _int, _c_void_p, _int] + [_c_void_p] * 4 + [_size_t, _i64, _c_void_p]),
     "naylis_mom_linear_wgrad": (_int, [_c_void_p] * 3 + [_int, _c_void_p, _size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
@@ -129,3 +133,24 @@ def available():
         return True
     except (RuntimeError, OSError):
         return False
+
+
+_NULL_CTX = contextlib.nullcontext()
+
+
+def on_device(device):
+    """Context making `device` current only when it is not already: a switch
+    costs two runtime calls per launch, and the layer's tensors normally sit
+    on the current device."""
+    import torch
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if torch.cuda.current_device() == idx:
+        return _NULL_CTX
+    return torch.cuda.device(idx)
+
+
+def stream_of(device):
+    """Raw handle of torch's current stream on `device` (where launches go)."""
+    import torch
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

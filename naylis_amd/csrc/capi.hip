@@ -16,6 +16,7 @@
 #include "launch_router.h"
 #include "launch_bank.h"
 #include "launch_gemm.h"
+#include "launch_rezero.h"
 
 using namespace naylis;
 
@@ -325,8 +326,8 @@ int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtyp
     return fail(NAYLIS_ERR_WORKSPACE, "linear_wgrad: workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
   if (N == 0)  // no tokens: the gradient is zero
-    return hip_status(hipMemsetAsync(dw, 0, (size_t)D_out * D_in * (dw_dtype == NAYLIS_DTYPE_F32 ? 4 : 2),
-                                     (hipStream_t)stream),
+    return hip_status(launch_zero(dw, (size_t)D_out * D_in * (dw_dtype == NAYLIS_DTYPE_F32 ? 4 : 2),
+                                  (hipStream_t)stream),
                       "linear_wgrad");
   GemmLaunch g{};
   g.njobs = 1;
@@ -343,6 +344,38 @@ int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtyp
   if (!gemm_supported(g))
     return fail(NAYLIS_ERR_ARG, "linear_wgrad: needs 16-byte aligned pointers and N * max(D_in, D_out) < 2^30");
   return hip_status(launch_gemm(g, "linear_wgrad", (hipStream_t)stream), "linear_wgrad");
+}
+
+// -------------------------------------------------------------------- ReZero
+size_t naylis_mom_rezero_workspace_bytes(int64_t n) {
+  if (n < 0) return 0;
+  return rezero_ws_bytes((long)n);
+}
+
+int naylis_mom_rezero_fwd(const void* z, int z_dtype, const float* s, float* y, int64_t n, void* stream) {
+  int rc;
+  if (n < 0) return fail(NAYLIS_ERR_ARG, "rezero_fwd: negative size %lld", (long long)n);
+  if ((rc = check_dtype(z_dtype, "rezero_fwd"))) return rc;
+  if (n == 0) return NAYLIS_OK;
+  if (!z || !s || !y) return fail(NAYLIS_ERR_ARG, "rezero_fwd: null pointer argument");
+  return hip_status(launch_rezero_fwd(z, z_dtype == NAYLIS_DTYPE_BF16, s, y, (long)n, (hipStream_t)stream),
+                    "rezero_fwd");
+}
+
+int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dtype, const float* s, void* dz, float* ds,
+                          void* workspace, size_t workspace_bytes, int64_t n, void* stream) {
+  int rc;
+  if (n < 0) return fail(NAYLIS_ERR_ARG, "rezero_bwd: negative size %lld", (long long)n);
+  if ((rc = check_dtype(dy_dtype, "rezero_bwd"))) return rc;
+  if ((rc = check_dtype(z_dtype, "rezero_bwd"))) return rc;
+  if (!s || !ds || (n > 0 && (!dy || !z))) return fail(NAYLIS_ERR_ARG, "rezero_bwd: null pointer argument");
+  const size_t need = rezero_ws_bytes((long)n);
+  if (!workspace || workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "rezero_bwd: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  return hip_status(launch_rezero_bwd(dy, dy_dtype == NAYLIS_DTYPE_BF16, z, z_dtype == NAYLIS_DTYPE_BF16, s, dz, ds,
+                                      workspace, (long)n, (hipStream_t)stream),
+                    "rezero_bwd");
 }
 
 }  // extern "C"

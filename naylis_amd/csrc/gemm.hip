@@ -273,6 +273,22 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(DevJobs jobs, const fl
   }
 }
 
+// Zero-fill through a kernel (a memset node is not safe inside captured HIP graphs).
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint8_t* __restrict__ p, size_t bytes) {
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (i + 16 <= bytes && ((uintptr_t)(p + i) & 15) == 0) {
+    *reinterpret_cast<uint4*>(p + i) = make_uint4(0, 0, 0, 0);
+  } else {
+    for (size_t j = i; j < i + 16 && j < bytes; ++j) p[j] = 0;
+  }
+}
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((bytes + 4095) / 4096)), dim3(256), 0, st, (uint8_t*)p, bytes);
+  return hipGetLastError();
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 bool gemm_supported(const GemmLaunch& g) {

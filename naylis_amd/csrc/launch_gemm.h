@@ -43,4 +43,7 @@ bool gemm_supported(const GemmLaunch& g);
 size_t gemm_ws_bytes(int njobs, int M, int N, int splits);
 hipError_t launch_gemm(const GemmLaunch& g, const char* timer_name, hipStream_t st);
 
+// Zero `bytes` bytes at p with a kernel (safe inside captured HIP graphs).
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t st);
+
 }  // namespace naylis

@@ -1,0 +1,13 @@
+// Host-side launchers of the ReZero output gate (rezero.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace naylis {
+
+size_t rezero_ws_bytes(long n);
+hipError_t launch_rezero_fwd(const void* z, bool z_bf16, const float* s, float* y, long n, hipStream_t st);
+hipError_t launch_rezero_bwd(const void* dy, bool dy_bf16, const void* z, bool z_bf16, const float* s, void* dz,
+                             float* ds, void* ws, long n, hipStream_t st);
+
+}  // namespace naylis

@@ -94,7 +94,7 @@ class MoMLayer(nn.Module):
                 self._read, x, top_idx, top_gates, M_blocks, use_reentrant=False, preserve_rng_state=False)
         else:
             out = self._read(x, top_idx, top_gates, M_blocks)
-        return self.mom_scale * out
+        return mom_kernels.mom_rezero(out, self.mom_scale)
 
     def _read(self, x, top_idx, top_gates, M_blocks):
         """q projection, bank K/V, gated flash read, o projection (model.py:241-276)."""

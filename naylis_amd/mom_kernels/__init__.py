@@ -20,7 +20,7 @@ from .. import _lib
 from .hip_read import mom_read as _hip_mom_read
 
 __all__ = ["HAS_HIP", "preflight", "resolve_mode", "mom_read", "announce", "mom_route",
-           "mom_bank_kv", "mom_linear", "has_hip"]
+           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip"]
 
 _ANNOUNCED = {"backend": None}
 
@@ -108,3 +108,8 @@ def mom_bank_kv(*args, **kwargs):
 def mom_linear(*args, **kwargs):
     from .hip_linear import mom_linear as _linear
     return _linear(*args, **kwargs)
+
+
+def mom_rezero(*args, **kwargs):
+    from .hip_rezero import mom_rezero as _rezero
+    return _rezero(*args, **kwargs)

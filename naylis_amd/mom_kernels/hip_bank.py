@@ -13,10 +13,6 @@ from .. import _lib
 _DT = {torch.float32: 0, torch.bfloat16: 1}
 
 
-def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
-
-
 class MomBankKVFunction(torch.autograd.Function):
 
     @staticmethod
@@ -35,9 +31,9 @@ class MomBankKVFunction(torch.autograd.Function):
         dev = slots.device
         k = torch.empty((L, D_out), device=dev, dtype=torch.bfloat16)
         v = torch.empty((L, D_out), device=dev, dtype=torch.bfloat16)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_bank_kv_fwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), k.data_ptr(),
-                                            v.data_ptr(), L, D_in, D_out, _stream(dev))
+                                            v.data_ptr(), L, D_in, D_out, _lib.stream_of(dev))
         _lib.check(rc)
         ctx.save_for_backward(slots, w_k, w_v)
         ctx.gdt = (slots_grad_dtype, w_grad_dtype)
@@ -56,10 +52,10 @@ class MomBankKVFunction(torch.autograd.Function):
         d_slots = torch.empty((L, D_in), device=dev, dtype=sdt)
         dw_k = torch.empty((D_out, D_in), device=dev, dtype=wdt)
         dw_v = torch.empty((D_out, D_in), device=dev, dtype=wdt)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_bank_kv_bwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), dk.data_ptr(),
                                             dv.data_ptr(), d_slots.data_ptr(), _DT[sdt], dw_k.data_ptr(),
-                                            dw_v.data_ptr(), _DT[wdt], L, D_in, D_out, _stream(dev))
+                                            dw_v.data_ptr(), _DT[wdt], L, D_in, D_out, _lib.stream_of(dev))
         _lib.check(rc)
         return d_slots, dw_k, dw_v
 

@@ -41,10 +41,10 @@ class MomLinearFunction(torch.autograd.Function):
             ws = torch.empty(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), device=dev,
                              dtype=torch.uint8)
             dw = torch.empty((D_out, D_in), device=dev, dtype=weight.dtype)
-            with torch.cuda.device(dev):
+            with _lib.on_device(dev):
                 rc = lib.naylis_mom_linear_wgrad(x2.data_ptr(), dy2.data_ptr(), dw.data_ptr(), _DT[weight.dtype],
                                                  ws.data_ptr(), ws.numel(), N, D_in, D_out,
-                                                 torch.cuda.current_stream(dev).cuda_stream)
+                                                 _lib.stream_of(dev))
             _lib.check(rc)
         return dx, dw
 

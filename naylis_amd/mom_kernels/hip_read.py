@@ -13,10 +13,6 @@ import torch
 from .. import _lib
 
 
-def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
-
-
 def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -33,11 +29,11 @@ class MomReadFunction(torch.autograd.Function):
         dev = q_sh.device
         out = torch.empty_like(q_sh)
         lse = torch.empty((H, B, S), device=dev, dtype=torch.float32)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_read_fwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
                 out.data_ptr(), lse.data_ptr(), None, 0,
-                B, S, H, HD, num_blocks, block_size, topk, _stream(dev))
+                B, S, H, HD, num_blocks, block_size, topk, _lib.stream_of(dev))
         _lib.check(rc)
         ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, out, lse)
         ctx.geom = (num_blocks, block_size)
@@ -62,12 +58,12 @@ class MomReadFunction(torch.autograd.Function):
         if nbytes == 0:
             _lib.check(_lib.NAYLIS_ERR_ARG)
         ws = _workspace(nbytes, dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_read_bwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
                 out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                 dgates.data_ptr(), ws.data_ptr(), ws.numel(),
-                B, S, H, HD, num_blocks, block_size, topk, _stream(dev))
+                B, S, H, HD, num_blocks, block_size, topk, _lib.stream_of(dev))
         _lib.check(rc)
         return dq, dk, dv, None, dgates, None, None
 

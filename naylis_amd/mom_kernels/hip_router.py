@@ -16,10 +16,6 @@ from .. import _lib
 _DT = {torch.float32: 0, torch.bfloat16: 1}
 
 
-def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
-
-
 class MomRouteFunction(torch.autograd.Function):
 
     @staticmethod
@@ -39,13 +35,13 @@ class MomRouteFunction(torch.autograd.Function):
         if nbytes == 0:
             _lib.check(_lib.NAYLIS_ERR_ARG)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_router_fwd(
                 x.data_ptr(), _DT[x.dtype], w_down.data_ptr(), w_up.data_ptr(),
                 noise.data_ptr() if noise is not None else None, float(noise_scale),
                 logits.data_ptr(), probs.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(), act.data_ptr(),
                 h.data_ptr() if h is not None else None, ws.data_ptr(), ws.numel(),
-                B, T, D, R, E, top_k, _stream(dev))
+                B, T, D, R, E, top_k, _lib.stream_of(dev))
         _lib.check(rc)
         ctx.save_for_backward(x, w_down, w_up, act, probs, top_idx, top_gates)
         ctx.mark_non_differentiable(top_idx)
@@ -72,7 +68,7 @@ class MomRouteFunction(torch.autograd.Function):
         dw_up = torch.empty((E, R), device=dev, dtype=torch.float32)
         nbytes = lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, top_k)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.naylis_mom_router_bwd(
                 x.data_ptr(), _DT[x.dtype], w_down.data_ptr(), w_up.data_ptr(), act.data_ptr(),
                 probs.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
@@ -80,7 +76,7 @@ class MomRouteFunction(torch.autograd.Function):
                 d_probs.data_ptr() if d_probs is not None else None,
                 d_logits.data_ptr() if d_logits is not None else None,
                 dx.data_ptr(), dw_down.data_ptr(), dw_up.data_ptr(), ws.data_ptr(), ws.numel(),
-                B, T, D, R, E, top_k, _stream(dev))
+                B, T, D, R, E, top_k, _lib.stream_of(dev))
         _lib.check(rc)
         return dx, dw_down, dw_up, None, None, None, None
 

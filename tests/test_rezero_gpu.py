@@ -1,0 +1,50 @@
+"""GPU checks of the ReZero output gate kernel (C ABI naylis_mom_rezero_*;
+model.py:239 `self.mom_scale * out`) against fp64 torch on the same inputs:
+y = s z, dz = s dy, ds = sum(dy z); ragged sizes, both dtypes, determinism."""
+import pytest
+import torch
+
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n,zdt,dydt", [
+    (8 * 2048 * 1024, torch.bfloat16, torch.float32),   # config 2: o_proj output bf16, y fp32
+    (1000003, torch.bfloat16, torch.bfloat16),          # ragged, bf16 upstream gradient
+    (4099, torch.float32, torch.float32),
+    (5, torch.float32, torch.bfloat16),
+])
+def test_rezero_matches_fp64(n, zdt, dydt, dev):
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(n % 1000)
+    z = torch.randn(n, generator=g).to(zdt).to(dev).requires_grad_(True)
+    s = torch.tensor([0.37], device=dev, requires_grad=True)
+    dy = torch.randn(n, generator=g).to(dydt).to(dev)
+    y = mom_kernels.mom_rezero(z, s)
+    assert y.dtype == torch.float32
+    y.backward(dy)
+    zr = z.detach().double()
+    assert_close(y, 0.37 * zr, "y", rtol=1e-6, atol=1e-7)
+    assert_close(z.grad, (0.37 * dy.double()).to(zdt), "dz")
+    ds_ref = (dy.double() * zr).sum()
+    assert z.grad.dtype == zdt and s.grad.shape == (1,)
+    assert abs(float(s.grad) - float(ds_ref)) <= 1e-5 * float((dy.double() * zr).abs().sum()) + 1e-6
+
+
+def test_rezero_deterministic_and_zero_size(dev):
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(1)
+    z = torch.randn(3 * 1024 * 1024, generator=g).bfloat16().to(dev)
+    dy = torch.randn(3 * 1024 * 1024, generator=g).to(dev)
+    grads = []
+    for _ in range(2):
+        zz = z.clone().requires_grad_(True)
+        s = torch.tensor([1.5], device=dev, requires_grad=True)
+        mom_kernels.mom_rezero(zz, s).backward(dy)
+        grads.append((zz.grad.clone(), s.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    e = torch.zeros(0, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    s = torch.tensor([2.0], device=dev, requires_grad=True)
+    mom_kernels.mom_rezero(e, s).backward(torch.zeros(0, device=dev))
+    assert float(s.grad) == 0.0
