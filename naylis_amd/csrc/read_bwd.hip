@@ -157,6 +157,20 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     __syncthreads();
     if (it + 1 < n_act) load_group(groups[it + 1]);
 
+    // a wave whose 32 tokens select no block of the group has P = 0 there:
+    // nothing to add to dQ, the gate sums or delta
+    bool mine = false;
+    if constexpr (ALIGNED) {
+      const int e = (gi * SG) / block_size;
+#pragma unroll
+      for (int t = 0; t < TK; ++t) mine |= (t < topk && rt.idx[t] == e);
+    } else {
+      const int b0 = (gi * SG) / block_size, b1 = (min(gi * SG + SG, L) - 1) / block_size;
+#pragma unroll
+      for (int t = 0; t < TK; ++t) mine |= (t < topk && rt.idx[t] >= b0 && rt.idx[t] <= b1);
+    }
+    if (!__any(mine)) continue;
+
     f32x16 acc_s[NS], acc_p[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
