@@ -122,6 +122,23 @@ def active_tiles(idx, E, tile=128):
     return int(oh.view(B, n_tiles, tile, E).any(2).sum())
 
 
+def executed_tiles(idx, E, tile=128):
+    """(tile, block) pairs over the flattened tokens in the order the read
+    kernels walk them (the library's token order for this routing)."""
+    import torch
+    from naylis_amd.mom_kernels.hip_read import read_order
+    B, T, K = idx.shape
+    N = B * T
+    order = read_order(idx.to(torch.int32).contiguous(), E)
+    flat = idx.reshape(N, K).long()
+    if int(order[0]) == 1:
+        flat = flat[order[1:].long()]
+    n_tiles = (N + tile - 1) // tile
+    oh = torch.zeros(n_tiles * tile, E, dtype=torch.bool, device=idx.device)
+    oh[:N].scatter_(1, flat, True)
+    return int(oh.view(n_tiles, tile, E).any(1).sum()), ("grouped" if int(order[0]) == 1 else "sequence")
+
+
 def cpu_baseline(cfg, sample_b):
     """Eager fp32 oracle layer fwd+bwd on the host cores, on `sample_b` of the
     B sequences at the full T (1 warmup + median of 3)."""
@@ -210,6 +227,7 @@ def main(argv=None):
     # reference's BLOCK_M): per (b, tile, active block) d*bs*128 MACs per GEMM
     idx = routing(layer, M, x)
     A = active_tiles(idx, E)
+    A_exec, order_mode = executed_tiles(idx, E)
     unit = 2.0 * D * BS * 128 * A          # FLOP of one GEMM-shaped product
     L = E * BS
     alg = {"read_fwd": 2 * unit, "read_bwd_dq": 3 * unit, "read_bwd_dkdv": 4 * unit,
@@ -255,6 +273,7 @@ def main(argv=None):
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
         "roofline": roof,
         "read": {"active_tile_blocks": A, "active_per_tile": round(A / (B * ((T + 127) // 128)), 3),
+                 "token_order": order_mode, "executed_tile_blocks": A_exec,
                  "alg_flop": read_flop, "ms": round(read_ms, 4), "tflops": round(read_tf, 2),
                  "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},

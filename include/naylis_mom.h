@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 1
+#define NAYLIS_MOM_ABI_VERSION 2
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -60,6 +60,16 @@ const char* naylis_mom_last_error(void);
  *   out      (B, S, H, head_dim) bf16
  *   lse      (H, B, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
+ *   token_order (1 + B*S) int32 or NULL  the order in which the read walks
+ *                                          the flattened tokens b*S + s, as
+ *                                          written by naylis_mom_read_order:
+ *                                          word 0 = 1 when words 1.. hold a
+ *                                          grouped order, 0 for sequence
+ *                                          order; NULL is sequence order.
+ *                                          Results do not depend on it beyond
+ *                                          fp32 rounding of the dK/dV sums;
+ *                                          the backward must get the
+ *                                          forward's order.
  * Constraints: head_dim a power of two in [16, 128]; 1 <= k <= min(8, E);
  * E <= 1024; L <= 16384.  The forward needs no workspace (pass NULL, 0); the
  * backward needs naylis_mom_read_workspace_bytes() bytes.
@@ -68,18 +78,31 @@ size_t naylis_mom_read_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t 
                                        int64_t block_size, int64_t top_k);
 
 int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                        const float* top_gates, void* out, float* lse, void* workspace, size_t workspace_bytes,
-                        int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                        int64_t top_k, void* stream);
+                        const float* top_gates, const int32_t* token_order, void* out, float* lse, void* workspace,
+                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
 
 /* Backward of the read: dq (B,S,H,head_dim) bf16; dk, dv (L, D) bf16 reduced
  * over all N tokens (deterministic, fixed-order); dgates (B,S,k) fp32 =
  * d loss / d top_gates.  `out` and `lse` are the forward's outputs. */
 int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                        const float* top_gates, const void* out, const float* lse, const void* dout, void* dq,
-                        void* dk, void* dv, float* dgates, void* workspace, size_t workspace_bytes, int64_t B,
-                        int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                        int64_t top_k, void* stream);
+                        const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, float* dgates, void* workspace,
+                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
+
+/* Token order for the read (no counterpart in the reference, which walks
+ * tokens in sequence order with BLOCK_M = 128, triton_gpu.py:50,98): the
+ * bank's K/V are shared by the whole batch, so tokens may be read in any
+ * order.  order (1 + B*S) int32: for top-2 routing over at most 32 blocks,
+ * words 1.. receive the flattened tokens grouped by their block pair (stable
+ * within a pair) and word 0 = 1, when that lowers the number of (128-token
+ * tile, block) pairs by at least 10 %; otherwise word 0 = 0 (sequence order;
+ * also for every other routing and for more than 2^18 tokens).  A function
+ * of top_idx only.  Workspace: naylis_mom_read_order_workspace_bytes(). */
+size_t naylis_mom_read_order_workspace_bytes(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k);
+int naylis_mom_read_order(const int32_t* top_idx, int32_t* order, void* workspace, size_t workspace_bytes, int64_t B,
+                          int64_t S, int64_t num_blocks, int64_t top_k, void* stream);
 
 /* -------------------------------------------------------------- router ---
  * The causal prefix-mean router of MoMLayer, which the reference runs as

@@ -151,14 +151,15 @@ size_t naylis_mom_read_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t 
 }
 
 int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx, const float* top_gates,
-                        void* out, float* lse, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
-                        int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
-                        void* stream) {
+                        const int32_t* token_order, void* out, float* lse, void* workspace, size_t workspace_bytes,
+                        int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                        int64_t top_k, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
   ReadDims d;
   int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
   if (rc) return rc;
+  d.order = token_order;
   if (B * S == 0) return NAYLIS_OK;
   if (!q || !k || !v || !top_idx || !top_gates || !out || !lse)
     return fail(NAYLIS_ERR_ARG, "mom_read_fwd: null pointer argument");
@@ -166,12 +167,14 @@ int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32
 }
 
 int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32_t* top_idx, const float* top_gates,
-                        const void* out, const float* lse, const void* dout, void* dq, void* dk, void* dv,
-                        float* dgates, void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t H,
-                        int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream) {
+                        const int32_t* token_order, const void* out, const float* lse, const void* dout, void* dq,
+                        void* dk, void* dv, float* dgates, void* workspace, size_t workspace_bytes, int64_t B,
+                        int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                        int64_t top_k, void* stream) {
   ReadDims d;
   int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
   if (rc) return rc;
+  d.order = token_order;
   if (!k || !v || !dk || !dv || !workspace) return fail(NAYLIS_ERR_ARG, "mom_read_bwd: null pointer argument");
   if (B * S > 0 && (!q || !top_idx || !top_gates || !out || !lse || !dout || !dq || !dgates))
     return fail(NAYLIS_ERR_ARG, "mom_read_bwd: null pointer argument");
@@ -202,6 +205,38 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   if (rc) return rc;
   return hip_status(launch_read_bwd_reduce(dkp, dvp, dlg, top_gates, dk, dv, dgates, w.n_chunks, d, st),
                     "mom_read_bwd reduce");
+}
+
+static int check_order_dims(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k) {
+  if (B < 0 || S < 0 || B * S > ((int64_t)1 << 30))
+    return fail(NAYLIS_ERR_ARG, "mom_read_order: bad token count B=%lld S=%lld", (long long)B, (long long)S);
+  if (num_blocks < 1 || num_blocks > NAYLIS_MAX_BLOCKS)
+    return fail(NAYLIS_ERR_ARG, "mom_read_order: num_blocks %lld must be in [1, %d]", (long long)num_blocks,
+                NAYLIS_MAX_BLOCKS);
+  if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > num_blocks)
+    return fail(NAYLIS_ERR_ARG, "mom_read_order: top_k %lld must be in [1, min(%d, num_blocks=%lld)]",
+                (long long)top_k, NAYLIS_MAX_TOPK, (long long)num_blocks);
+  return NAYLIS_OK;
+}
+
+size_t naylis_mom_read_order_workspace_bytes(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k) {
+  if (check_order_dims(B, S, num_blocks, top_k) != NAYLIS_OK) return 0;
+  return read_order_ws_bytes((long)(B * S), (int)num_blocks, (int)top_k);
+}
+
+int naylis_mom_read_order(const int32_t* top_idx, int32_t* order, void* workspace, size_t workspace_bytes, int64_t B,
+                          int64_t S, int64_t num_blocks, int64_t top_k, void* stream) {
+  int rc = check_order_dims(B, S, num_blocks, top_k);
+  if (rc) return rc;
+  if (B * S == 0) return NAYLIS_OK;
+  if (!top_idx || !order || !workspace) return fail(NAYLIS_ERR_ARG, "mom_read_order: null pointer argument");
+  const size_t need = read_order_ws_bytes((long)(B * S), (int)num_blocks, (int)top_k);
+  if (workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_read_order: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  return hip_status(launch_read_order(top_idx, (long)(B * S), (int)num_blocks, (int)top_k, order, workspace,
+                                      (hipStream_t)stream),
+                    "mom_read_order");
 }
 
 size_t naylis_mom_router_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k) {

@@ -2,13 +2,24 @@
 // launch error; argument validation lives in the C ABI layer (capi.hip).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace naylis {
 
 struct ReadDims {
   int B, S, H, HD, L, E, block_size, topk;
+  // Token order of the read's tiles, from launch_read_order: 1 + N int32,
+  // word 0 = 1 when words 1..N map position -> flattened token b*S + s, 0 for
+  // sequence order; nullptr is sequence order too.
+  const int32_t* order = nullptr;
 };
+
+// The read's token order (read_order.hip): tokens grouped by selected blocks
+// when that lowers the (tile, block) pairs, else the sequence-order mode word.
+size_t read_order_ws_bytes(long N, int E, int topk);
+hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, int32_t* order, void* ws,
+                             hipStream_t st);
 
 hipError_t launch_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
                            const float* top_gates, void* out, float* lse, const ReadDims& d, hipStream_t st);

@@ -31,8 +31,8 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
     const bf16_t* __restrict__ dout, const float* __restrict__ lse, bf16_t* __restrict__ dq,
-    float* __restrict__ delta, float* __restrict__ dlg_part, int B, int S, int H, int L, int E, int block_size,
-    int topk, float alpha, float scale, int n_tiles) {
+    float* __restrict__ delta, float* __restrict__ dlg_part, const int32_t* __restrict__ order, long N, int H,
+    int L, int E, int block_size, int topk, float alpha, float scale, int n_tiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NS = SG / 32;
@@ -45,20 +45,20 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
   __shared__ uint16_t groups[kMaxGroups];
   __shared__ int n_active;
 
-  const int G = B * H * n_tiles;
+  const int G = H * n_tiles;
   const int wid = xcd_remap(blockIdx.x, G);
   const int tile = wid % n_tiles;
-  const int b = (wid / n_tiles) % B;
-  const int h = wid / (n_tiles * B);
+  const int h = wid / n_tiles;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const int s_tok = tile * 128 + wave * 32 + col;
-  const bool tok_ok = s_tok < S;
-  const long tok = (long)b * S + s_tok;
+  const long pos = (long)tile * 128 + wave * 32 + col;  // position in the token order
+  const bool tok_ok = pos < N;
+  const int32_t* ord = order_table(order);
+  const long tok = tok_ok ? order_token(ord, pos, N) : 0;  // flattened b*S + s
   const int D = H * HD;
 
   TokenRoute<TK> rt;
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
     }
   }
   dl = wave_sum_pair(dl);
-  const float lse_t = tok_ok ? lse[(long)h * B * S + tok] : 0.f;
+  const float lse_t = tok_ok ? lse[(long)h * N + tok] : 0.f;
 
   f32x16 acc_dq[NO];
 #pragma unroll
@@ -267,8 +267,8 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
       }
     }
     if (g == 0) {
-      const long ntok = (long)B * S;
-      delta[(long)h * B * S + tok] = dx;
+      const long ntok = N;
+      delta[(long)h * N + tok] = dx;
 #pragma unroll
       for (int t = 0; t < TK; ++t)
         if (t < topk) dlg_part[((long)h * ntok + tok) * topk + t] = dlg[t];
@@ -280,15 +280,18 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
 // Active 64-token tiles per 128-slot group.
 constexpr int kDkdvTile = 64;
 
-// tile_flags[tile][e] = 1 when a token of the tile selects block e
+// tile_flags[tile][e] = 1 when a token of the tile (64 positions of the token
+// order) selects block e
 __global__ __launch_bounds__(64) void read_tile_flags_kernel(const int32_t* __restrict__ top_idx,
+                                                             const int32_t* __restrict__ order,
                                                              uint8_t* __restrict__ tile_flags, long ntok, int E,
                                                              int topk) {
   __shared__ uint8_t fl[kMaxBlocks];
   const long tile = blockIdx.x;
   for (int e = threadIdx.x; e < E; e += 64) fl[e] = 0;
   __syncthreads();
-  const long tk = tile * kDkdvTile + threadIdx.x;
+  const long pos = tile * kDkdvTile + threadIdx.x;
+  const long tk = pos < ntok ? order_token(order_table(order), pos, ntok) : ntok;
   if (tk < ntok)
     for (int t = 0; t < topk; ++t) {
       const int id = top_idx[tk * topk + t];
@@ -338,8 +341,9 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, const int32_t* __restrict__ tile_list,
-    const int32_t* __restrict__ tile_count, float* __restrict__ dk_part, float* __restrict__ dv_part, int B, int S,
-    int H, int L, int Lq, int E, int block_size, int topk, float alpha, int n_chunks, int n_ttiles) {
+    const int32_t* __restrict__ tile_count, float* __restrict__ dk_part, float* __restrict__ dv_part,
+    const int32_t* __restrict__ order, long ntok, int H, int L, int Lq, int E, int block_size, int topk, float alpha,
+    int n_chunks, int n_ttiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NO = HDP / 32;
@@ -373,7 +377,6 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   const int slot = sg * 128 + quarter * 32 + col;
   const bool slot_ok = slot < L;
   const int D = H * HD;
-  const long ntok = (long)B * S;
   const int lane_blk = slot / block_size;
 
   // this workgroup's share of the group's active tiles
@@ -412,31 +415,40 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   int pidx[TK];
   float pg[TK], plse = 0.f, pdl = 0.f;
   // per-thread constant part of the tile copy: row (token in tile) and column
-  int cp_row[PER], cp_off[PER];
+  int cp_row[PER], cp_col[PER];
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
     const int vi = tid + 512 * r;
     cp_row[r] = vi < VEC ? vi / (HD / 8) : TT;
-    cp_off[r] = cp_row[r] * D + h * HD + 8 * (vi % (HD / 8));
+    cp_col[r] = h * HD + 8 * (vi % (HD / 8));
   }
-  auto load_tile = [&](int tt) {
-    const long tok0 = (long)tt * TT;
-    const bf16_t* qb = q + tok0 * D;
-    const bf16_t* db = dout + tok0 * D;
-    const int rows = (int)min((long)TT, ntok - tok0);
+  // Tokens of a tile (rows of this thread's copies, and row tid < TT for the
+  // routing / statistics), fetched from the token order one tile ahead of the
+  // data loads that use them, so those loads do not wait on the order.
+  const int32_t* ord = order_table(order);
+  long rtok[PER], ttok = -1;
+  auto fetch_tokens = [&](int tt) {
+    const long pos0 = (long)tt * TT;
+    const int rows = (int)min((long)TT, ntok - pos0);
+#pragma unroll
+    for (int r = 0; r < PER; ++r) rtok[r] = cp_row[r] < rows ? order_token(ord, pos0 + cp_row[r], ntok) : -1;
+    ttok = (tid < TT && tid < rows) ? order_token(ord, pos0 + tid, ntok) : -1;
+  };
+  auto load_tile = [&]() {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
-      if (cp_row[r] < rows) {
-        qv = *reinterpret_cast<const uint4*>(qb + cp_off[r]);
-        dv4 = *reinterpret_cast<const uint4*>(db + cp_off[r]);
+      if (rtok[r] >= 0) {
+        const long off = rtok[r] * D + cp_col[r];
+        qv = *reinterpret_cast<const uint4*>(q + off);
+        dv4 = *reinterpret_cast<const uint4*>(dout + off);
       }
       qreg[r] = qv;
       dreg[r] = dv4;
     }
     if (tid < TT) {
-      const long tk = tok0 + tid;
-      const bool ok = tk < ntok;
+      const bool ok = ttok >= 0;
+      const long tk = ok ? ttok : 0;
 #pragma unroll
       for (int t = 0; t < TK; ++t) {
         pidx[t] = (ok && t < topk) ? top_idx[tk * topk + t] : -1;
@@ -484,12 +496,17 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     }
   };
 
-  if (i_begin < i_end) load_tile(tiles[i_begin]);
+  if (i_begin < i_end) {
+    fetch_tokens(tiles[i_begin]);
+    load_tile();
+  }
+  if (i_begin + 1 < i_end) fetch_tokens(tiles[i_begin + 1]);
   for (int it = i_begin; it < i_end; ++it) {
     __syncthreads();  // the previous tile's LDS reads are done
     store_tile();
     __syncthreads();
-    if (it + 1 < i_end) load_tile(tiles[it + 1]);  // in flight during the math below
+    if (it + 1 < i_end) load_tile();                       // in flight during the math below
+    if (it + 2 < i_end) fetch_tokens(tiles[it + 2]);       // the tokens of the tile after
 
     // ---- S = Q K^T and dP = dO V^T for this wave's 32 tokens x 32 slots
     f32x16 acc_s = f32x16{}, acc_p = f32x16{};
@@ -638,12 +655,13 @@ template <int HD, int SG, bool AL, int TK>
 static void dq_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
                     const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
                     hipStream_t st) {
-  const int n_tiles = (d.S + 127) / 128;
+  const long N = (long)d.B * d.S;
+  const int n_tiles = (int)((N + 127) / 128);
   const float scale = read_scale(HD);
   NAYLIS_TIMED("read_bwd_dq", st,
-               hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(256), 0, st,
+               hipLaunchKernelGGL((read_bwd_dq_kernel<HD, SG, AL, TK>), dim3(d.H * n_tiles), dim3(256), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)o,
-                                  (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.B, d.S, d.H, d.L, d.E,
+                                  (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.order, N, d.H, d.L, d.E,
                                   d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
 }
 
@@ -701,8 +719,8 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
   const int n_tt = read_bwd_n_ttiles(d);
   if (n_tt > 0)
     NAYLIS_TIMED("read_tile_lists", st,
-                 hipLaunchKernelGGL(read_tile_flags_kernel, dim3(n_tt), dim3(64), 0, st, top_idx, tile_flags, ntok, d.E,
-                                    d.topk));
+                 hipLaunchKernelGGL(read_tile_flags_kernel, dim3(n_tt), dim3(64), 0, st, top_idx, d.order, tile_flags,
+                                    ntok, d.E, d.topk));
   NAYLIS_TIMED("read_tile_lists", st,
                hipLaunchKernelGGL(read_tile_lists_kernel, dim3(read_lq(d.L) / 128), dim3(256), 0, st, tile_flags, list,
                                   count, n_tt, d.E, d.L, d.block_size));
@@ -718,8 +736,9 @@ static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t
   NAYLIS_TIMED("read_bwd_dkdv", st,
                hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(512), 0,
                                   st, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
-                                  (const bf16_t*)dout, lse, delta, list, count, dkp, dvp, d.B, d.S, d.H, d.L, Lq, d.E,
-                                  d.block_size, d.topk, alpha, nc, read_bwd_n_ttiles(d)));
+                                  (const bf16_t*)dout, lse, delta, list, count, dkp, dvp, d.order,
+                                  (long)d.B * d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc,
+                                  read_bwd_n_ttiles(d)));
 }
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,

@@ -10,6 +10,23 @@ constexpr int kMaxBlocks = 1024;  // bank blocks (flags live in LDS)
 constexpr int kMaxGroups = 512;   // slot groups of 32 over the whole bank (L <= 16384)
 constexpr int kReadWaves = 8;     // waves (x 32 tokens) per forward / dQ workgroup
 
+// A token-order buffer (read_order.hip) is 1 + N int32: word 0 is 1 when
+// words 1..N hold a grouped order, 0 for sequence order.  order_table()
+// returns the table to follow, or nullptr for sequence order (read once per
+// kernel: a uniform scalar load), so sequence order costs no loads.
+__device__ __forceinline__ const int32_t* order_table(const int32_t* __restrict__ buf) {
+  return (buf != nullptr && buf[0] != 0) ? buf + 1 : nullptr;
+}
+
+// Token at position `pos` of an order table (nullptr: sequence order).  An
+// entry outside [0, N) falls back to `pos`, so a malformed order can produce
+// wrong results but never an out-of-bounds access.
+__device__ __forceinline__ long order_token(const int32_t* __restrict__ order, long pos, long N) {
+  if (order == nullptr) return pos;
+  const long t = order[pos];
+  return (t >= 0 && t < N) ? t : pos;
+}
+
 // Per-token routing held in registers: block ids and log2 of the clamped
 // gates, as mom_kernels/reference.py:23 builds them (log(max(g, 1e-9))).
 // TK is the compiled maximum of selections per token (>= the runtime topk).

@@ -7,8 +7,10 @@
 // never materialised: it is one scalar per (token, bank block), folded into
 // the exp2 argument together with the running max.
 //
-// Work decomposition: one workgroup = (b, h, 256 tokens), 8 waves, each wave
-// owns 32 tokens (one MFMA column each).  The workgroup walks the slot groups
+// Work decomposition: one workgroup = (h, 256 consecutive positions of the
+// token order), 8 waves, each wave owns 32 tokens (one MFMA column each).
+// The order (read_order.hip) groups tokens of the whole batch by the blocks
+// they select, so a workgroup's tokens share few blocks.  The workgroup walks the slot groups
 // (SG slots) of the bank blocks any of its tokens selects, streaming K and V
 // rows through double-buffered LDS (one barrier per group, the next group's
 // copy in flight during the math); a wave computes a group only when one of
@@ -28,8 +30,8 @@ template <int HD, int SG, bool ALIGNED, int TK>
 __global__ __launch_bounds__(512) void read_fwd_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
-    float* __restrict__ lse, int B, int S, int H, int L, int E, int block_size, int topk, float alpha,
-    int n_tiles) {
+    float* __restrict__ lse, const int32_t* __restrict__ order, long N, int H, int L, int E, int block_size,
+    int topk, float alpha, int n_tiles) {
   constexpr int NW = kReadWaves;
   constexpr int NT = 64 * NW;
   constexpr int TM = 32 * NW;       // tokens per workgroup
@@ -46,20 +48,20 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
   __shared__ uint16_t groups[kMaxGroups];
   __shared__ int n_active;
 
-  const int G = B * H * n_tiles;
+  const int G = H * n_tiles;
   const int wid = xcd_remap(blockIdx.x, G);
   const int tile = wid % n_tiles;
-  const int b = (wid / n_tiles) % B;
-  const int h = wid / (n_tiles * B);
+  const int h = wid / n_tiles;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const int s_tok = tile * TM + wave * 32 + col;
-  const bool tok_ok = s_tok < S;
-  const long tok = (long)b * S + s_tok;
+  const long pos = (long)tile * TM + wave * 32 + col;  // position in the token order
+  const bool tok_ok = pos < N;
+  const int32_t* ord = order_table(order);
+  const long tok = tok_ok ? order_token(ord, pos, N) : 0;  // flattened b*S + s
   const int D = H * HD;
 
   // ---- routing of this lane's token; active-block flags of the workgroup
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
         *reinterpret_cast<bf16x8*>(dst + 8) = hi;
       }
     }
-    if (g == 0) lse[(long)h * B * S + tok] = m_run + log2f(l_run);
+    if (g == 0) lse[(long)h * N + tok] = m_run + log2f(l_run);
   }
 }
 
@@ -285,12 +287,13 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
 template <int HD, int SG, bool AL, int TK>
 static void fwd_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                      float* lse, const ReadDims& d, hipStream_t st) {
-  const int n_tiles = (d.S + 32 * kReadWaves - 1) / (32 * kReadWaves);
+  const long N = (long)d.B * d.S;
+  const int n_tiles = (int)((N + 32 * kReadWaves - 1) / (32 * kReadWaves));
   const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.B * d.H * n_tiles), dim3(64 * kReadWaves), 0, st,
+               hipLaunchKernelGGL((read_fwd_kernel<HD, SG, AL, TK>), dim3(d.H * n_tiles), dim3(64 * kReadWaves), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (bf16_t*)out, lse,
-                                  d.B, d.S, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
+                                  d.order, N, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
 }
 
 // Slot-group size of the forward: NAYLIS_READ_FWD_SG=128 selects 128-slot

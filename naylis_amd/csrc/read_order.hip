@@ -1,0 +1,236 @@
+// Token order for the read.  The bank's K/V rows are shared by every token of
+// the batch, so the read may process tokens in any order: grouping tokens by
+// the blocks they select makes a tile of consecutive positions touch fewer
+// blocks, and the read's work is proportional to the (tile, block) pairs it
+// touches.  The reference walks tokens in sequence order with BLOCK_M = 128
+// (mom_kernels/triton_gpu.py:50, 98) and skips blocks no token of the tile
+// selects; the same skipping applies here to the reordered tiles.
+//
+//   key(t) = the sorted pair of token t's two selected blocks (top-2 over at
+//            most 32 blocks: at most 1024 keys; other routings keep sequence
+//            order)
+//   sorted = tokens in ascending key order, sequence order within a key
+//            (a stable counting sort: the order is a function of top_idx only,
+//            so the forward and the backward get the same one)
+//   order  = sorted, if it lowers the number of (128-token tile, block) pairs
+//            by at least 10 %; otherwise the identity (routing that is already
+//            coherent within tiles, e.g. one logit bias per tile).  Calls with
+//            more than 2^18 tokens keep the identity.  For block pairs the
+//            grouped order's (tile, block) count follows exactly from the key
+//            offsets, so the decision needs no pass over the grouped order.
+//
+// Kernels: (1) per 1024-token chunk, each token's rank among the chunk's
+// earlier tokens of the same key, the chunk's key histogram and its tiles'
+// sequence-order block counts; (2) per chunk, key offsets (a scan over the
+// histograms), the decision, and the placement of the chunk's tokens.
+#include "launch.h"
+#include "read_common.h"
+#include "timing.h"
+
+namespace naylis {
+
+constexpr int kOrdChunk = 1024;  // tokens per chunk of the local ranking (one thread each)
+constexpr int kOrdTile = 128;    // tile of the decision (the reference's BLOCK_M)
+constexpr int kOrdWaves = kOrdChunk / 64;
+constexpr int kOrdMaxE = 32;     // grouping by block pair: E <= 32 (at most 1024 keys), top-2
+
+// Above this many tokens the scatter's scan over all chunks grows too long;
+// such calls keep the sequence order.
+constexpr long kOrdMaxTokens = 1L << 18;
+
+static bool ord_grouping(long N, int E, int topk) { return topk == 2 && E <= kOrdMaxE && N <= kOrdMaxTokens; }
+
+struct OrderWs {
+  size_t keys, rank, hist, seqcnt, total;
+};
+
+static OrderWs plan_order_ws(long N, int E) {
+  auto a256 = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const long nchunks = (N + kOrdChunk - 1) / kOrdChunk;
+  const long ntiles = (N + kOrdTile - 1) / kOrdTile;
+  OrderWs w{};
+  size_t off = 0;
+  w.keys = off;
+  off += a256((size_t)N * 2);
+  w.rank = off;
+  off += a256((size_t)N * 4);
+  w.hist = off;
+  off += a256((size_t)nchunks * E * E * 4);
+  w.seqcnt = off;
+  off += a256((size_t)ntiles * 4);
+  w.total = off;
+  return w;
+}
+
+// (1) per chunk of 1024 tokens: key = sorted block pair, rank among the
+// chunk's earlier tokens of the same key (a 64-lane comparison loop inside a
+// wave, per-wave key counts across waves), the chunk's key histogram, and
+// the distinct-block count of each 128-token tile in sequence order.
+__global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* __restrict__ top_idx,
+                                                                uint16_t* __restrict__ keys, int32_t* __restrict__ rank,
+                                                                int32_t* __restrict__ hist,
+                                                                int32_t* __restrict__ seqcnt, long N, int E) {
+  __shared__ int32_t wcnt[kOrdWaves][kOrdMaxE * kOrdMaxE];
+  __shared__ uint32_t wmask[kOrdWaves];
+  const int nkeys = E * E;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long tok = (long)blockIdx.x * kOrdChunk + tid;
+  const bool real = tok < N;
+  int key = -1;
+  uint32_t mask = 0;
+  if (real) {
+    const int a0 = top_idx[tok * 2], b0 = top_idx[tok * 2 + 1];
+    const int a = min(max(a0, 0), E - 1), b = min(max(b0, 0), E - 1);
+    key = a < b ? a * E + b : b * E + a;
+    if (a0 >= 0 && a0 < E) mask |= 1u << a0;
+    if (b0 >= 0 && b0 < E) mask |= 1u << b0;
+  }
+  for (int i = tid; i < kOrdWaves * nkeys; i += kOrdChunk) wcnt[i / nkeys][i % nkeys] = 0;
+  int before = 0, after = 0;
+#pragma unroll 8
+  for (int j = 0; j < 64; ++j) {
+    const int kj = __shfl(key, j, 64);
+    before += (j < lane && kj == key);
+    after += (j > lane && kj == key);
+  }
+  for (int o = 32; o > 0; o >>= 1) mask |= __shfl_xor(mask, o, 64);
+  if (lane == 0) wmask[wave] = mask;
+  __syncthreads();
+  if (real && after == 0) wcnt[wave][key] = before + 1;  // the last lane of its key in this wave
+  if (tid < kOrdChunk / kOrdTile) {                     // a 128-token tile = 2 waves
+    const long t = (long)blockIdx.x * (kOrdChunk / kOrdTile) + tid;
+    if (t * kOrdTile < N) seqcnt[t] = __popc(wmask[2 * tid] | wmask[2 * tid + 1]);
+  }
+  __syncthreads();
+  if (tid < nkeys) {
+    int run = 0;
+    for (int w = 0; w < kOrdWaves; ++w) {
+      const int c = wcnt[w][tid];
+      wcnt[w][tid] = run;
+      run += c;
+    }
+    hist[(long)blockIdx.x * nkeys + tid] = run;
+  }
+  __syncthreads();
+  if (real) {
+    keys[tok] = (uint16_t)key;
+    rank[tok] = wcnt[wave][key] + before;
+  }
+}
+
+// (2) per chunk: key offsets = (tokens of smaller keys) + (tokens of the same
+// key in earlier chunks).  Every workgroup also evaluates the decision from
+// the same data: in the grouped order a tile's blocks are the union of the
+// block pairs of the keys whose segments overlap it, which the offsets give
+// exactly.  Grouping is kept when it lowers the (tile, block) pairs by at
+// least 10 %: then order[1 + offset + rank] = token and the mode word
+// order[0] = 1; otherwise order[0] = 0 and the table is not written.
+__global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t* __restrict__ keys,
+                                                                  const int32_t* __restrict__ rank,
+                                                                  const int32_t* __restrict__ hist,
+                                                                  const int32_t* __restrict__ seqcnt,
+                                                                  int32_t* __restrict__ order, long N, int E,
+                                                                  int nchunks) {
+  __shared__ int32_t off[kOrdMaxE * kOrdMaxE];
+  __shared__ int32_t ends[kOrdMaxE * kOrdMaxE];  // inclusive scan of the key totals
+  __shared__ long red[2][kOrdWaves];
+  const int nkeys = E * E;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x;
+  int before = 0, all = 0;
+  if (tid < nkeys) {
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {  // 16 independent loads in flight
+      int h[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) h[u] = c0 + u < nchunks ? hist[(long)(c0 + u) * nkeys + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        all += h[u];
+        before += (c0 + u < c) ? h[u] : 0;
+      }
+    }
+    ends[tid] = all;
+  }
+  __syncthreads();
+  for (int st = 1; st < nkeys; st <<= 1) {  // inclusive scan over keys
+    int add = 0;
+    if (tid < nkeys && tid >= st) add = ends[tid - st];
+    __syncthreads();
+    if (tid < nkeys) ends[tid] += add;
+    __syncthreads();
+  }
+  if (tid < nkeys) off[tid] = ends[tid] - all + before;
+  // (tile, block) pairs of both orders
+  const long ntiles = (N + kOrdTile - 1) / kOrdTile;
+  long seq = 0, grp = 0;
+  for (long t = tid; t < ntiles; t += kOrdChunk) {
+    seq += seqcnt[t];
+    const long p0 = t * kOrdTile, p1 = min(N, p0 + kOrdTile);
+    int lo = 0, hi = nkeys - 1;  // first key whose segment ends after p0
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ends[mid] > p0) hi = mid; else lo = mid + 1;
+    }
+    uint32_t mask = 0;
+    for (int key = lo; key < nkeys; ++key) {
+      const int start = key > 0 ? ends[key - 1] : 0;
+      if (start >= p1) break;
+      if (ends[key] > start) mask |= (1u << (key / E)) | (1u << (key % E));
+    }
+    grp += __popc(mask);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    seq += __shfl_xor(seq, o, 64);
+    grp += __shfl_xor(grp, o, 64);
+  }
+  if (lane == 0) {
+    red[0][wave] = seq;
+    red[1][wave] = grp;
+  }
+  __syncthreads();
+  long s_all = 0, g_all = 0;
+  for (int w = 0; w < kOrdWaves; ++w) {
+    s_all += red[0][w];
+    g_all += red[1][w];
+  }
+  const bool grouped = g_all * 10 <= s_all * 9;
+  if (c == 0 && tid == 0) order[0] = grouped ? 1 : 0;  // the mode word
+  const long tok = (long)c * kOrdChunk + tid;
+  if (tok >= N || !grouped) return;
+  const long dst = (long)off[keys[tok]] + rank[tok];
+  if (dst >= 0 && dst < N) order[1 + dst] = (int32_t)tok;
+}
+
+// sequence order: only the mode word
+__global__ __launch_bounds__(64) void order_sequence_kernel(int32_t* __restrict__ order) {
+  if (threadIdx.x == 0) order[0] = 0;
+}
+
+size_t read_order_ws_bytes(long N, int E, int topk) {
+  return ord_grouping(N, E, topk) ? plan_order_ws(N, E).total : 256;
+}
+
+hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, int32_t* order, void* ws,
+                             hipStream_t st) {
+  if (N == 0) return hipSuccess;
+  if (!ord_grouping(N, E, topk)) {
+    NAYLIS_TIMED("read_order", st, hipLaunchKernelGGL(order_sequence_kernel, dim3(1), dim3(64), 0, st, order));
+    return hipGetLastError();
+  }
+  const OrderWs w = plan_order_ws(N, E);
+  char* base = (char*)ws;
+  uint16_t* keys = (uint16_t*)(base + w.keys);
+  int32_t* rank = (int32_t*)(base + w.rank);
+  int32_t* hist = (int32_t*)(base + w.hist);
+  int32_t* seqcnt = (int32_t*)(base + w.seqcnt);
+  const int nchunks = (int)((N + kOrdChunk - 1) / kOrdChunk);
+  NAYLIS_TIMED("read_order", st,
+               hipLaunchKernelGGL(order_local_kernel, dim3(nchunks), dim3(kOrdChunk), 0, st, top_idx, keys, rank, hist,
+                                  seqcnt, N, E));
+  NAYLIS_TIMED("read_order", st,
+               hipLaunchKernelGGL(order_scatter_kernel, dim3(nchunks), dim3(kOrdChunk), 0, st, keys, rank, hist,
+                                  seqcnt, order, N, E, nchunks));
+  return hipGetLastError();
+}
+
+}  // namespace naylis

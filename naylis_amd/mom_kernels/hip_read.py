@@ -17,9 +17,28 @@ def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+def read_order(top_idx, num_blocks):
+    """The token order the read uses for this routing (C ABI:
+    naylis_mom_read_order): an int32 tensor of 1 + B*S words, word 0 = 1 when
+    words 1.. hold the grouped position -> token table, 0 for sequence order.
+    Launched on the current stream; top_idx must be int32 (B, S, k)."""
+    lib = _lib.load()
+    B, S, topk = top_idx.shape
+    dev = top_idx.device
+    order = torch.empty((1 + B * S,), device=dev, dtype=torch.int32)
+    ows = _workspace(lib.naylis_mom_read_order_workspace_bytes(B, S, num_blocks, topk), dev)
+    with _lib.on_device(dev):
+        rc = lib.naylis_mom_read_order(top_idx.data_ptr(), order.data_ptr(), ows.data_ptr(), ows.numel(),
+                                       B, S, num_blocks, topk, _lib.stream_of(dev))
+    _lib.check(rc)
+    return order
+
+
 class MomReadFunction(torch.autograd.Function):
-    """Forward saves (q, k, v, top_idx, top_gates, o, lse); backward runs the
-    dq / dk-dv / reduce launches of the library."""
+    """Forward computes the token order (tokens grouped by selected blocks, or
+    sequence order when that does not pay) and saves (q, k, v, top_idx,
+    top_gates, order, o, lse); backward runs the dq / dk-dv / reduce launches
+    of the library with the same order."""
 
     @staticmethod
     def forward(ctx, q_sh, k, v, top_idx, top_gates, num_blocks, block_size):
@@ -29,20 +48,22 @@ class MomReadFunction(torch.autograd.Function):
         dev = q_sh.device
         out = torch.empty_like(q_sh)
         lse = torch.empty((H, B, S), device=dev, dtype=torch.float32)
+        order = read_order(top_idx, num_blocks)  # mode word + table
         with _lib.on_device(dev):
+            st = _lib.stream_of(dev)
             rc = lib.naylis_mom_read_fwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), None, 0,
-                B, S, H, HD, num_blocks, block_size, topk, _lib.stream_of(dev))
+                order.data_ptr(), out.data_ptr(), lse.data_ptr(), None, 0,
+                B, S, H, HD, num_blocks, block_size, topk, st)
         _lib.check(rc)
-        ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, out, lse)
+        ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, order, out, lse)
         ctx.geom = (num_blocks, block_size)
         return out
 
     @staticmethod
     def backward(ctx, dout):
         lib = _lib.load()
-        q_sh, k, v, top_idx, top_gates, out, lse = ctx.saved_tensors
+        q_sh, k, v, top_idx, top_gates, order, out, lse = ctx.saved_tensors
         num_blocks, block_size = ctx.geom
         B, S, H, HD = q_sh.shape
         topk = top_idx.shape[-1]
@@ -61,7 +82,8 @@ class MomReadFunction(torch.autograd.Function):
         with _lib.on_device(dev):
             rc = lib.naylis_mom_read_bwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                order.data_ptr(), out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                dv.data_ptr(),
                 dgates.data_ptr(), ws.data_ptr(), ws.numel(),
                 B, S, H, HD, num_blocks, block_size, topk, _lib.stream_of(dev))
         _lib.check(rc)

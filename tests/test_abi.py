@@ -47,8 +47,8 @@ READ_OK = dict(B=2, S=64, H=2, hd=16, nb=4, bs=16, k=2)
 
 def read_fwd(lib, **kw):
     a = dict(READ_OK, **kw)
-    return lib.naylis_mom_read_fwd(1, 1, 1, 1, 1, 1, 1, None, 0, a["B"], a["S"], a["H"], a["hd"], a["nb"], a["bs"],
-                                   a["k"], None)
+    return lib.naylis_mom_read_fwd(1, 1, 1, 1, 1, None, 1, 1, None, 0, a["B"], a["S"], a["H"], a["hd"], a["nb"],
+                                   a["bs"], a["k"], None)
 
 
 @pytest.mark.parametrize("bad", [dict(hd=96), dict(hd=256), dict(hd=8), dict(k=0), dict(k=9), dict(k=5, nb=4),
@@ -62,15 +62,20 @@ def test_read_rejects_bad_arguments(lib, bad):
 
 
 def test_read_null_pointers_and_workspace(lib):
-    rc = lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, 0, 2, 64, 2, 16, 4, 16, 2, None)
+    rc = lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, 0, 2, 64, 2, 16, 4, 16, 2, None)
     assert rc == _lib.NAYLIS_ERR_ARG and b"null" in lib.naylis_mom_last_error()
     ws = lib.naylis_mom_read_workspace_bytes(8, 2048, 16, 64, 8, 128, 2)
     assert ws > 0
-    rc = lib.naylis_mom_read_bwd(*([1] * 12), 1, ws - 1, 8, 2048, 16, 64, 8, 128, 2, None)
+    rc = lib.naylis_mom_read_bwd(*([1] * 13), 1, ws - 1, 8, 2048, 16, 64, 8, 128, 2, None)
     assert rc == _lib.NAYLIS_ERR_WORKSPACE
     # empty sequences are a valid no-op for the forward
-    assert lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, 0, 2, 0, 2, 16, 4, 16, 2,
+    assert lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, 0, 2, 0, 2, 16, 4, 16, 2,
                                    None) == _lib.NAYLIS_OK
+    # the token order: argument checks, workspace, empty input
+    assert lib.naylis_mom_read_order_workspace_bytes(8, 2048, 8, 2) > 0
+    assert lib.naylis_mom_read_order_workspace_bytes(8, 2048, 8, 9) == 0
+    assert lib.naylis_mom_read_order(1, 1, 1, 1, 8, 2048, 8, 2, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert lib.naylis_mom_read_order(None, None, None, 0, 0, 2048, 8, 2, None) == _lib.NAYLIS_OK
 
 
 def test_router_and_bank_reject_bad_arguments(lib):
