@@ -7,7 +7,7 @@ Workload ("config2"): one Naylis MoM layer in bf16,
 forward + backward at the training shape B=8, T=2048, d=1024, 16 heads x 64,
 bank 8 blocks x 128 slots x 1024 rescaled to Frobenius norm 63, router
 d -> 32 -> 8 with top-2, ReZero scale 1.0, Gumbel noise off.  x is RMS-normed
-N(0,1) in bf16, dy ~ N(0,1); router weights, prefix mean and routing in fp32.
+N(0,1) in bf16, dy ~ N(0,1) in fp32 (the dtype of y); router weights, prefix mean and routing in fp32.
 Random-init weights, synthetic data.  A step is y = layer(x, M); y.backward(dy)
 with all parameter gradients.
 
@@ -66,7 +66,7 @@ def build(cfg, device):
     x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
     x = x.bfloat16().to(device).requires_grad_(True)
     gd = torch.Generator().manual_seed(2)
-    dy = torch.randn(B, T, D, generator=gd).bfloat16().to(device)
+    dy = torch.randn(B, T, D, generator=gd).to(device)  # fp32: the dtype of y (ReZero promotes to fp32)
     if cfg["tile_bias"]:
         lo, hi = cfg["tile_bias"]
         bias = torch.zeros(B, T, E)
@@ -267,7 +267,7 @@ def main(argv=None):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights, RMS-normed N(0,1) x, N(0,1) dy)",
+        "data": "synthetic (random-init weights, RMS-normed N(0,1) x in bf16, N(0,1) dy in fp32)",
         "config": {"workload": f"{args.workload}: MoM layer fwd+bwd B={B} T={T} d={D} heads={H}x{D // H} "
                                f"bank {E}x{BS} top-{cfg['K']} rank {cfg['R']}",
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},

@@ -424,17 +424,33 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   }
   // Tokens of a tile (rows of this thread's copies, and row tid < TT for the
   // routing / statistics), fetched from the token order one tile ahead of the
-  // data loads that use them, so those loads do not wait on the order.
+  // data loads that use them.  The raw order entries are only checked when
+  // those loads are issued (next iteration, after the loop's wait for the
+  // previous tile), so fetching them never makes the wave wait for the tile
+  // loads just issued.
   const int32_t* ord = order_table(order);
-  long rtok[PER], ttok = -1;
+  long rpos[PER], tpos = -1;  // position in the order, -1: no token
+  int rraw[PER], traw = 0;    // the order's entry at that position
   auto fetch_tokens = [&](int tt) {
     const long pos0 = (long)tt * TT;
     const int rows = (int)min((long)TT, ntok - pos0);
 #pragma unroll
-    for (int r = 0; r < PER; ++r) rtok[r] = cp_row[r] < rows ? order_token(ord, pos0 + cp_row[r], ntok) : -1;
-    ttok = (tid < TT && tid < rows) ? order_token(ord, pos0 + tid, ntok) : -1;
+    for (int r = 0; r < PER; ++r) {
+      rpos[r] = cp_row[r] < rows ? pos0 + cp_row[r] : -1;
+      if (ord != nullptr && rpos[r] >= 0) rraw[r] = ord[rpos[r]];
+    }
+    tpos = (tid < TT && tid < rows) ? pos0 + tid : -1;
+    if (ord != nullptr && tpos >= 0) traw = ord[tpos];
+  };
+  auto token_at = [&](long pos, int raw) -> long {
+    if (pos < 0 || ord == nullptr) return pos;
+    return (raw >= 0 && raw < ntok) ? (long)raw : pos;  // a malformed entry falls back to the position
   };
   auto load_tile = [&]() {
+    long rtok[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) rtok[r] = token_at(rpos[r], rraw[r]);
+    const long ttok = token_at(tpos, traw);
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
