@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 2
+#define NAYLIS_MOM_ABI_VERSION 3
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -135,12 +135,23 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
 /* Backward of the router: any of d_gates (B,T,k), d_probs (B,T,E), d_logits
  * (B,T,E) may be NULL (no gradient from that output).  Writes dx (same dtype
  * and shape as x), dw_down (R, D) and dw_up (E, R), both fp32, reduced over
- * all tokens in a fixed order. */
+ * all tokens in a fixed order.  dx_accumulate != 0 adds the router's input
+ * gradient to the dx the caller passes (the sum of x's gradients from the
+ * router and from the query projection that autograd would form, with one
+ * bf16 rounding of the fp32 sum); it needs bf16 x, D a multiple of 128,
+ * R <= 64 and 16-byte aligned x / dx (NAYLIS_ERR_ARG otherwise).
+ *
+ * For bf16 x with D % 128 == 0 (D <= 2048) and no h_out, the forward projects x first
+ * (y = x W_down^T, W_down split exactly into three bf16 planes on the bf16
+ * MFMA) and scans the R-wide y in fp64: the linear-algebra identity
+ * cumsum(x) W^T = cumsum(x W^T) of model.py:169-187, with fp32-GEMM accuracy
+ * and indices equal outside near-ties; with h_out (or fp32 x) it scans x
+ * itself and h_out is bit-exact. */
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                          const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
-                          void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
-                          int64_t E, int64_t top_k, void* stream);
+                          const float* d_probs, const float* d_logits, void* dx, int dx_accumulate, float* dw_down,
+                          float* dw_up, void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D,
+                          int64_t R, int64_t E, int64_t top_k, void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

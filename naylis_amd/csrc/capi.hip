@@ -267,13 +267,16 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
 
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                          const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
-                          void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D, int64_t R,
-                          int64_t E, int64_t top_k, void* stream) {
+                          const float* d_probs, const float* d_logits, void* dx, int dx_accumulate, float* dw_down,
+                          float* dw_up, void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D,
+                          int64_t R, int64_t E, int64_t top_k, void* stream) {
   RouterDims d;
   int rc = check_router_dims(B, T, D, R, E, top_k, &d);
   if (rc) return rc;
   if ((rc = check_dtype(x_dtype, "mom_route"))) return rc;
+  if (dx_accumulate && B * T > 0 && !router_fast_bwd_ok(x, x_dtype == NAYLIS_DTYPE_BF16, dx, d))
+    return fail(NAYLIS_ERR_ARG,
+                "mom_route_bwd: dx_accumulate needs bf16 x, D a multiple of 128, R <= 64 and 16-byte aligned x / dx");
   if (!w_down || !w_up || !dw_down || !dw_up || !workspace)
     return fail(NAYLIS_ERR_ARG, "mom_route_bwd: null pointer argument");
   if (B * T > 0 && (!x || !act || !probs || !top_idx || !top_gates || !dx))
@@ -283,7 +286,7 @@ int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const
     return fail(NAYLIS_ERR_WORKSPACE, "mom_route_bwd: workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, w.total);
   return hip_status(launch_router_bwd(x, x_dtype == NAYLIS_DTYPE_BF16, w_down, w_up, act, probs, top_idx, top_gates,
-                                      d_gates, d_probs, d_logits, dx, dw_down, dw_up, workspace, d,
+                                      d_gates, d_probs, d_logits, dx, dx_accumulate != 0, dw_down, dw_up, workspace, d,
                                       (hipStream_t)stream),
                     "mom_route_bwd");
 }

@@ -118,6 +118,13 @@ __device__ __forceinline__ float wave_max_pair(float x) {
 }
 __device__ __forceinline__ float wave_sum_pair(float x) { return x + __shfl_xor(x, 32, 64); }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, not for its outstanding global loads (a __syncthreads() fence
+// would also drain those, serialising prefetches that are meant to stay in
+// flight across the barrier).  The "memory" clobber keeps the compiler from
+// moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for running maxima
 

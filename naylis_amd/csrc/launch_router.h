@@ -12,7 +12,7 @@ struct RouterDims {
 
 // Byte offsets into the caller's workspace.  The forward uses [0, fwd_total).
 struct RouterWs {
-  size_t carry, w, wt, scan_csum, dwup_part, dwd_part;
+  size_t carry, y, ycs, w, wt, scan_csum, dwup_part, dwd_part;
   size_t fwd_total, total;
 };
 
@@ -22,9 +22,25 @@ hipError_t launch_router_fwd(const void* x, bool x_bf16, const float* w_down, co
                              float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
                              float* act, float* h_out, void* ws, const RouterDims& d, hipStream_t st);
 
+// dx_accumulate: dx += the router's input gradient (one rounding of the fp32
+// sum) instead of dx = it.
 hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, const float* w_up, const float* act,
                              const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                             const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
-                             void* ws, const RouterDims& d, hipStream_t st);
+                             const float* d_probs, const float* d_logits, void* dx, bool dx_accumulate,
+                             float* dw_down, float* dw_up, void* ws, const RouterDims& d, hipStream_t st);
+
+// Fast path (router_fast.hip): bf16 x, projection before the prefix scan.
+bool router_fast_fwd_ok(const void* x, bool x_bf16, const float* w_down, const float* h_out, const RouterDims& d);
+bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const RouterDims& d);
+void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_up, const float* noise,
+                            float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
+                            float* act, float* y, double* ycs, const RouterDims& d, hipStream_t st);
+// fast backward (B1 + B2): w, its 32-token chunk sums, W~ and the dW_up
+// partials; returns the number of dW_up partials
+int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,
+                            const float* dg, const float* dp, const float* dl, const float* w_up, float* w,
+                            double* wcs, float* wt, float* dwup_part, const RouterDims& d, hipStream_t st);
+void launch_router_fast_dx(const void* x, const float* wt, const float* w_down, const void* dx_in, void* dx,
+                           float* dwd_part, const RouterDims& d, hipStream_t st);
 
 }  // namespace naylis

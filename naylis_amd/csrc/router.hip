@@ -21,6 +21,8 @@
 //   dx = W~ W_down          dW_down = W~^T x
 // (d h_s = dz_s W_down and dx_t = sum_{s>=t} dh_s / (s+1), so both the
 // reverse scan and the recomputation of h fold into W~).
+#include <algorithm>
+
 #include "launch_router.h"
 #include "common.h"
 #include "timing.h"
@@ -731,18 +733,23 @@ RouterWs plan_router_ws(const RouterDims& d) {
   size_t off = 0;
   w.carry = off;
   off += a256((size_t)d.B * n_chunks * d.D * 8);
+  w.y = off;  // fast path: y = x W_down^T and its per-chunk fp64 sums
+  off += a256((size_t)ntok * d.R * 4);
+  w.ycs = off;
+  off += a256((size_t)d.B * n_chunks * d.R * 8);
+  w.fwd_total = off;
   w.w = off;
   off += a256((size_t)ntok * d.R * 4);
   w.wt = off;
   off += a256((size_t)ntok * d.R * 4);
+  // sized for the larger of the two paths: 32-token chunks (fast) vs 64 (exact-h)
   w.scan_csum = off;
-  off += a256((size_t)d.B * ((d.T + kScanChunk - 1) / kScanChunk) * d.R * 8);
+  off += a256((size_t)d.B * n_chunks * d.R * 8);
   w.dwup_part = off;
-  off += a256((size_t)n_tok_blocks * d.E * d.R * 4);
+  off += a256((size_t)std::max<long>(n_tok_blocks, (long)d.B * n_chunks) * d.E * d.R * 4);
   w.dwd_part = off;
   off += a256((size_t)((ntok + kDxRange - 1) / kDxRange) * d.R * d.D * 4);
   w.total = off;
-  w.fwd_total = w.w;
   return w;
 }
 
@@ -791,6 +798,12 @@ static void fwd_x(const void* x, const float* w_down, const float* w_up, const f
 hipError_t launch_router_fwd(const void* x, bool x_bf16, const float* w_down, const float* w_up, const float* noise,
                              float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
                              float* act, float* h_out, void* ws, const RouterDims& d, hipStream_t st) {
+  if (router_fast_fwd_ok(x, x_bf16, w_down, h_out, d)) {
+    const RouterWs w = plan_router_ws(d);
+    launch_router_fast_fwd(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act,
+                           (float*)((char*)ws + w.y), (double*)((char*)ws + w.ycs), d, st);
+    return hipGetLastError();
+  }
   const RouterWs w = plan_router_ws(d);
   if (x_bf16)
     fwd_x<bf16_t>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, h_out, (char*)ws, w, d,
@@ -828,8 +841,11 @@ static void bwd_dx(const void* x, const float* wt, const float* w_down, void* dx
 
 hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, const float* w_up, const float* act,
                              const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                             const float* d_probs, const float* d_logits, void* dx, float* dw_down, float* dw_up,
-                             void* ws, const RouterDims& d, hipStream_t st) {
+                             const float* d_probs, const float* d_logits, void* dx, bool dx_accumulate,
+                             float* dw_down, float* dw_up, void* ws, const RouterDims& d, hipStream_t st) {
+  // accumulation into dx exists on the fast path only (bf16 x, D % 128 == 0);
+  // the C ABI rejects other requests before this point
+  if (dx_accumulate && !router_fast_bwd_ok(x, x_bf16, dx, d)) return hipErrorInvalidValue;
   const RouterWs w = plan_router_ws(d);
   char* base = (char*)ws;
   float* wbuf = (float*)(base + w.w);
@@ -845,6 +861,18 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
                        dim3(256), 0, st, dwd_part, dw_down, nwd, 0));
     NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,
                        0));
+    return hipGetLastError();
+  }
+  const bool fast = router_fast_bwd_ok(x, x_bf16, dx, d);
+  if (fast) {
+    const int n_up = launch_router_fast_scan(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf,
+                                             (double*)(base + w.scan_csum), wt, dwup_part, d, st);
+    launch_router_fast_dx(x, wt, w_down, dx_accumulate ? dx : nullptr, dx, dwd_part, d, st);
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)),
+                                                         dim3(256), 0, st, dwd_part, dw_down, nwd,
+                                                         (int)((ntok + kDxRange - 1) / kDxRange)));
+    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)),
+                                                         dim3(256), 0, st, dwup_part, dw_up, nwu, n_up));
     return hipGetLastError();
   }
   if (d.E <= 8 && d.topk <= 2)
@@ -868,7 +896,7 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
     bwd_dx<bf16_t>(x, wt, w_down, dx, dwd_part, d, st);
   else
     bwd_dx<float>(x, wt, w_down, dx, dwd_part, d, st);
-  const int n_dx_chunks = (int)((ntok + kDxRange - 1) / kDxRange);
+  const int n_dx_chunks = (int)((ntok + kDxRange - 1) / kDxRange);  // both paths: 256-token ranges
   NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)), dim3(256),
                      0, st, dwd_part, dw_down, nwd, n_dx_chunks));
   NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,

@@ -1,0 +1,673 @@
+// Router fast path for bf16 activations (gfx950): projection first, then the
+// causal prefix over the R-wide projection.
+//
+// The reference forms the prefix mean h_t = cumsum(x)_t / (t+1) and projects
+// it, z_t = h_t W_down^T (model.py:169-187).  The projection is linear, so
+//   z_t = (sum_{s<=t} y_s) / (t+1),   y_s = x_s W_down^T,
+// and the D-wide prefix never has to exist: x is read once, by one bf16 MFMA
+// GEMM, and the scan runs over R = 32 columns.  bf16 x is exact in bf16;
+// W_down (fp32) is split exactly into three bf16 planes w = w1 + w2 + w3
+// (w1 = bf16(w), w2 = bf16(w - w1), w3 = bf16(w - w1 - w2); 3 x 8 significant
+// bits cover fp32's 24), so every MFMA product is an exact fp32 product and y
+// carries only the fp32 accumulation error of an fp32 GEMM (about 2^-24
+// sqrt(D) relative), as the reference's own sgemm does.  The prefix sums run
+// in fp64.  z therefore agrees with the reference to fp32 GEMM accuracy (not
+// bitwise: the reference rounds h to fp32 before projecting); top-k indices
+// agree outside near-ties, the same criterion as the exact-h path, which
+// stays in router.hip for callers that ask for h itself or pass fp32 x.
+//
+// Backward: dx = W~ W_down (+ the caller's dx, accumulated in fp32 before the
+// single bf16 rounding) and dW_down = W~^T x, W~ the reverse prefix of
+// w_t = dz_t / (t+1) (router.hip).  W~ enters the MFMA as a bf16 hi/lo pair,
+// W_down as a hi/lo pair; the three significant products give 2^-16 relative
+// accuracy for the bf16 dx, and x is exact for dW_down.
+#include <type_traits>
+
+#include "common.h"
+#include "launch_router.h"
+#include "timing.h"
+
+namespace naylis {
+
+constexpr int kFastChunk = 32;    // tokens per projection / head workgroup
+constexpr int kFastDxRange = 256; // tokens per dx workgroup (one dW_down partial)
+constexpr int kFastDxSlab = 128;  // features per dx workgroup
+
+// Split 8 fp32 values into three bf16 planes whose sum is the input exactly.
+__device__ __forceinline__ void split3(const f32x4& a, const f32x4& b, bf16x8& p1, bf16x8& p2, bf16x8& p3) {
+  float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h1 = (__bf16)v[e];
+    const float r1 = v[e] - (float)h1;
+    const __bf16 h2 = (__bf16)r1;
+    const float r2 = r1 - (float)h2;
+    p1[e] = h1;
+    p2[e] = h2;
+    p3[e] = (__bf16)r2;
+  }
+}
+
+// Split 8 fp32 values into a bf16 hi/lo pair (hi + lo within 2^-16 relative).
+__device__ __forceinline__ void split2(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)v[e];
+    hi[e] = h;
+    lo[e] = (__bf16)(v[e] - (float)h);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (F1) y[b][t][r] = x[b][t] . W_down[r] for one (b, 32-token chunk) per
+// workgroup, and the chunk's fp64 column sums ycs[b][c][r].  Wave w of NW
+// takes the features [w D/NW, (w+1) D/NW) and issues all of its x and W_down
+// loads before the first MFMA (16-byte x row loads straight from HBM: A =
+// x, tokens x d; B = W_down^T, d x r, the lane's W_down row split into three
+// bf16 planes); the NW partial 32 x R tiles are added in wave order in LDS.
+template <int RT, int KSW>  // KSW: K-steps (16 features) per wave
+__global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restrict__ x,
+                                                          const float* __restrict__ w_down, float* __restrict__ y,
+                                                          double* __restrict__ ycs, int T, int D, int R, int n_ch) {
+  constexpr int CT = kFastChunk;
+  constexpr int NW = 8;
+  constexpr int P = 33;  // partial tile pitch
+  __shared__ float part[NW][RT][CT * P];
+  __shared__ float ysum[CT][RT * 32 + 1];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int t0 = c * CT, nt = min(CT, T - t0);
+  const int nks = D / (16 * NW);  // K-steps of this wave (<= KSW)
+  const int d0 = wave * nks * 16;
+  const bf16_t* xrow = x + ((long)b * T + t0 + min(l32, nt - 1)) * D + d0 + 8 * g;
+
+  bf16x8 xf[KSW];
+  f32x4 wf[KSW][RT][2];
+#pragma unroll
+  for (int ks = 0; ks < KSW; ++ks) {
+    const int kc = min(ks, nks - 1);
+    xf[ks] = *reinterpret_cast<const bf16x8*>(xrow + 16 * kc);
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float* wrow = w_down + (long)min(rt * 32 + l32, R - 1) * D + d0 + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks) {
+      const int kc = min(ks, nks - 1);
+      wf[ks][rt][0] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc);
+      wf[ks][rt][1] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc + 4);
+    }
+  }
+  f32x16 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x16{};
+#pragma unroll
+  for (int ks = 0; ks < KSW; ++ks) {
+    if (ks < nks) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        bf16x8 p1, p2, p3;
+        split3(wf[ks][rt][0], wf[ks][rt][1], p1, p2, p3);
+        acc[rt] = mfma32(xf[ks], p3, acc[rt]);  // smallest terms first
+        acc[rt] = mfma32(xf[ks], p2, acc[rt]);
+        acc[rt] = mfma32(xf[ks], p1, acc[rt]);
+      }
+    }
+  }
+  // partial tiles: D[row = token][col = rank]
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) part[wave][rt][acc_row(g, v) * P + l32] = acc[rt][v];
+  __syncthreads();
+  const int RW = RT * 32;
+  for (int i = tid; i < CT * RW; i += NW * 64) {
+    const int t = i / RW, r = i % RW, rt = r >> 5, rl = r & 31;
+    float s = part[0][rt][t * P + rl];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) s += part[w][rt][t * P + rl];
+    ysum[t][r] = s;
+    if (t < nt && r < R) y[((long)b * T + t0 + t) * R + r] = s;
+  }
+  __syncthreads();
+  if (tid < R) {
+    double cs = 0.0;
+    for (int t = 0; t < nt; ++t) cs += (double)ysum[t][tid];
+    ycs[((long)b * n_ch + c) * R + tid] = cs;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (F2) per (b, 32-token chunk): fp64 carry of the earlier chunks' sums, the
+// in-chunk prefix, z = Z / (t+1), tanh, logits = a W_up^T, softmax probs,
+// top-k (ties -> lowest id) and gates; the tail matches router_fwd_kernel.
+template <int EMAX, int TK>
+__global__ __launch_bounds__(256) void router_head_kernel(
+    const float* __restrict__ y, const double* __restrict__ ycs, const float* __restrict__ w_up,
+    const float* __restrict__ noise, float noise_scale, float* __restrict__ logits, float* __restrict__ probs,
+    int32_t* __restrict__ top_idx, float* __restrict__ top_gates, float* __restrict__ act, int T, int R, int E,
+    int topk, int n_ch) {
+  constexpr int CT = kFastChunk;
+  constexpr int LP = EMAX + 1;
+  __shared__ float y_lds[CT * 65];
+  __shared__ float a_lds[CT * 65];
+  __shared__ float wu_lds[EMAX * 65];
+  __shared__ float lg_lds[CT * LP];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t0 = c * CT, nt = min(CT, T - t0);
+  __shared__ double carry_lds[64];
+  for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
+  for (int i = tid; i < nt * R; i += 256) y_lds[(i / R) * 65 + i % R] = y[((long)b * T + t0) * R + i];
+  if (tid < R) {
+    // carry = sum of the earlier chunks' fp64 sums, in chunk order (loads in
+    // flight 16 at a time)
+    const double* cs = ycs + (long)b * n_ch * R + tid;
+    double run = 0.0;
+    for (int c0 = 0; c0 < c; c0 += 16) {
+      double v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = c0 + i < c ? cs[(long)(c0 + i) * R] : 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) run += v[i];
+    }
+    carry_lds[tid] = run;
+  }
+  __syncthreads();
+  // (token, rank) pairs in parallel: Z_t = carry + y_0 + ... + y_t in token
+  // order (fp64), z = fp32(Z_t * fp64(1 / (t+1))), a = tanh(z)
+  for (int i = tid; i < nt * R; i += 256) {
+    const int t = i / R, r = i % R;
+    double run = carry_lds[r];
+    for (int s2 = 0; s2 <= t; ++s2) run += (double)y_lds[s2 * 65 + r];
+    const float z = (float)(run * (1.0 / (double)(t0 + t + 1)));
+    const float a = tanhf(z);
+    a_lds[t * 65 + r] = a;
+    act[((long)b * T + t0) * R + i] = a;
+  }
+  __syncthreads();
+  {
+    const int t = tid >> 3, part = tid & 7;
+    if (t < nt) {
+      const long tok = (long)b * T + t0 + t;
+#pragma unroll
+      for (int e0 = 0; e0 < EMAX; e0 += 8) {
+        const int e = e0 + part;
+        if (e < E) {
+          float lg = 0.f;
+          for (int r = 0; r < R; ++r) lg = fmaf(a_lds[t * 65 + r], wu_lds[e * 65 + r], lg);
+          lg_lds[t * LP + e] = lg;
+          logits[tok * E + e] = lg;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < nt) {
+    const long tok = (long)b * T + t0 + tid;
+    float lg[EMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) lg[e] = e < E ? lg_lds[tid * LP + e] : 0.f;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) mx = fmaxf(mx, lg[e]);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) sum += expf(lg[e] - mx);
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) probs[tok * E + e] = expf(lg[e] - mx) / sum;
+    float nz[EMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      nz[e] = (e < E) ? (noise ? fmaf(noise_scale, noise[tok * E + e], lg[e]) : lg[e]) : -INFINITY;
+    int sel[TK];
+    float val[TK];
+#pragma unroll
+    for (int t = 0; t < TK; ++t) {
+      sel[t] = 0;
+      val[t] = 0.f;
+      if (t < topk) {
+        int best = -1;
+        float bv = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+          bool taken = false;
+#pragma unroll
+          for (int u = 0; u < TK; ++u)
+            if (u < t && sel[u] == e) taken = true;
+          if (e < E && !taken && (best < 0 || nz[e] > bv)) {
+            best = e;
+            bv = nz[e];
+          }
+        }
+        sel[t] = best;
+        val[t] = bv;
+      }
+    }
+    float gs = 0.f;
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk) gs += expf(val[t] - val[0]);
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk) {
+        top_idx[tok * topk + t] = sel[t];
+        top_gates[tok * topk + t] = expf(val[t] - val[0]) / gs;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (B3) dx and dW_down for one (256-token range, 128-feature slab); wave w
+// owns features f0 = 128 slab + 32 w .. +31.  Per 32-token step the W~ rows
+// (as a bf16 hi/lo pair) and the x rows are staged in LDS (double-buffered
+// through registers):
+//   dx^T (32 feat x 32 tok) = W_down^T W~^T: A = W_down^T from registers
+//     (rows permuted by row_perm32 so a lane half holds 16 consecutive
+//     features), B = W~ rows from LDS; + dx_in; one bf16 rounding.
+//   dW_down^T (32 feat x R) += x^T W~: both operands K(token)-major, read
+//     with transposing LDS reads from the natural-layout tiles.
+// The range's dW_down partial goes to dwd_part[range][r][f] (summed over
+// ranges in a fixed order by router_reduce_kernel).
+template <int RT>
+__global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __restrict__ x,
+                                                             const float* __restrict__ wt,
+                                                             const float* __restrict__ w_down,
+                                                             const bf16_t* __restrict__ dx_in,
+                                                             bf16_t* __restrict__ dx, float* __restrict__ dwd_part,
+                                                             int D, int R, long ntok) {
+  constexpr int ST = 32;                 // tokens per step
+  constexpr int RW = RT * 32;            // staged ranks (zero padded)
+  constexpr int WP = RW + 8;             // W~ plane pitch (bf16)
+  constexpr int XP = kFastDxSlab + 8;    // x tile pitch (bf16)
+  constexpr int KR = RW / 16;            // K-steps over ranks
+  __shared__ __attribute__((aligned(16))) bf16_t wt_hi[2][ST * WP];
+  __shared__ __attribute__((aligned(16))) bf16_t wt_lo[2][ST * WP];
+  __shared__ __attribute__((aligned(16))) bf16_t x_lds[2][ST * XP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const long tok_beg = (long)blockIdx.x * kFastDxRange;
+  const int slab = blockIdx.y * kFastDxSlab;
+  const int f0 = slab + wave * 32;
+
+  // A operand of dx^T: W_down[r = 16 ks + 8 g + e][f0 + row_perm32(l32)], hi/lo
+  bf16x8 wa_hi[KR], wa_lo[KR];
+  {
+    const int f = f0 + row_perm32(l32);
+#pragma unroll
+    for (int ks = 0; ks < KR; ++ks) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = 16 * ks + 8 * g + e;
+        v[e] = r < R ? w_down[(long)r * D + f] : 0.f;
+      }
+      split2(v, wa_hi[ks], wa_lo[ks]);
+    }
+  }
+  f32x16 accw[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) accw[rt] = f32x16{};
+
+  // staging registers: W~ (ST x RW fp32: RW / 8 values per thread) and x
+  // (ST x 128 bf16: 16 per thread)
+  constexpr int WV = ST * RW / 256;  // fp32 values of W~ per thread (4 or 8)
+  float wreg[WV];
+  uint4 xreg[2];
+  auto fetch = [&](long ts) {
+    {
+      const int t = tid / (RW / WV), r0 = (tid % (RW / WV)) * WV;
+      const long tk = ts + t;
+#pragma unroll
+      for (int e = 0; e < WV; ++e) {
+        const int r = r0 + e;
+        wreg[e] = (tk < ntok && r < R) ? wt[tk * R + r] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + 256 * u, t = i >> 4, c8 = i & 15;
+      const long tk = ts + t;
+      xreg[u] = tk < ntok ? *reinterpret_cast<const uint4*>(x + tk * D + slab + 8 * c8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&](int buf) {
+    {
+      const int t = tid / (RW / WV), r0 = (tid % (RW / WV)) * WV;
+#pragma unroll
+      for (int e = 0; e < WV; ++e) {
+        const __bf16 h = (__bf16)wreg[e];
+        wt_hi[buf][t * WP + r0 + e] = __builtin_bit_cast(bf16_t, h);
+        wt_lo[buf][t * WP + r0 + e] = f32_to_bf16(wreg[e] - (float)h);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + 256 * u, t = i >> 4, c8 = i & 15;
+      *reinterpret_cast<uint4*>(&x_lds[buf][t * XP + 8 * c8]) = xreg[u];
+    }
+  };
+
+  const int n_steps = (int)min((long)(kFastDxRange / ST), (ntok - tok_beg + ST - 1) / ST);
+  fetch(tok_beg);
+  stash(0);
+  __syncthreads();
+  for (int st = 0; st < n_steps; ++st) {
+    const int buf = st & 1;
+    const long ts = tok_beg + (long)st * ST;
+    if (st + 1 < n_steps) fetch(ts + ST);
+    // ---- dx^T = W_down^T W~^T for this wave's 32 features x 32 tokens
+    {
+      f32x16 acc = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KR; ++ks) {
+        const int off = l32 * WP + 16 * ks + 8 * g;
+        const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&wt_hi[buf][off]);
+        const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&wt_lo[buf][off]);
+        acc = mfma32(wa_lo[ks], bh, acc);
+        acc = mfma32(wa_hi[ks], bl, acc);
+        acc = mfma32(wa_hi[ks], bh, acc);
+      }
+      const long tok = ts + l32;
+      if (tok < ntok) {
+        const long o = tok * D + f0 + 16 * g;  // this lane half's 16 consecutive features
+        float add[16];
+        if (dx_in != nullptr) {
+          const uint4 a0 = *reinterpret_cast<const uint4*>(dx_in + o);
+          const uint4 a1 = *reinterpret_cast<const uint4*>(dx_in + o + 8);
+          const uint32_t w8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            add[2 * e] = __uint_as_float(w8[e] << 16);
+            add[2 * e + 1] = __uint_as_float(w8[e] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) add[e] = 0.f;
+        }
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          lo[e] = (__bf16)(acc[e] + add[e]);
+          hi[e] = (__bf16)(acc[8 + e] + add[8 + e]);
+        }
+        *reinterpret_cast<bf16x8*>(dx + o) = lo;
+        *reinterpret_cast<bf16x8*>(dx + o + 8) = hi;
+      }
+    }
+    // ---- dW_down^T (32 features x R) += x^T W~ over the step's 32 tokens
+#pragma unroll
+    for (int kk = 0; kk < ST / 16; ++kk) {
+      const bf16x8 ax = lds_frag_T<false, false>(x_lds[buf], XP, 16 * kk, wave * 32);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const bf16x8 bh = lds_frag_T<false, false>(wt_hi[buf], WP, 16 * kk, 32 * rt);
+        const bf16x8 bl = lds_frag_T<false, false>(wt_lo[buf], WP, 16 * kk, 32 * rt);
+        accw[rt] = mfma32(ax, bl, accw[rt]);
+        accw[rt] = mfma32(ax, bh, accw[rt]);
+      }
+    }
+    if (st + 1 < n_steps) stash(buf ^ 1);  // last read before the previous barrier
+    __syncthreads();
+  }
+  // dW_down partial of this range: accw[rt] row = feature f0 + acc_row(g, v), column = rank
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = rt * 32 + l32;
+    if (r < R) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        dwd_part[((long)blockIdx.x * R + r) * D + f0 + acc_row(g, v)] = accw[rt][v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (B1) per (b, 32-token chunk): d(logits) of each token from d(gates),
+// d(probs) and d(logits) (softmax and softmax-of-top-k chains, model.py:215-
+// 220), then w_t = (dl_t W_up)(1 - a_t^2) / (t+1) for every (token, rank)
+// pair in parallel, the chunk's fp64 column sums of w, and the chunk's
+// partial dW_up = dl^T a (summed over chunks by router_reduce_kernel).
+template <int EMAX, int TK>
+__global__ __launch_bounds__(256) void router_bwd_token_fast_kernel(
+    const float* __restrict__ act, const float* __restrict__ probs, const int32_t* __restrict__ top_idx,
+    const float* __restrict__ top_gates, const float* __restrict__ d_gates, const float* __restrict__ d_probs,
+    const float* __restrict__ d_logits, const float* __restrict__ w_up, float* __restrict__ w_out,
+    double* __restrict__ wcs, float* __restrict__ dwup_part, int T, int R, int E, int topk, int n_ch) {
+  constexpr int CT = kFastChunk;
+  __shared__ float dl_lds[CT * (EMAX + 1)];
+  __shared__ float a_lds[CT * 65];
+  __shared__ float wu_lds[EMAX * 65];
+  __shared__ float w_lds[CT * 65];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t0 = c * CT, nt = min(CT, T - t0);
+  const long tok0 = (long)b * T + t0;
+  for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
+  for (int i = tid; i < CT * R; i += 256) a_lds[(i / R) * 65 + i % R] = i < nt * R ? act[tok0 * R + i] : 0.f;
+  if (tid < CT) {
+    float dl[EMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) dl[e] = 0.f;
+    if (tid < nt) {
+      const long tok = tok0 + tid;
+      if (d_logits) {
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+          if (e < E) dl[e] = d_logits[tok * E + e];
+      }
+      if (d_probs) {
+        float pv[EMAX], dp[EMAX];
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+          pv[e] = e < E ? probs[tok * E + e] : 0.f;
+          dp[e] = e < E ? d_probs[tok * E + e] : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) dot = fmaf(pv[e], dp[e], dot);
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+          if (e < E) dl[e] = fmaf(pv[e], dp[e] - dot, dl[e]);
+      }
+      if (d_gates) {
+        float gv[TK], dg[TK];
+        int gi[TK];
+        float gdot = 0.f;
+#pragma unroll
+        for (int t = 0; t < TK; ++t) {
+          gv[t] = t < topk ? top_gates[tok * topk + t] : 0.f;
+          dg[t] = t < topk ? d_gates[tok * topk + t] : 0.f;
+          gi[t] = t < topk ? top_idx[tok * topk + t] : -1;
+        }
+#pragma unroll
+        for (int t = 0; t < TK; ++t) gdot = fmaf(gv[t], dg[t], gdot);
+#pragma unroll
+        for (int t = 0; t < TK; ++t)
+          if (t < topk) {
+            const float dv = gv[t] * (dg[t] - gdot);
+#pragma unroll
+            for (int u = 0; u < EMAX; ++u)
+              if (u == gi[t]) dl[u] += dv;
+          }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) dl_lds[tid * (EMAX + 1) + e] = dl[e];
+  }
+  __syncthreads();
+  for (int i = tid; i < nt * R; i += 256) {
+    const int j = i / R, r = i % R;
+    float da = 0.f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) da = fmaf(dl_lds[j * (EMAX + 1) + e], wu_lds[e * 65 + r], da);
+    const float a = a_lds[j * 65 + r];
+    const float wv = da * (1.f - a * a) / (float)(t0 + j + 1);
+    w_lds[j * 65 + r] = wv;
+    w_out[tok0 * R + i] = wv;
+  }
+  __syncthreads();
+  if (tid < R) {
+    double cs = 0.0;
+    for (int t = 0; t < nt; ++t) cs += (double)w_lds[t * 65 + tid];
+    wcs[((long)b * n_ch + c) * R + tid] = cs;
+  }
+  const long part = (long)b * n_ch + c;
+  for (int i = tid; i < E * R; i += 256) {
+    const int e = i / R, r = i % R;
+    float acc = 0.f;
+    for (int j = 0; j < nt; ++j) acc = fmaf(dl_lds[j * (EMAX + 1) + e], a_lds[j * 65 + r], acc);
+    dwup_part[part * E * R + i] = acc;
+  }
+}
+
+// (B2) W~_t = sum_{s >= t} w_s within the sequence: per (b, 32-token chunk),
+// the fp64 carry of the later chunks' sums (chunk order) plus the in-chunk
+// suffix (token order, descending), for every (token, rank) pair in parallel.
+__global__ __launch_bounds__(256) void router_wtilde_kernel(const float* __restrict__ w,
+                                                            const double* __restrict__ wcs,
+                                                            float* __restrict__ wt, int T, int R, int n_ch) {
+  constexpr int CT = kFastChunk;
+  __shared__ float w_lds[CT * 65];
+  __shared__ double carry_lds[64];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t0 = c * CT, nt = min(CT, T - t0);
+  const long tok0 = (long)b * T + t0;
+  for (int i = tid; i < nt * R; i += 256) w_lds[(i / R) * 65 + i % R] = w[tok0 * R + i];
+  if (tid < R) {
+    const double* cs = wcs + (long)b * n_ch * R + tid;
+    double run = 0.0;
+    for (int c0 = c + 1; c0 < n_ch; c0 += 16) {
+      double v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = c0 + i < n_ch ? cs[(long)(c0 + i) * R] : 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) run += v[i];
+    }
+    carry_lds[tid] = run;
+  }
+  __syncthreads();
+  for (int i = tid; i < nt * R; i += 256) {
+    const int t = i / R, r = i % R;
+    double run = carry_lds[r];
+    for (int s2 = nt - 1; s2 >= t; --s2) run += (double)w_lds[s2 * 65 + r];
+    wt[tok0 * R + i] = (float)run;
+  }
+}
+
+// ---------------------------------------------------------------------------
+bool router_fast_fwd_ok(const void* x, bool x_bf16, const float* w_down, const float* h_out, const RouterDims& d) {
+  // the projection holds a wave's D / 128 K-steps of x and W_down in registers:
+  // at most 16 (R <= 32) or 8 (R <= 64) of them
+  const int nks = d.D / 128;
+  return x_bf16 && h_out == nullptr && d.D % 128 == 0 && d.R <= 64 && nks <= (d.R <= 32 ? 16 : 8) &&
+         (((uintptr_t)x | (uintptr_t)w_down) & 15) == 0;
+}
+
+bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const RouterDims& d) {
+  return x_bf16 && d.D % kFastDxSlab == 0 && d.R <= 64 && (((uintptr_t)x | (uintptr_t)dx) & 15) == 0;
+}
+
+template <int RT, int EMAX, int TK>
+static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
+                          float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
+                          const RouterDims& d, hipStream_t st) {
+  const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
+  // 8 waves split D; a wave takes D / 128 K-steps, held in registers at once
+  const int nks = d.D / 128;
+  auto go = [&](auto ksw) {
+    constexpr int KSW = decltype(ksw)::value;
+    NAYLIS_TIMED("router_proj", st,
+                 hipLaunchKernelGGL((router_proj_kernel<RT, KSW>), dim3(n_ch, d.B), dim3(512), 0, st,
+                                    (const bf16_t*)x, w_down, y, ycs, d.T, d.D, d.R, n_ch));
+  };
+  if (nks <= 2)
+    go(std::integral_constant<int, 2>{});
+  else if (nks <= 4)
+    go(std::integral_constant<int, 4>{});
+  else if (nks <= 8)
+    go(std::integral_constant<int, 8>{});
+  else
+    go(std::integral_constant<int, 16 / RT>{});  // router_fast_fwd_ok bounds nks by 16 / RT
+  NAYLIS_TIMED("router_head", st,
+               hipLaunchKernelGGL((router_head_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, y, ycs, w_up,
+                                  noise, ns, logits, probs, idx, gates, act, d.T, d.R, d.E, d.topk, n_ch));
+}
+
+template <int RT>
+static void fast_fwd_rt(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
+                        float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
+                        const RouterDims& d, hipStream_t st) {
+  if (d.E <= 8 && d.topk <= 2)
+    fast_fwd_inst<RT, 8, 2>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+  else if (d.E <= 8)
+    fast_fwd_inst<RT, 8, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+  else if (d.E <= 32)
+    fast_fwd_inst<RT, 32, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+  else
+    fast_fwd_inst<RT, 64, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+}
+
+void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_up, const float* noise,
+                            float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
+                            float* act, float* y, double* ycs, const RouterDims& d, hipStream_t st) {
+  if (d.R <= 32)
+    fast_fwd_rt<1>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, d, st);
+  else
+    fast_fwd_rt<2>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, d, st);
+}
+
+void launch_router_fast_dx(const void* x, const float* wt, const float* w_down, const void* dx_in, void* dx,
+                           float* dwd_part, const RouterDims& d, hipStream_t st) {
+  const long ntok = (long)d.B * d.T;
+  const dim3 grid((unsigned)((ntok + kFastDxRange - 1) / kFastDxRange), d.D / kFastDxSlab);
+  if (d.R <= 32)
+    NAYLIS_TIMED("router_bwd_dx", st,
+                 hipLaunchKernelGGL((router_dx_fast_kernel<1>), grid, dim3(256), 0, st, (const bf16_t*)x, wt, w_down,
+                                    (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok));
+  else
+    NAYLIS_TIMED("router_bwd_dx", st,
+                 hipLaunchKernelGGL((router_dx_fast_kernel<2>), grid, dim3(256), 0, st, (const bf16_t*)x, wt, w_down,
+                                    (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok));
+}
+
+}  // namespace naylis
+
+namespace naylis {
+
+template <int EMAX, int TK>
+static void fast_token(const float* act, const float* probs, const int32_t* idx, const float* gates, const float* dg,
+                       const float* dp, const float* dl, const float* w_up, float* w, double* wcs, float* dwup_part,
+                       const RouterDims& d, hipStream_t st) {
+  const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
+  NAYLIS_TIMED("router_bwd_token", st,
+               hipLaunchKernelGGL((router_bwd_token_fast_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, act,
+                                  probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d.T, d.R, d.E, d.topk,
+                                  n_ch));
+}
+
+int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,
+                            const float* dg, const float* dp, const float* dl, const float* w_up, float* w,
+                            double* wcs, float* wt, float* dwup_part, const RouterDims& d, hipStream_t st) {
+  if (d.E <= 8 && d.topk <= 2)
+    fast_token<8, 2>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
+  else if (d.E <= 8)
+    fast_token<8, 8>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
+  else if (d.E <= 32)
+    fast_token<32, 8>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
+  else
+    fast_token<64, 8>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
+  const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
+  NAYLIS_TIMED("router_bwd_scan", st,
+               hipLaunchKernelGGL(router_wtilde_kernel, dim3(n_ch, d.B), dim3(256), 0, st, w, wcs, wt, d.T, d.R,
+                                  n_ch));
+  return d.B * n_ch;  // dW_up partials written
+}
+
+}  // namespace naylis

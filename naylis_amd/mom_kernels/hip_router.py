@@ -75,7 +75,7 @@ class MomRouteFunction(torch.autograd.Function):
                 d_gates.data_ptr() if d_gates is not None else None,
                 d_probs.data_ptr() if d_probs is not None else None,
                 d_logits.data_ptr() if d_logits is not None else None,
-                dx.data_ptr(), dw_down.data_ptr(), dw_up.data_ptr(), ws.data_ptr(), ws.numel(),
+                dx.data_ptr(), 0, dw_down.data_ptr(), dw_up.data_ptr(), ws.data_ptr(), ws.numel(),
                 B, T, D, R, E, top_k, _lib.stream_of(dev))
         _lib.check(rc)
         return dx, dw_down, dw_up, None, None, None, None

@@ -77,17 +77,25 @@ def test_router_prefix_mean_tiny_values(dev):
     assert torch.equal(h.cpu(), r_h), f"{int((h.cpu() != r_h).sum())} prefix-mean values differ"
 
 
+@pytest.mark.parametrize("want_h", [True, False], ids=["scan_x", "project_first"])
 @pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}T{c[1]}D{c[2]}R{c[3]}E{c[4]}k{c[5]}{str(c[6])[6:]}" for c in CASES])
-def test_router_forward(case, dev):
+def test_router_forward(case, want_h, dev):
+    """With h requested the router scans x and h is bit-exact; without it,
+    bf16 x with D % 128 == 0 takes the project-first path (y = x W_down^T on
+    exact three-plane bf16 MFMA, fp64 prefix over the R-wide y); both must
+    meet the same index / logit criteria."""
     from naylis_amd import mom_kernels
     B, T, D, R, E, k, dtype = case
     x, w_down, w_up, _ = make(B, T, D, R, E, dtype)
-    logits, probs, idx, gates, h = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), k, return_h=True)
+    out = mom_kernels.mom_route(x.to(dev), w_down.to(dev), w_up.to(dev), k, return_h=want_h)
     torch.cuda.synchronize()
+    logits, probs, idx, gates = out[:4]
     r_logits, r_probs, r_idx, r_gates, r_h = oracle.router(x, w_down, w_up, k)
-    # bit-exact prefix mean
-    assert torch.equal(h.cpu(), r_h), f"prefix mean differs: max {float((h.cpu() - r_h).abs().max())}"
-    assert torch.equal(h[:, 0].cpu(), x[:, 0].float())
+    if want_h:
+        # bit-exact prefix mean
+        h = out[4]
+        assert torch.equal(h.cpu(), r_h), f"prefix mean differs: max {float((h.cpu() - r_h).abs().max())}"
+        assert torch.equal(h[:, 0].cpu(), x[:, 0].float())
     # indices: exact outside near-ties
     margin, scale = fp64_margin(x, w_down, w_up, k, None, 1.0)
     tau = 1e-5 * float(scale)
@@ -164,3 +172,52 @@ def test_router_causal(dev):
     b = mom_kernels.mom_route(x2.to(dev), w_down.to(dev), w_up.to(dev), 2, return_h=True)
     for ta, tb in zip(a, b):
         assert torch.equal(ta[:, :301], tb[:, :301])
+
+
+def test_router_backward_accumulates_dx(dev):
+    """dx_accumulate = 1 adds the router's input gradient to the dx the
+    caller passes (the layer folds the query projection's dx in this way);
+    it matches the plain gradient plus that dx to one bf16 rounding."""
+    from naylis_amd import _lib, mom_kernels
+    lib = _lib.load()
+    B, T, D, R, E, k = 2, 384, 1024, 32, 8, 2
+    x, w_down, w_up, _ = make(B, T, D, R, E, torch.bfloat16, seed=5)
+    g = torch.Generator().manual_seed(9)
+    dg = torch.randn(B, T, k, generator=g).to(dev)
+    xd = x.to(dev)
+    wd, wu = w_down.to(dev), w_up.to(dev)
+    logits, probs, idx, gates = mom_kernels.mom_route(xd, wd, wu, k)
+    act = torch.empty(B, T, R, device=dev)
+    # recompute the forward's saved activation through the C ABI
+    nbytes = lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    lg, pr, ti, tg = (torch.empty_like(t) for t in (logits, probs, idx, gates))
+    st = _lib.stream_of(dev)
+    assert lib.naylis_mom_router_fwd(xd.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(), None, 1.0, lg.data_ptr(),
+                                     pr.data_ptr(), ti.data_ptr(), tg.data_ptr(), act.data_ptr(), None,
+                                     ws.data_ptr(), nbytes, B, T, D, R, E, k, st) == 0
+    prior = (torch.randn(B, T, D, generator=g) * 0.01).bfloat16().to(dev)
+    outs = []
+    for acc in (0, 1):
+        dx = prior.clone() if acc else torch.empty_like(xd)
+        dwd = torch.empty(R, D, device=dev)
+        dwu = torch.empty(E, R, device=dev)
+        rc = lib.naylis_mom_router_bwd(xd.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(), act.data_ptr(), pr.data_ptr(),
+                                       ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, None, dx.data_ptr(), acc,
+                                       dwd.data_ptr(), dwu.data_ptr(), ws.data_ptr(), nbytes, B, T, D, R, E, k, st)
+        assert rc == 0, lib.naylis_mom_last_error()
+        outs.append((dx, dwd, dwu))
+    torch.cuda.synchronize()
+    plain, accd = outs
+    ref = plain[0].float() + prior.float()
+    err = (accd[0].float() - ref).abs()
+    # two bf16 roundings (of the plain gradient, and of the sum) at most
+    bound = 2.0 ** -8 * (plain[0].float().abs() + prior.float().abs() + ref.abs()) + 1e-6
+    assert bool((err <= bound).all()), f"max err {float(err.max())}"
+    assert torch.equal(plain[1], accd[1]) and torch.equal(plain[2], accd[2])
+    # fp32 x cannot accumulate: rejected before any device work
+    xf = x.float().to(dev)
+    rc = lib.naylis_mom_router_bwd(xf.data_ptr(), 0, wd.data_ptr(), wu.data_ptr(), act.data_ptr(), pr.data_ptr(),
+                                   ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, None, xf.data_ptr(), 1,
+                                   dwd.data_ptr(), dwu.data_ptr(), ws.data_ptr(), nbytes, B, T, D, R, E, k, st)
+    assert rc == _lib.NAYLIS_ERR_ARG
