@@ -93,10 +93,18 @@ def layer_step(layer, M, x, dy):
 
 
 def _forward_with_bias(layer, x, M, bias):
-    """Layer forward with an additive router-logit bias (config 4's sparsity)."""
+    """Layer forward with an additive router-logit bias (config 4's sparsity),
+    through the layer's fused node when it applies."""
     from naylis_amd import mom_kernels
+    from naylis_amd.mom_kernels.hip_layer import fused_layer_supported, mom_layer
     if layer._kernel_mode is None:
         layer._kernel_mode = layer._resolve_kernel(x)
+    ws = (layer.router_down.weight, layer.router_up.weight, layer.q_proj.weight, layer.k_proj.weight,
+          layer.v_proj.weight, layer.o_proj.weight, layer.mom_scale)
+    if fused_layer_supported(x, M, *ws):
+        y, _, _ = mom_layer(x, M, *ws, n_heads=layer.n_heads, num_blocks=layer.num_blocks,
+                            block_size=layer.block_size, top_k=layer.top_blocks, noise=bias, noise_scale=1.0)
+        return y
     _, probs, idx, gates = mom_kernels.mom_route(x, layer.router_down.weight, layer.router_up.weight,
                                                  layer.top_blocks, noise=bias, noise_scale=1.0)
     return mom_kernels.mom_rezero(layer._read(x, idx, gates, M), layer.mom_scale)

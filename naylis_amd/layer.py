@@ -12,7 +12,11 @@ between the two unchanged.  The forward is
     y     = mom_scale * o_proj(out)
 
 q_proj / o_proj run their forward and input gradient as torch GEMMs
-(hipBLASLt) and their weight gradient on the library's split-K GEMM.  There is one backend: the
+(hipBLASLt) and their weight gradient on the library's split-K GEMM.  In the
+common training case (bf16 activations and projection weights, no gradient
+checkpointing) the whole forward is one autograd node
+(``mom_kernels.hip_layer``) whose backward orders the library calls so the
+router's input gradient accumulates into the q projection's.  There is one backend: the
 HIP kernels (``use_kernel`` is accepted for signature compatibility).  The
 eager SDPA path of model.py:262-275 is the parity oracle and lives in
 ``oracle/``, outside the product.
@@ -23,6 +27,7 @@ import torch
 import torch.nn as nn
 
 from . import mom_kernels
+from .mom_kernels.hip_layer import fused_layer_supported, mom_layer
 
 __all__ = ["MoMLayer", "mom_aux_loss"]
 
@@ -85,11 +90,25 @@ class MoMLayer(nn.Module):
             # the Gumbel draw of model.py:210, same shape/dtype as the logits
             u = torch.rand((B, S, self.num_blocks), device=x.device, dtype=torch.float32)
             noise = -torch.log(-torch.log(u + 1e-9) + 1e-9)
+        ckpt = self.mom_grad_ckpt and self.training and torch.is_grad_enabled()
+        if not ckpt and fused_layer_supported(x, M_blocks, self.router_down.weight, self.router_up.weight,
+                                              self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                                              self.o_proj.weight, self.mom_scale):
+            # one autograd node for router + bank + q + read + o + ReZero
+            y, router_probs, top_idx = mom_layer(
+                x, M_blocks, self.router_down.weight, self.router_up.weight, self.q_proj.weight,
+                self.k_proj.weight, self.v_proj.weight, self.o_proj.weight, self.mom_scale,
+                n_heads=self.n_heads, num_blocks=self.num_blocks, block_size=self.block_size,
+                top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale)
+            if self.training:
+                self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
+                self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
+            return y
         _, router_probs, top_idx, top_gates = self.route(x, noise)
         if self.training:
             self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
             self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
-        if self.mom_grad_ckpt and self.training and torch.is_grad_enabled():
+        if ckpt:
             out = torch.utils.checkpoint.checkpoint(
                 self._read, x, top_idx, top_gates, M_blocks, use_reentrant=False, preserve_rng_state=False)
         else:

@@ -1,0 +1,208 @@
+"""One autograd node for the whole MoM layer (model.py:189-276): router, bank
+K/V, q projection, gated read, o projection and the ReZero gate.
+
+The layer's separate autograd Functions (hip_router, hip_bank, hip_read,
+hip_linear, hip_rezero) give autograd a graph in which x feeds both the router
+and the q projection, so autograd sums the two input gradients with an extra
+elementwise kernel, and materialises zero gradients for router outputs the
+loss does not use.  Here the backward runs the library calls in a fixed
+order instead: the q projection's input gradient is written first and the
+router's backward accumulates into it (C ABI dx_accumulate, one bf16 rounding
+of the fp32 sum), and absent output gradients are passed as NULL.  Results
+equal the modular path's to bf16 rounding; the modular Functions stay the
+public drop-in API (mom_read etc.) and serve gradient checkpointing.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+from .hip_read import read_order
+
+_F32, _BF16 = 0, 1
+
+
+def _ws(nbytes, dev):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def fused_layer_supported(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale):
+    """True when the fused node applies: bf16 activations and projection
+    weights, fp32 router weights and gate, D a multiple of 128 (the router's
+    accumulating backward), all on one ROCm device."""
+    if torch.version.hip is None or not x.is_cuda:
+        return False
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.shape[-1] % 128 != 0:
+        return False
+    dev = x.device
+    for w in (w_q, w_k, w_v, w_o):
+        if w.dtype != torch.bfloat16 or w.device != dev or w.dim() != 2:
+            return False
+    if w_q.shape != (x.shape[-1], x.shape[-1]) or w_o.shape != w_q.shape:
+        return False
+    if w_down.dtype != torch.float32 or w_up.dtype != torch.float32 or w_down.shape[0] > 64:
+        return False
+    if scale.dtype != torch.float32 or scale.numel() != 1 or scale.device != dev:
+        return False
+    return M_blocks.device == dev and M_blocks.dtype in (torch.bfloat16, torch.float32)
+
+
+class MomLayerFunction(torch.autograd.Function):
+    """y, probs, top_idx = layer(x, M_blocks, ...); y fp32 (ReZero promotes),
+    probs the router softmax (for the load-balance aux loss), top_idx int32."""
+
+    @staticmethod
+    def forward(ctx, x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, noise, noise_scale, geom):
+        n_heads, num_blocks, block_size, top_k = geom
+        lib = _lib.load()
+        B, T, D = x.shape
+        R, E = w_down.shape[0], w_up.shape[0]
+        H, HD = n_heads, D // n_heads
+        dev = x.device
+        st = _lib.stream_of(dev)
+        x = x.contiguous()
+        f32 = dict(device=dev, dtype=torch.float32)
+        with _lib.on_device(dev):
+            # ---- router (model.py:169-220)
+            logits = torch.empty((B, T, E), **f32)
+            probs = torch.empty((B, T, E), **f32)
+            top_idx = torch.empty((B, T, top_k), device=dev, dtype=torch.int32)
+            gates = torch.empty((B, T, top_k), **f32)
+            act = torch.empty((B, T, R), **f32)
+            rws = _ws(lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, top_k), dev)
+            _lib.check(lib.naylis_mom_router_fwd(
+                x.data_ptr(), _BF16, w_down.data_ptr(), w_up.data_ptr(),
+                noise.data_ptr() if noise is not None else None, float(noise_scale), logits.data_ptr(),
+                probs.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), act.data_ptr(), None, rws.data_ptr(),
+                rws.numel(), B, T, D, R, E, top_k, st))
+            del rws
+            # ---- bank K/V (model.py:253-256)
+            slots = M_blocks.reshape(-1, D)
+            m_dtype = slots.dtype
+            slots = slots.to(torch.bfloat16).contiguous()
+            L = slots.shape[0]
+            k = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
+            v = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
+            _lib.check(lib.naylis_mom_bank_kv_fwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), k.data_ptr(),
+                                                  v.data_ptr(), L, D, D, st))
+            # ---- q projection, gated read, o projection (model.py:251, 258-276)
+            q = F.linear(x, w_q)
+            order = read_order(top_idx, num_blocks)
+            out = torch.empty_like(q)
+            lse = torch.empty((H, B, T), **f32)
+            _lib.check(lib.naylis_mom_read_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), order.data_ptr(),
+                out.data_ptr(), lse.data_ptr(), None, 0, B, T, H, HD, num_blocks, block_size, top_k, st))
+            z = F.linear(out, w_o)
+            # ---- ReZero gate (model.py:239)
+            y = torch.empty((B, T, D), **f32)
+            _lib.check(lib.naylis_mom_rezero_fwd(z.data_ptr(), _BF16, scale.data_ptr(), y.data_ptr(), z.numel(),
+                                                 st))
+        ctx.save_for_backward(x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v,
+                              q, order, out, lse, z)
+        ctx.geom = geom
+        ctx.m_shape = (tuple(M_blocks.shape), m_dtype)
+        ctx.mark_non_differentiable(top_idx)
+        ctx.set_materialize_grads(False)
+        return y, probs, top_idx
+
+    @staticmethod
+    def backward(ctx, dy, d_probs, _d_idx):
+        (x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order, out, lse,
+         z) = ctx.saved_tensors
+        n_heads, num_blocks, block_size, top_k = ctx.geom
+        lib = _lib.load()
+        B, T, D = x.shape
+        R, E = w_down.shape[0], w_up.shape[0]
+        H, HD = n_heads, D // n_heads
+        L = slots.shape[0]
+        dev = x.device
+        st = _lib.stream_of(dev)
+        f32 = dict(device=dev, dtype=torch.float32)
+        N = B * T
+        with _lib.on_device(dev):
+            # ---- ReZero: dz = s dy (bf16), ds = sum(dy z)
+            if dy is None:
+                dy = torch.zeros((B, T, D), **f32)
+            dy = dy.contiguous()
+            dy_dt = _F32 if dy.dtype == torch.float32 else _BF16
+            if dy.dtype not in (torch.float32, torch.bfloat16):
+                dy, dy_dt = dy.float(), _F32
+            dz = torch.empty_like(z)
+            ds = torch.empty(1, **f32)
+            zws = _ws(lib.naylis_mom_rezero_workspace_bytes(z.numel()), dev)
+            _lib.check(lib.naylis_mom_rezero_bwd(dy.data_ptr(), dy_dt, z.data_ptr(), _BF16, scale.data_ptr(),
+                                                 dz.data_ptr(), ds.data_ptr(), zws.data_ptr(), zws.numel(),
+                                                 z.numel(), st))
+            # ---- o projection: d out = dz W_o, dW_o = dz^T out
+            dz2 = dz.view(N, D)
+            dout = torch.mm(dz2, w_o).view(B, T, H, HD)
+            dw_o = _wgrad(lib, out.view(N, D), dz2, w_o.dtype, dev, st)
+            # ---- gated read
+            dq = torch.empty_like(q)
+            dk = torch.empty_like(k)
+            dv = torch.empty_like(v)
+            dgates = torch.empty_like(gates)
+            nbytes = lib.naylis_mom_read_workspace_bytes(B, T, H, HD, num_blocks, block_size, top_k)
+            if nbytes == 0:
+                _lib.check(_lib.NAYLIS_ERR_ARG)
+            rws = _ws(nbytes, dev)
+            _lib.check(lib.naylis_mom_read_bwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), order.data_ptr(),
+                out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                dgates.data_ptr(), rws.data_ptr(), rws.numel(), B, T, H, HD, num_blocks, block_size, top_k, st))
+            del rws, dout
+            # ---- bank K/V
+            m_shape, m_dtype = ctx.m_shape
+            sdt = _BF16 if m_dtype == torch.bfloat16 else _F32
+            d_slots = torch.empty((L, D), device=dev, dtype=m_dtype)
+            dw_k = torch.empty_like(w_k)
+            dw_v = torch.empty_like(w_v)
+            _lib.check(lib.naylis_mom_bank_kv_bwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), dk.data_ptr(),
+                                                  dv.data_ptr(), d_slots.data_ptr(), sdt, dw_k.data_ptr(),
+                                                  dw_v.data_ptr(), _BF16, L, D, D, st))
+            # ---- q projection: dx = dq W_q (the router adds its part below), dW_q = dq^T x
+            dq2 = dq.view(N, D)
+            dx = torch.mm(dq2, w_q).view(B, T, D)
+            dw_q = _wgrad(lib, x.view(N, D), dq2, w_q.dtype, dev, st)
+            # ---- router, accumulating into dx
+            if d_probs is not None:
+                d_probs = d_probs.float().contiguous()
+            dw_down = torch.empty((R, D), **f32)
+            dw_up = torch.empty((E, R), **f32)
+            rws = _ws(lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, top_k), dev)
+            _lib.check(lib.naylis_mom_router_bwd(
+                x.data_ptr(), _BF16, w_down.data_ptr(), w_up.data_ptr(), act.data_ptr(), probs.data_ptr(),
+                top_idx.data_ptr(), gates.data_ptr(), dgates.data_ptr(),
+                d_probs.data_ptr() if d_probs is not None else None, None, dx.data_ptr(), 1, dw_down.data_ptr(),
+                dw_up.data_ptr(), rws.data_ptr(), rws.numel(), B, T, D, R, E, top_k, st))
+        return (dx, d_slots.view(m_shape), dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None,
+                None)
+
+
+def _wgrad(lib, xin, dy, dtype, dev, st):
+    """dW = dy^T xin over all rows (C ABI naylis_mom_linear_wgrad; its split-K
+    kernel needs N, D_in, D_out multiples of 8 — otherwise the torch product
+    that autograd would use for nn.Linear's weight gradient)."""
+    N, D_in = xin.shape
+    D_out = dy.shape[1]
+    if N % 8 or D_in % 8 or D_out % 8:
+        return torch.mm(dy.t(), xin).to(dtype)
+    ws = _ws(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), dev)
+    dw = torch.empty((D_out, D_in), device=dev, dtype=dtype)
+    _lib.check(lib.naylis_mom_linear_wgrad(xin.data_ptr(), dy.data_ptr(), dw.data_ptr(),
+                                           _BF16 if dtype == torch.bfloat16 else _F32, ws.data_ptr(), ws.numel(),
+                                           N, D_in, D_out, st))
+    return dw
+
+
+def mom_layer(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, *, n_heads, num_blocks, block_size, top_k,
+              noise=None, noise_scale=1.0):
+    """The fused layer node; callers check fused_layer_supported() first.
+    Returns (y fp32, router probs, top_idx int32)."""
+    if noise is not None:
+        noise = noise.detach().float().contiguous()
+    return MomLayerFunction.apply(x, M_blocks, w_down.float().contiguous(), w_up.float().contiguous(), w_q, w_k,
+                                  w_v, w_o, scale, noise, float(noise_scale),
+                                  (int(n_heads), int(num_blocks), int(block_size), int(top_k)))

@@ -137,3 +137,43 @@ def test_layer_grad_ckpt_exact_and_alive(dev):
         assert torch.isfinite(g0[n]).all(), n
     assert float(g0["router_up.weight"].abs().sum()) > 0
     assert float(m0.float().abs().sum()) > 0
+
+
+def test_layer_fused_node_matches_modular(dev, monkeypatch):
+    """The single-node layer (hip_layer.MomLayerFunction) against the
+    modular autograd graph on the same inputs: forward bitwise, parameter
+    gradients bitwise (same kernels in the same order), and dx within one
+    bf16 rounding (the fused backward adds the router's fp32 input gradient
+    before rounding; autograd adds two bf16 tensors)."""
+    import naylis_amd.layer as layer_mod
+    B, S, D, H, NB, BS, K, R = 2, 256, 256, 4, 8, 128, 2, 32
+    res = []
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(layer_mod, "fused_layer_supported", lambda *a, **k: False)
+        layer, _, M = build_pair(D, H, NB, BS, K, R, seed=13)
+        ld = layer.to(dev)
+        for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+            lin.to(torch.bfloat16)
+        ld.train()
+        ld.noise_scale = 0.0
+        g = torch.Generator().manual_seed(4)
+        x = torch.randn(B, S, D, generator=g).bfloat16().to(dev).requires_grad_(True)
+        dy = torch.randn(B, S, D, generator=g).to(dev)
+        Md = M.to(dev).requires_grad_(True)
+        y = ld(x, Md)
+        # the load-balance aux loss reaches the router through the probs
+        aux = layer_mod.mom_aux_loss([ld])
+        (y * dy).sum().add(aux).backward()
+        res.append((y.detach(), x.grad.clone(), Md.grad.clone(), {n: p.grad.clone() for n, p in ld.named_parameters()}))
+    (y0, x0, m0, g0), (y1, x1, m1, g1) = res
+    assert torch.equal(y0, y1)
+    assert torch.equal(m0, m1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+    # dx is the sum of the q projection's and the router's parts; where they
+    # cancel, the modular path's two separate bf16 roundings dominate, so the
+    # difference is bounded by bf16 rounding at the gradient's scale
+    err = (x0.float() - x1.float()).abs()
+    scale = float(x1.float().abs().max())
+    assert float(err.max()) <= 2.0 ** -7 * scale, (float(err.max()), scale)
