@@ -48,6 +48,10 @@ struct GemmCfg {
 // or 4 of 128 x 128 measured no faster on MI355X for these shapes: with one
 // stage of prefetch the K loop waits on load latency, not on MFMA or LDS.)
 using CfgSmall = GemmCfg<2, 2, 2, 2>;
+// Narrower tiles for GEMMs too small to give every CU a 128 x 128 tile (the
+// 1024 x 1024 bank projections): 64 x 128 (waves of 32 x 64) and 64 x 64.
+using CfgMid = GemmCfg<2, 2, 1, 2>;
+using CfgTiny = GemmCfg<2, 2, 1, 1>;
 
 // LDS pitches: a [row][k] tile row is 64 + 8 elements (36 dwords: eight
 // consecutive rows' 16-byte reads hit distinct banks); a [k][row] tile row
@@ -368,7 +372,17 @@ hipError_t launch_gemm(const GemmLaunch& g, const char* name, hipStream_t st) {
   splits = (g.K + kper - 1) / kper;
   GemmLaunch gl = g;
   gl.K1 = g.K1 < g.K ? g.K1 : g.K;
-  gemm_layouts<CfgSmall>(dj, gl, kper, splits, name, st);
+  // the largest tile that still gives at least one workgroup per CU
+  auto wgs = [&](int bm, int bn) {
+    return (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * splits * g.njobs;
+  };
+  const long cus = 256;
+  if (wgs(CfgSmall::BM, CfgSmall::BN) >= cus)
+    gemm_layouts<CfgSmall>(dj, gl, kper, splits, name, st);
+  else if (wgs(CfgMid::BM, CfgMid::BN) >= cus)
+    gemm_layouts<CfgMid>(dj, gl, kper, splits, name, st);
+  else
+    gemm_layouts<CfgTiny>(dj, gl, kper, splits, name, st);
   return hipGetLastError();
 }
 
