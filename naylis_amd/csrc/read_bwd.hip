@@ -27,7 +27,7 @@
 namespace naylis {
 
 template <int HD, int SG, bool ALIGNED, int TK>
-__global__ __launch_bounds__(256) void read_bwd_dq_kernel(
+__global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
     const bf16_t* __restrict__ dout, const float* __restrict__ lse, bf16_t* __restrict__ dq,
@@ -63,39 +63,45 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
 
   TokenRoute<TK> rt;
   load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
-  for (int e = tid; e < E; e += 256) flags[e] = 0;
-  if constexpr (HD < 32) {
-    for (int i = tid; i < SG * PITCH; i += 256) k_lds[i] = 0;  // K^T rows beyond HD stay zero
-  }
-  __syncthreads();
-  if (g == 0 && tok_ok) {
-#pragma unroll
-    for (int t = 0; t < TK; ++t)
-      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
-  }
-  __syncthreads();
-  const int n_groups = (L + SG - 1) / SG;
-  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
-
-  // Q^T and dO^T fragments; delta0 = rowsum(o * do) from the same rows
-  bf16x8 qf[KS], df[KS];
-  float dl = 0.f;
+  // Q^T, dO^T and o rows and the lse, issued right after the routing loads
+  // (loads retire in issue order, so the routing can be used while these are
+  // still in flight across the LDS barriers below)
+  bf16x8 qf[KS], df[KS], of[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     if (tok_ok) {
       const long off = tok * D + (long)h * HD + 16 * ks + 8 * g;
       qf[ks] = *reinterpret_cast<const bf16x8*>(q + off);
       df[ks] = *reinterpret_cast<const bf16x8*>(dout + off);
-      const bf16x8 of = *reinterpret_cast<const bf16x8*>(o + off);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dl = fmaf((float)of[e], (float)df[ks][e], dl);
+      of[ks] = *reinterpret_cast<const bf16x8*>(o + off);
     } else {
       qf[ks] = bf16x8{};
       df[ks] = bf16x8{};
+      of[ks] = bf16x8{};
     }
   }
-  dl = wave_sum_pair(dl);
   const float lse_t = tok_ok ? lse[(long)h * N + tok] : 0.f;
+  for (int e = tid; e < E; e += 256) flags[e] = 0;
+  if constexpr (HD < 32) {
+    for (int i = tid; i < SG * PITCH; i += 256) k_lds[i] = 0;  // K^T rows beyond HD stay zero
+  }
+  lds_barrier();
+  if (g == 0 && tok_ok) {
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+  }
+  lds_barrier();
+  const int n_groups = (L + SG - 1) / SG;
+  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
+
+  // delta0 = rowsum(o * do) from the rows loaded above
+  float dl = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dl = fmaf((float)of[ks][e], (float)df[ks][e], dl);
+  dl = wave_sum_pair(dl);
 
   f32x16 acc_dq[NO];
 #pragma unroll
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
   }
   float dx = 0.f;
 
-  __syncthreads();
+  lds_barrier();
   const int n_act = n_active;
 
   constexpr int VEC = SG * HD / 8;
@@ -152,9 +158,9 @@ __global__ __launch_bounds__(256) void read_bwd_dq_kernel(
 
   for (int it = 0; it < n_act; ++it) {
     const int gi = groups[it];
-    __syncthreads();
+    lds_barrier();
     store_group();
-    __syncthreads();
+    lds_barrier();
     if (it + 1 < n_act) load_group(groups[it + 1]);
 
     // a wave whose 32 tokens select no block of the group has P = 0 there:
@@ -518,9 +524,9 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   }
   if (i_begin + 1 < i_end) fetch_tokens(tiles[i_begin + 1]);
   for (int it = i_begin; it < i_end; ++it) {
-    __syncthreads();  // the previous tile's LDS reads are done
+    lds_barrier();  // the previous tile's LDS reads are done
     store_tile();
-    __syncthreads();
+    lds_barrier();
     if (it + 1 < i_end) load_tile();                       // in flight during the math below
     if (it + 2 < i_end) fetch_tokens(tiles[it + 2]);       // the tokens of the tile after
 
@@ -589,28 +595,28 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   }
 
   // ---- sum the two token halves (fixed order), write this share's partials
-  __syncthreads();
+  lds_barrier();
   if (half == 1) {
 #pragma unroll
     for (int j = 0; j < NO; ++j)
 #pragma unroll
       for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dk[j][vv];
   }
-  __syncthreads();
+  lds_barrier();
   if (half == 0) {
 #pragma unroll
     for (int j = 0; j < NO; ++j)
 #pragma unroll
       for (int vv = 0; vv < 16; ++vv) acc_dk[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
   }
-  __syncthreads();
+  lds_barrier();
   if (half == 1) {
 #pragma unroll
     for (int j = 0; j < NO; ++j)
 #pragma unroll
       for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dv[j][vv];
   }
-  __syncthreads();
+  lds_barrier();
   if (half == 0 && slot_ok) {
 #pragma unroll
     for (int j = 0; j < NO; ++j) {

@@ -67,22 +67,9 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
   // ---- routing of this lane's token; active-block flags of the workgroup
   TokenRoute<TK> rt;
   load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
-  for (int e = tid; e < E; e += NT) flags[e] = 0;
-  if constexpr (HD < 32) {
-    // feature columns HD..31 of the V tiles stay zero (V^T rows beyond HD)
-    for (int i = tid; i < 2 * TILE; i += NT) v_lds[i] = 0;
-  }
-  __syncthreads();
-  if (g == 0 && tok_ok) {
-#pragma unroll
-    for (int t = 0; t < TK; ++t)
-      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
-  }
-  __syncthreads();
-  const int n_groups = (L + SG - 1) / SG;
-  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
-
-  // ---- Q^T fragments (B operand): lane holds q[token][16*ks + 8*g .. +8]
+  // Q^T fragments (B operand): lane holds q[token][16*ks + 8*g .. +8]; issued
+  // right after the routing loads (loads retire in issue order, so the
+  // routing can be used while these are in flight across the LDS barriers)
   bf16x8 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -91,13 +78,27 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
     else
       qf[ks] = bf16x8{};
   }
+  for (int e = tid; e < E; e += NT) flags[e] = 0;
+  if constexpr (HD < 32) {
+    // feature columns HD..31 of the V tiles stay zero (V^T rows beyond HD)
+    for (int i = tid; i < 2 * TILE; i += NT) v_lds[i] = 0;
+  }
+  lds_barrier();
+  if (g == 0 && tok_ok) {
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+  }
+  lds_barrier();
+  const int n_groups = (L + SG - 1) / SG;
+  if (wave == 0) build_group_list<SG>(flags, E, L, block_size, n_groups, groups, &n_active);
 
   f32x16 acc_o[NO];
 #pragma unroll
   for (int j = 0; j < NO; ++j) acc_o[j] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
 
-  __syncthreads();
+  lds_barrier();
   const int n_act = n_active;
 
   // staging: K and V rows of a group (SG x HD) as 16-byte vectors
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
     load_group(groups[0]);
     store_group(0);
   }
-  __syncthreads();
+  lds_barrier();
 
   for (int it = 0; it < n_act; ++it) {
     const int gi = groups[it];
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
       }
     }
     if (it + 1 < n_act) store_group(buf ^ 1);  // that buffer was last read before the previous barrier
-    __syncthreads();
+    lds_barrier();
   }
 
   // ---- epilogue: normalise, store o (bf16) and the log2-domain lse
@@ -572,11 +573,13 @@ static void fwd_wide_inst(const void* q, const void* k, const void* v, const int
 
 // The wide kernel covers block sizes that are multiples of 32 whose stage
 // slices tile the block (block_size % SG == 0, or block_size < SG dividing it)
-// and head_dim 32/64/128; NAYLIS_READ_FWD_WIDE=0 selects the narrow kernel.
+// and head_dim 32/64/128.  It is opt-in (NAYLIS_READ_FWD_WIDE=1): on MI355X at
+// config 2 the narrow kernel measured faster (47 vs 53 us), its per-workgroup
+// latency (route -> Q -> first stage) being spread over more workgroups.
 static bool fwd_wide_enabled() {
   static const bool v = [] {
     const char* e = getenv("NAYLIS_READ_FWD_WIDE");
-    return !(e && e[0] == '0');
+    return e && e[0] == '1';
   }();
   return v;
 }
