@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 3
+#define NAYLIS_MOM_ABI_VERSION 4
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -202,6 +202,42 @@ size_t naylis_mom_rezero_workspace_bytes(int64_t n);
 int naylis_mom_rezero_fwd(const void* z, int z_dtype, const float* s, float* y, int64_t n, void* stream);
 int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dtype, const float* s, void* dz, float* ds,
                           void* workspace, size_t workspace_bytes, int64_t n, void* stream);
+
+/* --------------------------------------------------------- decode step ---
+ * One new token per sequence: the O(1) running-sum form of the prefix-mean
+ * router that model.py:172-173 describes (the reference itself recomputes
+ * the cumsum over the whole sequence, model.py:169-176, and has no decode
+ * path: no reference entry point is replaced), then the gated read of the
+ * token's top-k blocks from an fp8 bank.
+ *
+ * naylis_mom_bank_quant_fp8: K / V (L, D) bf16 -> OCP fp8 e4m3 codes (L, D)
+ * uint8 and one fp32 scale per slot row, scale = max|row| / 448 (1 for an
+ * all-zero row), code = e4m3fn(x / scale) rounded to nearest even.  Run once
+ * per bank (the bank is fixed at inference).
+ *
+ * naylis_mom_decode_step, per sequence b:
+ *   S' = S + x_new             state_in / state_out (B, D) fp64 (sum of the
+ *                              tokens so far; must not overlap)
+ *   h = fp32(S') / fp32(t_prev[b] + 1)     t_prev (B,) int32 >= 0, the
+ *                              number of earlier tokens
+ *   logits = w_up tanh(w_down h)           w_down (R, D), w_up (E, R) fp32
+ *   top_idx (B, top_k) int32 = top-k logits (ties to the lower id),
+ *   top_gates (B, top_k) fp32 = softmax over them (model.py:209-220)
+ *   out (B, H, D/H) bf16 = softmax_n(q . k_n / sqrt(D/H) + log gate) v_n over
+ *   the slots n of the selected blocks (mom_kernels/reference.py:39-61 with the
+ *   bias of reference.py:14-29), q = q_new (B, H, D/H) bf16 and
+ *   k_n = k_scale[n] e4m3(k8[n]), v_n = v_scale[n] e4m3(v8[n]).
+ * x_new in x_dtype.  E = number of bank blocks, L = E * block_size.
+ * Constraints: D = H * head_dim with head_dim in {32, 64, 128}, D <= 4096,
+ * R <= 64, E <= 64, top_k <= min(8, E), top_k * block_size <= 1024, pointers
+ * 16-byte aligned. */
+int naylis_mom_bank_quant_fp8(const void* k, const void* v, uint8_t* k8, uint8_t* v8, float* k_scale, float* v_scale,
+                              int64_t L, int64_t D, void* stream);
+int naylis_mom_decode_step(const double* state_in, double* state_out, const int32_t* t_prev, const void* x_new,
+                           int x_dtype, const float* w_down, const float* w_up, const void* q_new, const uint8_t* k8,
+                           const uint8_t* v8, const float* k_scale, const float* v_scale, void* out, int32_t* top_idx,
+                           float* top_gates, int64_t B, int64_t D, int64_t H, int64_t R, int64_t E, int64_t block_size,
+                           int64_t top_k, void* stream);
 
 /* -------------------------------------------------------------- timing ---
  * Optional instrumentation (no counterpart in the reference; for benchmarks):

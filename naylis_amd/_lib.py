@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -49,6 +49,8 @@ SIGNATURES = {
     "naylis_mom_linear_wgrad": (_int, [_c_void_p] * 3 + [_int, _c_void_p, _size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
+    "naylis_mom_bank_quant_fp8": (_int, [_c_void_p] * 6 + [_i64] * 2 + [_c_void_p]),
+    "naylis_mom_decode_step": (_int, [_c_void_p] * 4 + [_int] + [_c_void_p] * 10 + [_i64] * 7 + [_c_void_p]),
     "naylis_mom_timing_enable": (None, [_int]),
     "naylis_mom_timing_reset": (None, []),
     "naylis_mom_timing_get": (_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),

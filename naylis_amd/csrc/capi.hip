@@ -417,3 +417,69 @@ int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dty
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- decode step
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool overlap(const void* a, const void* b, size_t bytes) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bytes && y < x + bytes;
+}
+
+}  // namespace
+
+extern "C" {
+
+int naylis_mom_bank_quant_fp8(const void* k, const void* v, uint8_t* k8, uint8_t* v8, float* k_scale, float* v_scale,
+                              int64_t L, int64_t D, void* stream) {
+  if (L < 0 || D <= 0 || L > NAYLIS_MAX_SLOTS || D > 65536)
+    return fail(NAYLIS_ERR_ARG, "bank_quant_fp8: bad shape L=%lld D=%lld", (long long)L, (long long)D);
+  if (L == 0) return NAYLIS_OK;
+  if (!k || !v || !k8 || !v8 || !k_scale || !v_scale)
+    return fail(NAYLIS_ERR_ARG, "bank_quant_fp8: null pointer argument");
+  return hip_status(launch_bank_quant_fp8(k, v, k8, v8, k_scale, v_scale, (int)L, (int)D, (hipStream_t)stream),
+                    "bank_quant_fp8");
+}
+
+int naylis_mom_decode_step(const double* state_in, double* state_out, const int32_t* t_prev, const void* x_new,
+                           int x_dtype, const float* w_down, const float* w_up, const void* q_new, const uint8_t* k8,
+                           const uint8_t* v8, const float* k_scale, const float* v_scale, void* out, int32_t* top_idx,
+                           float* top_gates, int64_t B, int64_t D, int64_t H, int64_t R, int64_t E, int64_t block_size,
+                           int64_t top_k, void* stream) {
+  int rc;
+  if ((rc = check_dtype(x_dtype, "decode_step"))) return rc;
+  if (B < 0 || B > 65535 || H <= 0 || D <= 0 || D % H != 0)
+    return fail(NAYLIS_ERR_ARG, "decode_step: bad shape B=%lld D=%lld H=%lld", (long long)B, (long long)D,
+                (long long)H);
+  const int64_t hd = D / H;
+  if (hd != 32 && hd != 64 && hd != 128)
+    return fail(NAYLIS_ERR_ARG, "decode_step: head_dim %lld must be 32, 64 or 128", (long long)hd);
+  if (D > kDecodeMaxD) return fail(NAYLIS_ERR_ARG, "decode_step: D %lld exceeds %d", (long long)D, kDecodeMaxD);
+  if (R <= 0 || R > kDecodeMaxRank)
+    return fail(NAYLIS_ERR_ARG, "decode_step: router rank %lld must be in [1, %d]", (long long)R, kDecodeMaxRank);
+  if (E <= 0 || E > kDecodeMaxExperts)
+    return fail(NAYLIS_ERR_ARG, "decode_step: num_blocks %lld must be in [1, %d]", (long long)E, kDecodeMaxExperts);
+  if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > E)
+    return fail(NAYLIS_ERR_ARG, "decode_step: top_k %lld must be in [1, min(%d, num_blocks)]", (long long)top_k,
+                NAYLIS_MAX_TOPK);
+  if (block_size <= 0 || top_k * block_size > kDecodeMaxSlots)
+    return fail(NAYLIS_ERR_ARG, "decode_step: top_k * block_size (%lld) must be in [1, %d]",
+                (long long)(top_k * block_size), kDecodeMaxSlots);
+  if (B == 0) return NAYLIS_OK;
+  if (!state_in || !state_out || !t_prev || !x_new || !w_down || !w_up || !q_new || !k8 || !v8 || !k_scale ||
+      !v_scale || !out || !top_idx || !top_gates)
+    return fail(NAYLIS_ERR_ARG, "decode_step: null pointer argument");
+  if (!aligned16(w_down) || !aligned16(q_new) || !aligned16(k8) || !aligned16(v8))
+    return fail(NAYLIS_ERR_ARG, "decode_step: w_down, q_new, k8 and v8 must be 16-byte aligned");
+  if (overlap(state_in, state_out, (size_t)B * D * sizeof(double)))
+    return fail(NAYLIS_ERR_ARG, "decode_step: state_in and state_out overlap");
+  DecodeDims d{(int)B, (int)D, (int)H, (int)hd, (int)R, (int)E, (int)block_size, (int)top_k};
+  return hip_status(launch_decode_step(state_in, state_out, t_prev, x_new, x_dtype == NAYLIS_DTYPE_F32, w_down, w_up,
+                                       q_new, k8, v8, k_scale, v_scale, out, top_idx, top_gates, d,
+                                       (hipStream_t)stream),
+                    "decode_step");
+}
+
+}  // extern "C"

@@ -40,6 +40,24 @@ hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, co
                                   const float* top_gates, void* dk, void* dv, float* dgates, int n_chunks,
                                   const ReadDims& d, hipStream_t st);
 
+// Decode step (decode.hip): B sequences, D = H * HD features, router rank R,
+// E experts (= bank blocks) of block_size slots, top-k blocks per token.
+struct DecodeDims {
+  int B, D, H, HD, R, E, block_size, topk;
+};
+constexpr int kDecodeMaxD = 4096;      // prefix mean held in LDS
+constexpr int kDecodeMaxRank = 64;     // router rank
+constexpr int kDecodeMaxExperts = 64;  // one wave's lanes rank the experts
+constexpr int kDecodeMaxSlots = 1024;  // top_k * block_size scores per head in LDS
+
+// fp8 e4m3 (OCP) bank with one fp32 scale per slot row, from bf16 K / V (L, D)
+hipError_t launch_bank_quant_fp8(const void* k, const void* v, uint8_t* k8, uint8_t* v8, float* k_scale,
+                                 float* v_scale, int L, int D, hipStream_t st);
+hipError_t launch_decode_step(const double* state_in, double* state_out, const int32_t* t_prev, const void* x_new,
+                              bool x_f32, const float* w_down, const float* w_up, const void* q_new,
+                              const uint8_t* k8, const uint8_t* v8, const float* k_scale, const float* v_scale,
+                              void* out, int32_t* top_idx, float* top_gates, const DecodeDims& d, hipStream_t st);
+
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }

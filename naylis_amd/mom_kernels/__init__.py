@@ -10,7 +10,9 @@ silent eager fallback (the eager maths lives only in the test oracle).
 
 New entry points beyond the reference (it has no kernel boundary for them):
 ``mom_route`` (fused prefix-mean router) and ``mom_bank_kv`` (bank K/V
-projection), used by ``naylis_amd.layer.MoMLayer``.
+projection), used by ``naylis_amd.layer.MoMLayer``; ``quantize_bank_fp8`` and
+``decode_step``, the one-token inference step over an fp8 bank (the reference
+has no decode path).
 """
 from __future__ import annotations
 
@@ -20,7 +22,7 @@ from .. import _lib
 from .hip_read import mom_read as _hip_mom_read
 
 __all__ = ["HAS_HIP", "preflight", "resolve_mode", "mom_read", "announce", "mom_route",
-           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip"]
+           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step"]
 
 _ANNOUNCED = {"backend": None}
 
@@ -113,3 +115,13 @@ def mom_linear(*args, **kwargs):
 def mom_rezero(*args, **kwargs):
     from .hip_rezero import mom_rezero as _rezero
     return _rezero(*args, **kwargs)
+
+
+def quantize_bank_fp8(*args, **kwargs):
+    from .hip_decode import quantize_bank_fp8 as _quant
+    return _quant(*args, **kwargs)
+
+
+def decode_step(*args, **kwargs):
+    from .hip_decode import decode_step as _step
+    return _step(*args, **kwargs)

@@ -90,6 +90,32 @@ def test_router_and_bank_reject_bad_arguments(lib):
     assert lib.naylis_mom_bank_kv_bwd(1, 1, 1, 1, 1, 1, 9, 1, 1, 0, 64, 32, 32, None) == _lib.NAYLIS_ERR_ARG
 
 
+DEC_OK = dict(B=64, D=1024, H=16, R=32, E=8, bs=128, k=2)
+
+
+def decode(lib, state_out=0x2000000, x_dtype=1, **kw):
+    a = dict(DEC_OK, **kw)
+    p = 0x1000  # 16-byte aligned stand-in pointers: validation runs before any device work
+    return lib.naylis_mom_decode_step(0x1000000, state_out, p, p, x_dtype, p, p, p, p, p, p, p, p, p, p, a["B"],
+                                      a["D"], a["H"], a["R"], a["E"], a["bs"], a["k"], None)
+
+
+@pytest.mark.parametrize("bad", [dict(H=12), dict(D=1000), dict(H=64), dict(D=8192, H=64), dict(R=65),
+                                 dict(R=0), dict(E=65), dict(k=0), dict(k=9), dict(k=3, E=2), dict(bs=0),
+                                 dict(k=8, bs=256), dict(B=-1), dict(x_dtype=5), dict(state_out=0x1000400)])
+def test_decode_rejects_bad_arguments(lib, bad):
+    assert decode(lib, **bad) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_last_error().startswith(b"decode_step")
+    assert decode(lib, B=0) == _lib.NAYLIS_OK  # nothing to do, no pointer touched
+
+
+def test_bank_quant_rejects_bad_arguments(lib):
+    assert lib.naylis_mom_bank_quant_fp8(1, 1, 1, 1, 1, 1, -1, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_bank_quant_fp8(1, 1, 1, 1, 1, 1, 64, 0, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_bank_quant_fp8(None, 1, 1, 1, 1, 1, 64, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_bank_quant_fp8(None, None, None, None, None, None, 0, 64, None) == _lib.NAYLIS_OK
+
+
 def test_error_message_is_per_thread(lib):
     import threading
     read_fwd(lib, hd=96)

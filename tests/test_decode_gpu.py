@@ -1,0 +1,200 @@
+"""GPU parity of the decode step (C ABI naylis_mom_decode_step and
+naylis_mom_bank_quant_fp8) against the CPU oracle's decode_step, the O(1)
+running-sum form of model.py:169-220 plus the read of
+mom_kernels/reference.py:39-61.
+
+* The fp8 quantizer's codes and scales are bit-exact with torch's
+  float8_e4m3fn conversion of x / (max|row| / 448) on the CPU, including
+  round-to-nearest-even ties in the normal and subnormal ranges and all-zero
+  rows.
+* The new state is bit-exact (one fp64 add); top_idx equals the oracle's
+  outside near-ties (fp64 k-th / (k+1)-th logit margin below
+  1e-5 * max|logit|, decided by fp32 summation order); gates to fp32
+  rounding; out (bf16) within the north-star tolerance rtol 2e-2 / atol 2e-3
+  of the oracle read over the dequantized fp8 bank.
+* Against a bf16 bank (config 5's stated reference) the fp8 bank's error is
+  quantisation error: e4m3 keeps 3 mantissa bits, a relative rounding error
+  of at most 2^-4 (rms about 2^-4 / sqrt(3) = 0.036) per element, and
+  out = sum_n p_n v_n carries the same weights on the errors as on the
+  values, so out's relative error stays near that figure.  Bound: relative
+  Frobenius error <= 0.05 over the batch, <= 0.1 per (sequence, head).
+* Stepping a sequence token by token through the decode step reproduces the
+  full-sequence router and read of the same tokens (the prefix mean of step
+  t is the fp32 cumsum / (t+1) of the whole sequence).
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from naylis_amd.mom_kernels.hip_decode import Fp8Bank, decode_step, quantize_bank_fp8
+from tests._tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def torch_fp8_codes(x):
+    """CPU reference quantizer: scale = amax / 448 per row, torch's e4m3fn cast."""
+    xf = x.float().cpu()
+    amax = xf.abs().amax(dim=1)
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    codes = (xf / scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    return codes, scale
+
+
+def test_quantizer_matches_torch_e4m3fn(dev):
+    g = torch.Generator().manual_seed(3)
+    L, D = 512, 1024
+    k = (torch.randn(L, D, generator=g) * 0.05).bfloat16()
+    v = (torch.randn(L, D, generator=g) * torch.rand(L, 1, generator=g) * 3).bfloat16()
+    k[7] = 0  # all-zero row: scale 1, codes 0
+    # rows whose amax is 448 (scale exactly 1): ties between e4m3 neighbours
+    tie = torch.tensor([448.0, 1.0625, 1.1875, -1.0625, 3 * 2.0 ** -10, 2.0 ** -10, 5 * 2.0 ** -10, 0.0,
+                        -3 * 2.0 ** -10, 2.0 ** -11, 240.0 + 8.0, 17.0, 19.0, -2.0 ** -9])
+    k[9, :tie.numel()] = tie.bfloat16()
+    k[9, tie.numel():] = 0
+    v[11, :tie.numel()] = (-tie).bfloat16()
+    v[11, tie.numel():] = 0
+    bank = quantize_bank_fp8(k.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    for name, src, codes, scale in (("k", k, bank.k8, bank.k_scale), ("v", v, bank.v8, bank.v_scale)):
+        want_c, want_s = torch_fp8_codes(src)
+        assert torch.equal(scale.cpu(), want_s), f"{name} scales differ"
+        got = codes.cpu()
+        bad = (got != want_c).nonzero()
+        assert bad.numel() == 0, (f"{name}: {bad.shape[0]} codes differ, first at {bad[0].tolist()}: "
+                                  f"got {int(got[tuple(bad[0])])} want {int(want_c[tuple(bad[0])])}")
+    # the tie row by hand (scale 1): e4m3 neighbours 1 | 1.125 | 1.25, subnormal quantum 2^-9,
+    # 240 | 256 in [128, 256), 16 | 18 | 20 in [16, 32); ties go to the even mantissa
+    q = 2.0 ** -9
+    want = torch.tensor([448.0, 1.0, 1.25, -1.0, 2 * q, 0.0, 2 * q, 0.0, -2 * q, 0.0, 256.0, 16.0, 20.0, -q])
+    kd, vd = bank.dequantize()
+    assert torch.equal(kd[9, :tie.numel()].cpu(), want)
+    assert torch.equal(vd[11, :tie.numel()].cpu(), -want)
+
+
+def make_step(B, D, H, R, E, BS, seed, x_dtype=torch.bfloat16, max_prior=4096):
+    g = torch.Generator().manual_seed(seed)
+    L = E * BS
+    M = torch.randn(L, D, generator=g)
+    M = M * (63.0 / M.norm())  # late-training bank magnitude (Frobenius 63)
+    wk = torch.randn(D, D, generator=g) / math.sqrt(D)
+    wv = torch.randn(D, D, generator=g) / math.sqrt(D)
+    k = (M @ wk.t()).bfloat16()
+    v = (M @ wv.t()).bfloat16()
+    t_prev = torch.randint(1, max_prior + 1, (B,), generator=g)
+    # a running sum of t_prev unit tokens: random walk of that length
+    state = torch.randn(B, D, generator=g, dtype=torch.float64) * t_prev.double().sqrt()[:, None]
+    x = torch.randn(B, D, generator=g).to(x_dtype)
+    w_down = torch.randn(R, D, generator=g) * 0.02
+    w_up = torch.randn(E, R, generator=g) * 0.02
+    q = torch.randn(B, H, D // H, generator=g).bfloat16()
+    return k, v, t_prev, state, x, w_down, w_up, q
+
+
+def near_tie_rows(state, t_prev, x, w_down, w_up, K):
+    """Rows whose fp64 k-th / (k+1)-th logit margin is below 1e-5 * max|logit|."""
+    s = state.double() + x.double()
+    h = (s.float() / (t_prev + 1).float()[:, None]).double()
+    logits = torch.tanh(h @ w_down.double().t()) @ w_up.double().t()
+    if K >= logits.shape[1]:
+        return torch.zeros(logits.shape[0], dtype=torch.bool)
+    srt = logits.sort(-1, descending=True).values
+    return (srt[:, K - 1] - srt[:, K]) < 1e-5 * logits.abs().max()
+
+
+def run_case(dev, B, D, H, R, E, BS, K, seed, x_dtype=torch.bfloat16, max_prior=4096):
+    k, v, t_prev, state, x, w_down, w_up, q = make_step(B, D, H, R, E, BS, seed, x_dtype, max_prior)
+    bank = quantize_bank_fp8(k.to(dev), v.to(dev))
+    out, new_state, idx, gates = decode_step(state.to(dev), t_prev.to(dev), x.to(dev), w_down.to(dev),
+                                             w_up.to(dev), K, q.to(dev), bank, E, BS)
+    torch.cuda.synchronize()
+    kd, vd = bank.dequantize()
+    o_ref, s_ref, i_ref, g_ref = oracle.decode_step(state, t_prev, x, w_down, w_up, K, q, kd.cpu(), vd.cpu(), E, BS)
+    assert torch.equal(new_state.cpu(), s_ref), "running state differs from state + x"
+    tie = near_tie_rows(state, t_prev, x, w_down, w_up, K)
+    same = (idx.cpu().long() == i_ref).all(dim=1)
+    assert bool((same | tie).all()), f"top_idx differs on {int((~same & ~tie).sum())} rows without a near-tie"
+    assert int((~same).sum()) <= max(1, B // 16), "too many near-tie rows"
+    rows = same.nonzero().flatten()
+    assert_close(gates.cpu()[rows], g_ref[rows], "gates", rtol=1e-5, atol=1e-6)
+    assert_close(out.cpu()[rows].float(), o_ref[rows], "out (fp8 bank)")
+    return out.cpu()[rows].float(), (state, t_prev, x, w_down, w_up, q, k, v), rows
+
+
+def test_decode_step_config5(dev):
+    """Config 5: B=64, d=1024, 16 x 64 heads, router rank 32, bank 8 x 128, top-2, prior lengths 1..4096."""
+    B, D, H, R, E, BS, K = 64, 1024, 16, 32, 8, 128, 2
+    out, (state, t_prev, x, w_down, w_up, q, k, v), rows = run_case(dev, B, D, H, R, E, BS, K, seed=11)
+    # against the bf16 bank (no quantisation): fp8 rounding error only
+    o_bf16, _, _, _ = oracle.decode_step(state, t_prev, x, w_down, w_up, K, q, k.float(), v.float(), E, BS)
+    o_bf16 = o_bf16[rows]
+    rel = float((out - o_bf16).norm() / o_bf16.norm())
+    per = ((out - o_bf16).norm(dim=-1) / o_bf16.norm(dim=-1)).max()
+    assert rel <= 0.05, f"fp8 bank vs bf16 bank: relative error {rel:.4f}"
+    assert float(per) <= 0.1, f"fp8 bank vs bf16 bank: worst (sequence, head) relative error {float(per):.4f}"
+
+
+@pytest.mark.parametrize("B,D,H,R,E,BS,K,x_dtype", [
+    (1, 1024, 16, 32, 8, 128, 2, torch.bfloat16),    # one sequence
+    (5, 512, 16, 8, 4, 64, 1, torch.float32),        # top-1, fp32 tokens
+    (7, 768, 6, 16, 16, 48, 3, torch.bfloat16),      # top-3 (TK 8 path), block not a multiple of 64, H % 4 != 0
+    (3, 2048, 16, 64, 64, 16, 8, torch.float32),     # head_dim 128, 64 experts, top-8, max router rank
+    (4, 256, 8, 4, 8, 128, 8, torch.bfloat16),       # head_dim 32, top-k = E (reads the whole bank)
+    (2, 4096, 32, 32, 8, 128, 2, torch.bfloat16),    # largest D
+])
+def test_decode_step_shapes(dev, B, D, H, R, E, BS, K, x_dtype):
+    run_case(dev, B, D, H, R, E, BS, K, seed=B * 100 + K, x_dtype=x_dtype)
+
+
+def test_decode_step_first_token(dev):
+    """t_prev = 0 and a zero state: h = x itself."""
+    B, D, H, R, E, BS, K = 8, 1024, 16, 32, 8, 128, 2
+    k, v, _, _, x, w_down, w_up, q = make_step(B, D, H, R, E, BS, seed=5)
+    bank = quantize_bank_fp8(k.to(dev), v.to(dev))
+    zero = torch.zeros(B, D, dtype=torch.float64)
+    t0 = torch.zeros(B, dtype=torch.int32)
+    out, st, idx, gates = decode_step(zero.to(dev), t0.to(dev), x.to(dev), w_down.to(dev), w_up.to(dev), K,
+                                      q.to(dev), bank, E, BS)
+    kd, vd = bank.dequantize()
+    o_ref, s_ref, i_ref, g_ref = oracle.decode_step(zero, t0, x, w_down, w_up, K, q, kd.cpu(), vd.cpu(), E, BS)
+    assert torch.equal(st.cpu(), x.double())
+    tie = near_tie_rows(zero, t0, x, w_down, w_up, K)
+    same = (idx.cpu().long() == i_ref).all(dim=1)
+    assert bool((same | tie).all())
+    rows = same.nonzero().flatten()
+    assert_close(out.cpu()[rows].float(), o_ref[rows], "out")
+
+
+def test_decode_steps_reproduce_full_sequence(dev):
+    """T steps of the decode loop (ping-pong state buffers) give the full-sequence
+    router's choice and the read of each position (oracle.router + mom_attention)."""
+    B, T, D, H, R, E, BS, K = 3, 96, 1024, 16, 32, 8, 128, 2
+    g = torch.Generator().manual_seed(21)
+    k, v, _, _, _, w_down, w_up, _ = make_step(B, D, H, R, E, BS, seed=21)
+    xs = torch.randn(B, T, D, generator=g).bfloat16()
+    qs = torch.randn(B, T, H, D // H, generator=g).bfloat16()
+    bank = quantize_bank_fp8(k.to(dev), v.to(dev))
+    kd, vd = (t.cpu() for t in bank.dequantize())
+    _, _, i_full, g_full, _ = oracle.router(xs, w_down, w_up, K)
+    bias = oracle.build_gate_bias(i_full, g_full, E, BS, torch.float32)
+    o_full = oracle.mom_attention(qs.float(), kd, vd, bias)
+    x_dev, q_dev = xs.to(dev), qs.to(dev)
+    st = [torch.zeros(B, D, dtype=torch.float64, device=dev), torch.empty(B, D, dtype=torch.float64, device=dev)]
+    wd, wu = w_down.to(dev), w_up.to(dev)
+    outs, idxs = [], []
+    for t in range(T):
+        tp = torch.full((B,), t, dtype=torch.int32, device=dev)
+        o, _, i, _ = decode_step(st[t % 2], tp, x_dev[:, t], wd, wu, K, q_dev[:, t], bank, E, BS,
+                                 out_state=st[(t + 1) % 2])
+        outs.append(o)
+        idxs.append(i)
+    torch.cuda.synchronize()
+    out = torch.stack(outs, 1).cpu()
+    idx = torch.stack(idxs, 1).cpu().long()
+    assert torch.equal(st[T % 2].cpu(), xs.double().sum(1)), "running sum after T steps"
+    same = (idx == i_full).all(-1)
+    assert float(same.float().mean()) >= 0.98, "decode-loop routing differs from the full-sequence router"
+    m = same.nonzero(as_tuple=True)
+    assert_close(out[m].float(), o_full[m], "out (decode loop vs full sequence)")
