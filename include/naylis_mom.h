@@ -229,7 +229,7 @@ int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dty
  *   k_n = k_scale[n] e4m3(k8[n]), v_n = v_scale[n] e4m3(v8[n]).
  * x_new in x_dtype.  E = number of bank blocks, L = E * block_size.
  * Constraints: D = H * head_dim with head_dim in {32, 64, 128}, D <= 4096,
- * R <= 64, E <= 64, top_k <= min(8, E), top_k * block_size <= 1024, pointers
+ * R <= 64, E <= 64, top_k <= min(8, E), E * block_size <= 16384, pointers
  * 16-byte aligned. */
 int naylis_mom_bank_quant_fp8(const void* k, const void* v, uint8_t* k8, uint8_t* v8, float* k_scale, float* v_scale,
                               int64_t L, int64_t D, void* stream);

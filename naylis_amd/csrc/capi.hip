@@ -464,9 +464,9 @@ int naylis_mom_decode_step(const double* state_in, double* state_out, const int3
   if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > E)
     return fail(NAYLIS_ERR_ARG, "decode_step: top_k %lld must be in [1, min(%d, num_blocks)]", (long long)top_k,
                 NAYLIS_MAX_TOPK);
-  if (block_size <= 0 || top_k * block_size > kDecodeMaxSlots)
-    return fail(NAYLIS_ERR_ARG, "decode_step: top_k * block_size (%lld) must be in [1, %d]",
-                (long long)(top_k * block_size), kDecodeMaxSlots);
+  if (block_size <= 0 || E * block_size > NAYLIS_MAX_SLOTS)
+    return fail(NAYLIS_ERR_ARG, "decode_step: num_blocks * block_size (%lld) must be in [1, %d]",
+                (long long)(E * block_size), NAYLIS_MAX_SLOTS);
   if (B == 0) return NAYLIS_OK;
   if (!state_in || !state_out || !t_prev || !x_new || !w_down || !w_up || !q_new || !k8 || !v8 || !k_scale ||
       !v_scale || !out || !top_idx || !top_gates)

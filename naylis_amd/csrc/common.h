@@ -118,6 +118,58 @@ __device__ __forceinline__ float wave_max_pair(float x) {
 }
 __device__ __forceinline__ float wave_sum_pair(float x) { return x + __shfl_xor(x, 32, 64); }
 
+// Cross-lane exchanges that stay in the VALU (DPP and the gfx950 permlane
+// swaps) instead of going through the LDS crossbar as __shfl_xor does.
+// DPP controls: quad_perm [1,0,3,2] = 0xb1 (lane ^ 1), [2,3,0,1] = 0x4e
+// (lane ^ 2), row_half_mirror = 0x141 (i <-> 7 - i in eight lanes),
+// row_mirror = 0x140 (i <-> 15 - i in a row of sixteen), row_ror:n = 0x120 + n.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+// lane l combined with lane l ^ 16 (row pairs) and with lane l ^ 32 (wave halves)
+template <typename F>
+__device__ __forceinline__ float xor16_f32(float x, F op) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <typename F>
+__device__ __forceinline__ float xor32_f32(float x, F op) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Butterfly all-reduce over the 64 lanes: every lane gets the same result
+// (each step combines two equal-shaped partials with a commutative op).
+template <typename F>
+__device__ __forceinline__ float wave_allreduce_f32(float x, F op) {
+  x = op(x, dpp_f32<0xb1>(x));
+  x = op(x, dpp_f32<0x4e>(x));
+  x = op(x, dpp_f32<0x141>(x));
+  x = op(x, dpp_f32<0x140>(x));
+  x = xor16_f32(x, op);
+  return xor32_f32(x, op);
+}
+__device__ __forceinline__ float wave_allsum(float x) {
+  return wave_allreduce_f32(x, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float wave_allmax(float x) {
+  return wave_allreduce_f32(x, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ int wave_allmin_i32(int x) {
+  x = min(x, dpp_i32<0xb1>(x));
+  x = min(x, dpp_i32<0x4e>(x));
+  x = min(x, dpp_i32<0x141>(x));
+  x = min(x, dpp_i32<0x140>(x));
+  auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  x = min((int)r[0], (int)r[1]);
+  r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return min((int)r[0], (int)r[1]);
+}
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // operations, not for its outstanding global loads (a __syncthreads() fence
 // would also drain those, serialising prefetches that are meant to stay in

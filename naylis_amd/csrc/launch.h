@@ -48,7 +48,6 @@ struct DecodeDims {
 constexpr int kDecodeMaxD = 4096;      // prefix mean held in LDS
 constexpr int kDecodeMaxRank = 64;     // router rank
 constexpr int kDecodeMaxExperts = 64;  // one wave's lanes rank the experts
-constexpr int kDecodeMaxSlots = 1024;  // top_k * block_size scores per head in LDS
 
 // fp8 e4m3 (OCP) bank with one fp32 scale per slot row, from bf16 K / V (L, D)
 hipError_t launch_bank_quant_fp8(const void* k, const void* v, uint8_t* k8, uint8_t* v8, float* k_scale,

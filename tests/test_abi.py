@@ -102,7 +102,7 @@ def decode(lib, state_out=0x2000000, x_dtype=1, **kw):
 
 @pytest.mark.parametrize("bad", [dict(H=12), dict(D=1000), dict(H=64), dict(D=8192, H=64), dict(R=65),
                                  dict(R=0), dict(E=65), dict(k=0), dict(k=9), dict(k=3, E=2), dict(bs=0),
-                                 dict(k=8, bs=256), dict(B=-1), dict(x_dtype=5), dict(state_out=0x1000400)])
+                                 dict(bs=4096), dict(B=-1), dict(x_dtype=5), dict(state_out=0x1000400)])
 def test_decode_rejects_bad_arguments(lib, bad):
     assert decode(lib, **bad) == _lib.NAYLIS_ERR_ARG
     assert lib.naylis_mom_last_error().startswith(b"decode_step")

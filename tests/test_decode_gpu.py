@@ -143,6 +143,7 @@ def test_decode_step_config5(dev):
     (3, 2048, 16, 64, 64, 16, 8, torch.float32),     # head_dim 128, 64 experts, top-8, max router rank
     (4, 256, 8, 4, 8, 128, 8, torch.bfloat16),       # head_dim 32, top-k = E (reads the whole bank)
     (2, 4096, 32, 32, 8, 128, 2, torch.bfloat16),    # largest D
+    (2, 1024, 16, 32, 4, 512, 3, torch.bfloat16),    # 1536 slots per head: six chunks of the online softmax
 ])
 def test_decode_step_shapes(dev, B, D, H, R, E, BS, K, x_dtype):
     run_case(dev, B, D, H, R, E, BS, K, seed=B * 100 + K, x_dtype=x_dtype)
