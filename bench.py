@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """MoM layer forward+backward throughput on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config4]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config4|config5]
 
 Workload ("config2"): one Naylis MoM layer in bf16,
 forward + backward at the training shape B=8, T=2048, d=1024, 16 heads x 64,
@@ -16,6 +16,14 @@ steps; then, over K further steps with every library launch bracketed by HIP
 events on its launch stream, each kernel's average duration, the roofline of
 the dominant kernel and the read's own MFMA fraction on the tile-active basis;
 and a CPU baseline (the eager fp32 oracle on the host).
+
+config5 is the inference decode step instead: B=64
+sequences, one new token each, running prefix-sum state of prior length
+1..4096, d=1024, 16 x 64 heads, router rank 32, bank 8 x 128 quantised to fp8
+e4m3 with per-slot scales, top-2.  A step is one naylis_mom_decode_step for
+the 64 sequences (state ping-pong between two buffers); the K timed steps are
+one captured HIP graph of K steps, replayed once, so host launch cost stays
+out of the figure.  value = decoded tokens/s (B per step).
 """
 from __future__ import annotations
 
@@ -37,7 +45,9 @@ WORKLOADS = {
     # B, T, d, heads, blocks, block_size, top_k, rank
     "config2": dict(B=8, T=2048, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, tile_bias=None),
     "config4": dict(B=4, T=4096, D=1536, H=24, E=32, BS=128, K=2, R=32, bank_fro=None, tile_bias=(3, 6)),
+    "config5": dict(B=64, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, max_prior=4096),
 }
+DECODE_METRIC = "MoM decode step tokens/s at B=64, d=1024, fp8 8x128 bank"
 
 
 def build(cfg, device):
@@ -183,6 +193,150 @@ def cpu_baseline(cfg, sample_b):
                       f"(1 warmup, median of 3 runs: {med:.3f} s), torch {torch.__version__}"}
 
 
+def build_decode(cfg, device):
+    """Config-5 inputs: bank K / V from a random bank (Frobenius 63) and random
+    N(0, 1/d) projections, quantised once to fp8; states of random prior
+    lengths; new tokens and queries N(0, 1) in bf16."""
+    import math
+
+    import torch
+
+    from naylis_amd.mom_kernels.hip_decode import quantize_bank_fp8
+    B, D, H, E, BS, R = (cfg[k] for k in ("B", "D", "H", "E", "BS", "R"))
+    g = torch.Generator().manual_seed(0)
+    M = torch.randn(E * BS, D, generator=g)
+    M = M * (cfg["bank_fro"] / float(M.norm()))
+    wk = torch.randn(D, D, generator=g) / math.sqrt(D)
+    wv = torch.randn(D, D, generator=g) / math.sqrt(D)
+    k = (M @ wk.t()).bfloat16().to(device)
+    v = (M @ wv.t()).bfloat16().to(device)
+    bank = quantize_bank_fp8(k, v)
+    t_prev = torch.randint(1, cfg["max_prior"] + 1, (B,), generator=g)
+    state = torch.randn(B, D, generator=g, dtype=torch.float64) * t_prev.double().sqrt()[:, None]
+    x = torch.randn(B, D, generator=g).bfloat16()
+    q = torch.randn(B, H, D // H, generator=g).bfloat16()
+    w_down = torch.randn(R, D, generator=g) * 0.02
+    w_up = torch.randn(E, R, generator=g) * 0.02
+    to = lambda t: t.to(device)
+    return bank, (k, v), to(state), to(t_prev.int()), to(x), to(q), to(w_down), to(w_up)
+
+
+def decode_alg_bytes(cfg, idx):
+    """Unique bytes one decode launch must move: state in + out (fp64), token,
+    query and output (bf16), router weights (fp32), and the K / V rows (fp8)
+    and scales of every block some sequence selected (all heads)."""
+    B, D, E, BS, R = (cfg[k] for k in ("B", "D", "E", "BS", "R"))
+    blocks = len(set(int(i) for i in idx.flatten().tolist()))
+    return (B * D * 8 * 2 + B * D * 2 * 3 + (R * D + E * R) * 4
+            + blocks * BS * (2 * D + 2 * 4) + B * cfg["K"] * 8)
+
+
+def decode_cpu_baseline(cfg, bank_bf16, state, t_prev, x, q, w_down, w_up, reps=20):
+    """oracle.decode_step (fp32 router, dense read over the bf16 bank) on the
+    host cores for the whole B=64 batch, median of `reps` steps."""
+    import torch
+
+    import oracle
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    k, v = (t.float().cpu() for t in bank_bf16)
+    args = (state.cpu(), t_prev.cpu(), x.cpu(), w_down.cpu(), w_up.cpu(), cfg["K"], q.cpu(), k, v, cfg["E"],
+            cfg["BS"])
+    oracle.decode_step(*args)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.decode_step(*args)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(cfg["B"] / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle.decode_step fp32 over the bf16 bank, the full B={cfg['B']} batch, "
+                      f"median of {reps} steps ({med * 1e3:.3f} ms/step), torch {torch.__version__}"}
+
+
+def decode_bench(args, cfg, dev):
+    import torch
+
+    from naylis_amd import _lib
+    from naylis_amd.mom_kernels.hip_decode import decode_step
+    B, D, H, E, BS, K = (cfg[k] for k in ("B", "D", "H", "E", "BS", "K"))
+    bank, kv_bf16, state, t_prev, x, q, w_down, w_up = build_decode(cfg, dev)
+    st = [state.clone(), torch.empty_like(state)]
+
+    def run(n, j0=0):
+        for j in range(j0, j0 + n):
+            o, _, idx, _ = decode_step(st[j % 2], t_prev, x, w_down, w_up, K, q, bank, E, BS,
+                                       out_state=st[(j + 1) % 2])
+        return idx
+
+    idx = run(max(args.warmup, 1))
+    torch.cuda.synchronize()
+    # (1) K steps captured in one graph (an even count keeps the ping-pong aligned), replayed once
+    n = args.steps + (args.steps & 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        run(2)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            run(n)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    # HIP events on the stream the graph (and so every decode launch) runs on
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / n
+    # the step is one decode_step launch, so the events' average per launch is the kernel's duration
+    # (back to back, inter-launch gaps included)
+    dom_ms = e0.elapsed_time(e1) / n
+    # (2) per-launch durations of eager launches, each bracketed by HIP events (adds the events' cost)
+    with _lib.KernelTimer():
+        run(args.steps)
+        torch.cuda.synchronize()
+    kernels = _lib.KernelTimer.results()
+    per = {k: (v[0] / v[1], v[1]) for k, v in kernels.items() if v[1]}
+    alg = decode_alg_bytes(cfg, idx)
+    ach = alg / (dom_ms * 1e-3) / 1e9
+    roof = {"kernel": "decode_step", "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "avg_us": round(dom_ms * 1e3, 2),
+            "alg_bytes_per_launch": alg}
+    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            roof["traffic"] = json.load(f).get("config5:decode_step")
+    line = {
+        "metric": DECODE_METRIC,
+        "value": round(B / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 bank, bf16 q, fp32 router, fp64 state",
+        "data": "synthetic (random bank / weights, random prior lengths 1..4096)",
+        "config": {"workload": f"config5: MoM decode step B={B} d={D} heads={H}x{D // H} bank {E}x{BS} fp8 "
+                               f"top-{K} rank {cfg['R']}",
+                   "global_batch": B, "seq_len": 1, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
+        "kernels_timing": f"roofline avg_us: HIP events around the graph of {n} launches; kernels_us: events "
+                          f"around each of {args.steps} eager launches",
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = decode_cpu_baseline(cfg, kv_bf16, state, t_prev, x, q, w_down, w_up)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +359,8 @@ def main(argv=None):
     from naylis_amd import _lib
     dev = torch.device("cuda:0")
     cfg = WORKLOADS[args.workload]
+    if args.workload == "config5":
+        return decode_bench(args, cfg, dev)
     layer, M, x, dy = build(cfg, dev)
     B, T, D, H, E, BS = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS"))
     ntok = B * T
