@@ -43,6 +43,10 @@ struct GemmCfg {
   static constexpr int NT = 64 * WAVES_M * WAVES_N;   // threads
   static constexpr int BM = 32 * TM * WAVES_M;        // workgroup tile rows
   static constexpr int BN = 32 * TN * WAVES_N;        // workgroup tile columns
+  // K stages in flight in registers: the K loop of these tiles waits on
+  // global-load latency (one stage of MFMA is 0.1 - 0.4 us), so a stage is
+  // loaded DEPTH steps before it is copied to LDS
+  static constexpr int DEPTH = TM * TN >= 4 ? 3 : 4;
 };
 // 128 x 128, 4 waves of 64 x 64.  (256 x 256 tiles with 8 waves of 128 x 64
 // or 4 of 128 x 128 measured no faster on MI355X for these shapes: with one
@@ -73,7 +77,6 @@ struct Stage {
   static constexpr int CPR = KC ? kGK / 8 : ROWS / 8;   // chunks per LDS row
   static constexpr int N = ROWS * kGK / 8 / NT;         // chunks per thread
   using Shape = TileShape<KC, ROWS>;
-  uint4 v[N];
   int voff[N];   // byte offset of the chunk within a stage (k relative to the stage start)
   int lds[N];    // element offset in the LDS tile
   int kk[N];     // k of the chunk within the stage
@@ -90,26 +93,21 @@ struct Stage {
       kk[j] = k;
     }
   }
-  // soff: byte offset of the stage start; klim: valid k within the stage
-  // (wave-uniform; only a split's last stage can be partial)
-  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int soff, int klim) {
+  // soff: byte offset of the stage start.  Loads only issue (no use of the
+  // data here), so several stages can be in flight.
+  __device__ __forceinline__ void load(uint4 (&r)[N], __amdgpu_buffer_rsrc_t rs, int soff) const {
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      v[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j], soff, 0));
-    if (klim < kGK) {
-#pragma unroll
-      for (int j = 0; j < N; ++j) {
-        const uint32_t m = kk[j] < klim ? 0xffffffffu : 0u;
-        v[j].x &= m;
-        v[j].y &= m;
-        v[j].z &= m;
-        v[j].w &= m;
-      }
-    }
+      r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j], soff, 0));
   }
-  __device__ __forceinline__ void store(bf16_t* tile) const {
+  // klim: valid k within the stage (wave-uniform; only a split's last stage
+  // is partial); chunks past it are written as zeros
+  __device__ __forceinline__ void store(const uint4 (&r)[N], bf16_t* tile, int klim) const {
 #pragma unroll
-    for (int j = 0; j < N; ++j) *reinterpret_cast<uint4*>(&tile[lds[j]]) = v[j];
+    for (int j = 0; j < N; ++j) {
+      const uint32_t m = kk[j] < klim ? 0xffffffffu : 0u;
+      *reinterpret_cast<uint4*>(&tile[lds[j]]) = make_uint4(r[j].x & m, r[j].y & m, r[j].z & m, r[j].w & m);
+    }
   }
 };
 
@@ -166,46 +164,78 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(DevJobs jobs, int M, int N,
   SB sb;
   sa.init(job.a.ld, M, m0, tid);
   sb.init(job.b.ld, N, n0, tid);
-  auto load_stage = [&](int k0) {
-    const bool seg2 = k0 >= K1;
-    const int kseg = seg2 ? k0 - K1 : k0;
-    sa.load(seg2 ? ra2 : ra1, koff(kseg, job.a.ld, AKC), kend - k0);
-    sb.load(seg2 ? rb2 : rb1, koff(kseg, job.b.ld, BKC), kend - k0);
-  };
-
   f32x16 acc[C::TM][C::TN];
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = f32x16{};
 
-  if (nk > 0) {
-    load_stage(kbeg);
-    sa.store(a_lds[0]);
-    sb.store(b_lds[0]);
-  }
-  __syncthreads();
-  for (int s = 0; s < nk; ++s) {
-    const int cur = s & 1;
-    const bool more = s + 1 < nk;
-    if (more) load_stage(kbeg + (s + 1) * kGK);
+  // register slots of the stages in flight: slot p holds stages p, p + P, ...
+  constexpr int P = C::DEPTH;
+  uint4 ra[P][SA::N], rb[P][SB::N];
+  // stage indices are clamped to the last stage, so loads are issued
+  // unconditionally (a surplus load near the end is never stored) and the
+  // compiler can count the loads in flight without merging paths
+  auto load_stage = [&](uint4 (&xa)[SA::N], uint4 (&xb)[SB::N], int s) {
+    const int k0 = kbeg + min(s, nk - 1) * kGK;
+    const bool seg2 = k0 >= K1;
+    const int kseg = seg2 ? k0 - K1 : k0;
+    sa.load(xa, seg2 ? ra2 : ra1, koff(kseg, job.a.ld, AKC));
+    sb.load(xb, seg2 ? rb2 : rb1, koff(kseg, job.b.ld, BKC));
+  };
+  auto store_stage = [&](const uint4 (&xa)[SA::N], const uint4 (&xb)[SB::N], int buf, int s) {
+    const int klim = kend - (kbeg + s * kGK);
+    sa.store(xa, a_lds[buf], klim);
+    sb.store(xb, b_lds[buf], klim);
+  };
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < kGK / 16; ++ks) {
       bf16x8 af[C::TM], bfr[C::TN];
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i) af[i] = gemm_frag<AKC, C::BM>(a_lds[cur], wm + 32 * i, ks);
+      for (int i = 0; i < C::TM; ++i) af[i] = gemm_frag<AKC, C::BM>(a_lds[buf], wm + 32 * i, ks);
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j) bfr[j] = gemm_frag<BKC, C::BN>(b_lds[cur], wn + 32 * j, ks);
+      for (int j = 0; j < C::TN; ++j) bfr[j] = gemm_frag<BKC, C::BN>(b_lds[buf], wn + 32 * j, ks);
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
     }
-    if (more) {
-      sa.store(a_lds[cur ^ 1]);
-      sb.store(b_lds[cur ^ 1]);
+  };
+
+  if (nk > 0) {
+    // stages 0 .. P-1 in flight, stage 0 to LDS, then its slot takes stage P
+#pragma unroll
+    for (int p = 0; p < P; ++p) load_stage(ra[p], rb[p], p);
+    store_stage(ra[0], rb[0], 0, 0);
+    load_stage(ra[0], rb[0], P);
+  }
+  // LDS-only barriers: the stages in flight stay in flight across them
+  lds_barrier();
+  // iteration s: compute stage s from LDS buffer s & 1; store stage s + 1
+  // (slot (s + 1) % P) into the other buffer, which every wave finished
+  // reading before the previous barrier; the slot then takes stage s + 1 + P
+  int s0 = 0;
+  for (; s0 + P < nk; s0 += P) {  // whole groups of P with a next stage each: no branches
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int s = s0 + p;
+      const int q = (p + 1) % P;
+      compute(s & 1);
+      store_stage(ra[q], rb[q], (s + 1) & 1, s + 1);
+      load_stage(ra[q], rb[q], s + 1 + P);
+      lds_barrier();
     }
-    __syncthreads();
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {  // the last group
+    const int s = s0 + p;
+    if (s < nk) {
+      const int q = (p + 1) % P;
+      compute(s & 1);
+      if (s + 1 < nk) store_stage(ra[q], rb[q], (s + 1) & 1, s + 1);
+      lds_barrier();
+    }
   }
 
   // epilogue: acc[i][j][v] = C(m0 + wm + 32i + acc_row(l/32, v), n0 + wn + 32j + l%32)
