@@ -59,13 +59,16 @@ __device__ __forceinline__ void split2(const float (&v)[8], bf16x8& hi, bf16x8& 
 }
 
 // ---------------------------------------------------------------------------
-// (F1) y[b][t][r] = x[b][t] . W_down[r] for one (b, 32-token chunk) per
-// workgroup, and the chunk's fp64 column sums ycs[b][c][r].  Wave w of NW
-// takes the features [w D/NW, (w+1) D/NW) and issues all of its x and W_down
-// loads before the first MFMA (16-byte x row loads straight from HBM: A =
-// x, tokens x d; B = W_down^T, d x r, the lane's W_down row split into three
-// bf16 planes); the NW partial 32 x R tiles are added in wave order in LDS.
-template <int RT, int KSW>  // KSW: K-steps (16 features) per wave
+// (F1) y[b][t][r] = x[b][t] . W_down[r] for NC consecutive 32-token chunks
+// of one sequence per workgroup, and each chunk's fp64 column sums
+// ycs[b][c][r].  Wave w of NW takes the features [w D/NW, (w+1) D/NW): its
+// W_down rows are loaded and split into three bf16 planes once (B = W_down^T,
+// d x r; every product of a bf16 x and a plane is exact in fp32), then the
+// chunks stream through (A = x, tokens x d, 16-byte row loads straight from
+// HBM, the next chunk's loads issued before this chunk's reduction); the NW
+// partial 32 x R tiles of a chunk are added in wave order in LDS.  NC > 1
+// amortises the W_down reads (and the plane split) over NC chunks.
+template <int RT, int KSW, int NC>  // KSW: K-steps (16 features) per wave
 __global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restrict__ x,
                                                           const float* __restrict__ w_down, float* __restrict__ y,
                                                           double* __restrict__ ycs, int T, int D, int R, int n_ch) {
@@ -74,67 +77,82 @@ __global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restri
   constexpr int P = 33;  // partial tile pitch
   __shared__ float part[NW][RT][CT * P];
   __shared__ float ysum[CT][RT * 32 + 1];
-  const int c = blockIdx.x, b = blockIdx.y;
+  const int cg = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int t0 = c * CT, nt = min(CT, T - t0);
   const int nks = D / (16 * NW);  // K-steps of this wave (<= KSW)
   const int d0 = wave * nks * 16;
-  const bf16_t* xrow = x + ((long)b * T + t0 + min(l32, nt - 1)) * D + d0 + 8 * g;
 
+  auto load_x = [&](bf16x8 (&xf)[KSW], int c) {
+    const int t0 = c * CT, nt = min(CT, T - t0);
+    const bf16_t* xrow = x + ((long)b * T + t0 + min(l32, nt - 1)) * D + d0 + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks) xf[ks] = *reinterpret_cast<const bf16x8*>(xrow + 16 * min(ks, nks - 1));
+  };
+  const int c_first = cg * NC;
   bf16x8 xf[KSW];
-  f32x4 wf[KSW][RT][2];
+  load_x(xf, c_first);
+  bf16x8 p1[KSW][RT], p2[KSW][RT], p3[KSW][RT];
+  {
+    f32x4 wf[KSW][RT][2];
 #pragma unroll
-  for (int ks = 0; ks < KSW; ++ks) {
-    const int kc = min(ks, nks - 1);
-    xf[ks] = *reinterpret_cast<const bf16x8*>(xrow + 16 * kc);
-  }
+    for (int rt = 0; rt < RT; ++rt) {
+      const float* wrow = w_down + (long)min(rt * 32 + l32, R - 1) * D + d0 + 8 * g;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float* wrow = w_down + (long)min(rt * 32 + l32, R - 1) * D + d0 + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < KSW; ++ks) {
-      const int kc = min(ks, nks - 1);
-      wf[ks][rt][0] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc);
-      wf[ks][rt][1] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc + 4);
-    }
-  }
-  f32x16 acc[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x16{};
-#pragma unroll
-  for (int ks = 0; ks < KSW; ++ks) {
-    if (ks < nks) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        bf16x8 p1, p2, p3;
-        split3(wf[ks][rt][0], wf[ks][rt][1], p1, p2, p3);
-        acc[rt] = mfma32(xf[ks], p3, acc[rt]);  // smallest terms first
-        acc[rt] = mfma32(xf[ks], p2, acc[rt]);
-        acc[rt] = mfma32(xf[ks], p1, acc[rt]);
+      for (int ks = 0; ks < KSW; ++ks) {
+        const int kc = min(ks, nks - 1);
+        wf[ks][rt][0] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc);
+        wf[ks][rt][1] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc + 4);
       }
     }
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) split3(wf[ks][rt][0], wf[ks][rt][1], p1[ks][rt], p2[ks][rt], p3[ks][rt]);
   }
-  // partial tiles: D[row = token][col = rank]
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) part[wave][rt][acc_row(g, v) * P + l32] = acc[rt][v];
-  __syncthreads();
   const int RW = RT * 32;
-  for (int i = tid; i < CT * RW; i += NW * 64) {
-    const int t = i / RW, r = i % RW, rt = r >> 5, rl = r & 31;
-    float s = part[0][rt][t * P + rl];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) s += part[w][rt][t * P + rl];
-    ysum[t][r] = s;
-    if (t < nt && r < R) y[((long)b * T + t0 + t) * R + r] = s;
-  }
-  __syncthreads();
-  if (tid < R) {
-    double cs = 0.0;
-    for (int t = 0; t < nt; ++t) cs += (double)ysum[t][tid];
-    ycs[((long)b * n_ch + c) * R + tid] = cs;
+  for (int j = 0; j < NC; ++j) {
+    const int c = c_first + j;
+    if (c >= n_ch) break;  // workgroup-uniform
+    const int t0 = c * CT, nt = min(CT, T - t0);
+    f32x16 acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks) {
+      if (ks < nks) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          acc[rt] = mfma32(xf[ks], p3[ks][rt], acc[rt]);  // smallest terms first
+          acc[rt] = mfma32(xf[ks], p2[ks][rt], acc[rt]);
+          acc[rt] = mfma32(xf[ks], p1[ks][rt], acc[rt]);
+        }
+      }
+    }
+    if (j + 1 < NC && c + 1 < n_ch) load_x(xf, c + 1);  // in flight during the reduction below
+    // partial tiles: D[row = token][col = rank]
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) part[wave][rt][acc_row(g, v) * P + l32] = acc[rt][v];
+    lds_barrier();
+    for (int i = tid; i < CT * RW; i += NW * 64) {
+      const int t = i / RW, r = i % RW, rt = r >> 5, rl = r & 31;
+      float sum = part[0][rt][t * P + rl];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) sum += part[w][rt][t * P + rl];
+      ysum[t][r] = sum;
+      if (t < nt && r < R) y[((long)b * T + t0 + t) * R + r] = sum;
+    }
+    lds_barrier();
+    if (tid < R) {
+      double cs = 0.0;
+      for (int t = 0; t < nt; ++t) cs += (double)ysum[t][tid];
+      ycs[((long)b * n_ch + c) * R + tid] = cs;
+    }
+    // ysum / part are rewritten by the next chunk only after this barrier
+    if (j + 1 < NC) lds_barrier();
   }
 }
 
@@ -583,9 +601,18 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
   const int nks = d.D / 128;
   auto go = [&](auto ksw) {
     constexpr int KSW = decltype(ksw)::value;
-    NAYLIS_TIMED("router_proj", st,
-                 hipLaunchKernelGGL((router_proj_kernel<RT, KSW>), dim3(n_ch, d.B), dim3(512), 0, st,
-                                    (const bf16_t*)x, w_down, y, ycs, d.T, d.D, d.R, n_ch));
+    // chunks per workgroup: two when the W_down planes leave room in registers
+    // and the grid still has a workgroup per CU
+    constexpr int NCW = KSW * RT <= 8 ? 2 : 1;
+    const int nc = (NCW > 1 && (long)((n_ch + 1) / 2) * d.B >= 256) ? 2 : 1;
+    if (nc == 2)
+      NAYLIS_TIMED("router_proj", st,
+                   hipLaunchKernelGGL((router_proj_kernel<RT, KSW, NCW>), dim3((n_ch + NCW - 1) / NCW, d.B),
+                                      dim3(512), 0, st, (const bf16_t*)x, w_down, y, ycs, d.T, d.D, d.R, n_ch));
+    else
+      NAYLIS_TIMED("router_proj", st,
+                   hipLaunchKernelGGL((router_proj_kernel<RT, KSW, 1>), dim3(n_ch, d.B), dim3(512), 0, st,
+                                      (const bf16_t*)x, w_down, y, ycs, d.T, d.D, d.R, n_ch));
   };
   if (nks <= 2)
     go(std::integral_constant<int, 2>{});
