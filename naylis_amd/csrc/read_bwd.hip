@@ -358,13 +358,14 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   constexpr int VEC = TT * HD / 8;        // 16-byte vectors per staged tensor tile
   constexpr int PER = (VEC + 511) / 512;
 
-  __shared__ __attribute__((aligned(16))) bf16_t q_lds[TT * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t do_lds[TT * PITCH];
-  __shared__ __attribute__((aligned(16))) float add_lds[4][TT];  // per quarter: c2 - lse, or -inf
-  __shared__ __attribute__((aligned(16))) float dl_lds[TT];
-  __shared__ int32_t idx_lds[TT * TK];
-  __shared__ float lg_lds[TT * TK];
-  __shared__ float lse_lds[TT];
+  // two buffers: tile it + 1 is stored while tile it is read, one barrier per tile
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds2[2][TT * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t do_lds2[2][TT * PITCH];
+  __shared__ __attribute__((aligned(16))) float add_lds2[2][4][TT];  // per quarter: c2 - lse, or -inf
+  __shared__ __attribute__((aligned(16))) float dl_lds2[2][TT];
+  __shared__ int32_t idx_lds2[2][TT * TK];
+  __shared__ float lg_lds2[2][TT * TK];
+  __shared__ float lse_lds2[2][TT];
   __shared__ __attribute__((aligned(16))) float red[4 * NO * 16 * 64];  // half-1 partials for the final sum
 
   const int n_sg = Lq / 128;
@@ -410,9 +411,9 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     acc_dv[j] = f32x16{};
   }
   if constexpr (HD < 32) {
-    for (int i = tid; i < TT * PITCH; i += 512) {
-      q_lds[i] = 0;
-      do_lds[i] = 0;
+    for (int i = tid; i < 2 * TT * PITCH; i += 512) {
+      q_lds2[i / (TT * PITCH)][i % (TT * PITCH)] = 0;
+      do_lds2[i / (TT * PITCH)][i % (TT * PITCH)] = 0;
     }
   }
 
@@ -480,7 +481,14 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
       pdl = ok ? delta[(long)h * ntok + tk] : 0.f;
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    bf16_t* q_lds = q_lds2[buf];
+    bf16_t* do_lds = do_lds2[buf];
+    float(*add_lds)[TT] = add_lds2[buf];
+    float* dl_lds = dl_lds2[buf];
+    int32_t* idx_lds = idx_lds2[buf];
+    float* lg_lds = lg_lds2[buf];
+    float* lse_lds = lse_lds2[buf];
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const int vi = tid + 512 * r;
@@ -523,12 +531,23 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     load_tile();
   }
   if (i_begin + 1 < i_end) fetch_tokens(tiles[i_begin + 1]);
+  if (i_begin < i_end) store_tile(0);
+  if (i_begin + 1 < i_end) load_tile();                  // tile i_begin + 1 in flight
+  if (i_begin + 2 < i_end) fetch_tokens(tiles[i_begin + 2]);
+  lds_barrier();
   for (int it = i_begin; it < i_end; ++it) {
-    lds_barrier();  // the previous tile's LDS reads are done
-    store_tile();
-    lds_barrier();
-    if (it + 1 < i_end) load_tile();                       // in flight during the math below
-    if (it + 2 < i_end) fetch_tokens(tiles[it + 2]);       // the tokens of the tile after
+    const int buf = (it - i_begin) & 1;
+    // tile it + 1 into the other buffer (last read before the previous barrier)
+    if (it + 1 < i_end) store_tile(buf ^ 1);
+    if (it + 2 < i_end) load_tile();                       // in flight during the math below
+    if (it + 3 < i_end) fetch_tokens(tiles[it + 3]);       // the tokens of the tile after
+    const bf16_t* q_lds = q_lds2[buf];
+    const bf16_t* do_lds = do_lds2[buf];
+    const float(*add_lds)[TT] = add_lds2[buf];
+    const float* dl_lds = dl_lds2[buf];
+    const int32_t* idx_lds = idx_lds2[buf];
+    const float* lg_lds = lg_lds2[buf];
+    const float* lse_lds = lse_lds2[buf];
 
     // ---- S = Q K^T and dP = dO V^T for this wave's 32 tokens x 32 slots
     f32x16 acc_s = f32x16{}, acc_p = f32x16{};
@@ -592,6 +611,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
         acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
       }
     }
+    lds_barrier();  // every wave is done with buffer buf before it is refilled
   }
 
   // ---- sum the two token halves (fixed order), write this share's partials

@@ -123,22 +123,27 @@ def test_read_empty_sequence(dev):
 def test_read_single_block_gate_independence(dev):
     """A token whose k selections all name one block attends to that block
     alone, whatever the gate values (the bias is constant over the block).
-    The gate enters the exp2 argument through two fp32 roundings, so the two
-    outputs agree to one bf16 ulp rather than bitwise."""
+    The gate enters the exp2 argument through two fp32 roundings, and P enters
+    the P.V product in bf16, so a gate change can move one p across a bf16
+    rounding boundary (2^-8 of p): the outputs agree to one bf16 ulp plus
+    2^-8 of the largest |o| of the (token, head) row, not bitwise (an output
+    that cancels, |o| << sum_n p_n |v_n|, shows that 2^-8 as several ulps)."""
     from naylis_amd import mom_kernels
     B, S, H, HD, NB, BS = 1, 128, 2, 64, 4, 64
     q, k, v, _, gates, _ = make_inputs(B, S, H, HD, NB, BS, 2, "random")
     top = torch.full((B, S, 2), 2, dtype=torch.long)
-    g2 = F.softmax(torch.randn(B, S, 2) * 3, -1)
+    g2 = F.softmax(torch.randn(B, S, 2, generator=torch.Generator().manual_seed(142)) * 3, -1)
     o1 = mom_kernels.mom_read(q.to(dev), k.to(dev), v.to(dev), top.to(dev), gates.to(dev),
                               num_blocks=NB, block_size=BS, mode="hip")
     o2 = mom_kernels.mom_read(q.to(dev), k.to(dev), v.to(dev), top.to(dev), g2.to(dev),
                               num_blocks=NB, block_size=BS, mode="hip")
     # one bf16 ulp of the larger of the two values (an ulp is at most 2^-7 of
     # the value; measuring against the smaller one fails spuriously when the
-    # two round to neighbours on either side of a power of two)
+    # two round to neighbours on either side of a power of two), plus the
+    # bf16 rounding of one P entry at the row's scale
     a, b = o1.float(), o2.float()
-    assert bool(((a - b).abs() <= 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-6).all())
+    row = torch.maximum(a.abs(), b.abs()).amax(-1, keepdim=True)
+    assert bool(((a - b).abs() <= 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 2.0 ** -8 * row + 1e-6).all())
 
 
 def test_read_full_config2_vs_torch_fp32(dev):
