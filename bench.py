@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """MoM layer forward+backward throughput on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config4|config5]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config3|config4|config5]
 
 Workload ("config2"): one Naylis MoM layer in bf16,
 forward + backward at the training shape B=8, T=2048, d=1024, 16 heads x 64,
@@ -24,6 +24,13 @@ e4m3 with per-slot scales, top-2.  A step is one naylis_mom_decode_step for
 the 64 sequences (state ping-pong between two buffers); the K timed steps are
 one captured HIP graph of K steps, replayed once, so host launch cost stays
 out of the figure.  value = decoded tokens/s (B per step).
+
+config3 is the full decoder: 20 Llama layers (d=1024,
+16 heads, SwiGLU 2816, RoPE, vocab 32768, tied head), each with a MoM read of
+the one shared 8 x 128 bank, bf16 with fp32 routing, random init, B=8, T=2048,
+token ids uniform; a step is next-token CE + 0.01 aux loss, forward and
+backward.  value = tokens/s; "model" gives the step's model FLOP rate and
+"read" the MoM reads' MFMA fraction summed over the layers.
 """
 from __future__ import annotations
 
@@ -46,8 +53,10 @@ WORKLOADS = {
     "config2": dict(B=8, T=2048, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, tile_bias=None),
     "config4": dict(B=4, T=4096, D=1536, H=24, E=32, BS=128, K=2, R=32, bank_fro=None, tile_bias=(3, 6)),
     "config5": dict(B=64, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, max_prior=4096),
+    "config3": dict(B=8, T=2048, D=1024, H=16, E=8, BS=128, K=2, R=32, layers=20, ffn=2816, vocab=32768),
 }
 DECODE_METRIC = "MoM decode step tokens/s at B=64, d=1024, fp8 8x128 bank"
+DECODER_METRIC = "Naylis decoder (20 layers, d=1024, shared 8x128 bank) fwd+bwd tokens/s"
 
 
 def build(cfg, device):
@@ -337,6 +346,148 @@ def decode_bench(args, cfg, dev):
     return 0
 
 
+def decoder_flops(cfg, params_dense):
+    """Model FLOP of one fwd+bwd step for the per-token weights and the trunk's
+    attention: 6 per weight per token (trunk, MoM q/o projections and router,
+    LM head) plus causal attention (QK^T and PV over half the square, x3 for
+    fwd+bwd)."""
+    B, T, D, L = cfg["B"], cfg["T"], cfg["D"], cfg["layers"]
+    return 6.0 * B * T * params_dense + 3.0 * L * 2 * 2 * B * T * T * D / 2
+
+
+def decoder_cpu_baseline(cfg, state):
+    """The fp32 CPU oracle decoder (all layers, full width, eager MoM read) fwd+bwd
+    on one sequence of 256 tokens, 1 warmup + median of 2."""
+    import torch
+
+    import oracle
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    ref = oracle.OracleDecoder(cfg["vocab"], cfg["D"], cfg["layers"], cfg["H"], cfg["ffn"], cfg["E"] * cfg["BS"],
+                               cfg["BS"], cfg["K"], cfg["R"])
+    ref.load_state_dict(state, strict=True)
+    ref.train()
+    T = 256
+    ids = torch.randint(0, cfg["vocab"], (1, T), generator=torch.Generator().manual_seed(4))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        loss, _, _ = ref(ids, labels=ids)
+        loss.backward()
+        times.append(time.perf_counter() - t0)
+        ref.zero_grad(set_to_none=True)
+    med = statistics.median(times[1:])
+    return {"value": round(T / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle.OracleDecoder fp32 fwd+bwd (CE + aux), 1 sequence x T={T} of the config-3 model "
+                      f"(1 warmup, median of 2 runs: {med:.3f} s), torch {torch.__version__}"}
+
+
+def decoder_bench(args, cfg, dev):
+    """Config 3: the full decoder, bf16 (router weights and ReZero scales fp32),
+    random init, token ids uniform over the vocabulary, next-token CE + 0.01 aux.
+    A step is loss = model(ids, labels=ids).loss; loss.backward(); grads dropped."""
+    import torch
+
+    from naylis_amd import _lib
+    from naylis_amd.decoder import NaylisLlamaForCausalLM, cast_for_training, naylis_config
+    from naylis_amd.layer import MoMLayer
+    B, T, D, H, E, BS = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS"))
+    torch.manual_seed(0)
+    mcfg = naylis_config(vocab_size=cfg["vocab"], d_model=D, n_layers=cfg["layers"], n_heads=H,
+                         intermediate_size=cfg["ffn"], seq_len=T, mem_size=E * BS, mom_block_size=BS,
+                         mom_top_blocks=cfg["K"], mom_router_rank=cfg["R"])
+    model = NaylisLlamaForCausalLM(mcfg)
+    state_fp32 = None if args.no_cpu_baseline else {k: v.detach().clone() for k, v in model.state_dict().items()}
+    model = cast_for_training(model).to(dev).train()
+    model.set_noise_scale(0.0)
+    ids = torch.randint(0, cfg["vocab"], (B, T), generator=torch.Generator().manual_seed(1)).to(dev)
+
+    def step():
+        out = model(input_ids=ids, labels=ids)
+        out.loss.backward()
+        model.zero_grad(set_to_none=True)
+        return out.loss
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    with _lib.KernelTimer():
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    kernels = _lib.KernelTimer.results()
+    per = {k: (v[0] / v[1], v[1] / args.steps) for k, v in kernels.items() if v[1]}
+
+    # routing of every MoM layer for one forward: capture each layer's input
+    inputs = {}
+    hooks = [m.register_forward_hook(lambda mod, a, out, key=i: inputs.__setitem__(key, a[0].detach()))
+             for i, m in enumerate(x for x in model.modules() if isinstance(x, MoMLayer))]
+    with torch.no_grad():
+        model(input_ids=ids, labels=ids)
+    for h in hooks:
+        h.remove()
+    A_total = 0
+    for i, m in enumerate(x for x in model.modules() if isinstance(x, MoMLayer)):
+        A_total += active_tiles(routing(m, model.model.M_blocks, inputs[i]), E)
+    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce_kv", "read_bwd_reduce_gates")
+    read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
+    read_flop = 14.0 * D * BS * 128 * A_total
+    read_tf = read_flop / (read_ms * 1e-3) / 1e12
+    unit_per_layer = 2.0 * D * BS * 128 * A_total / cfg["layers"]
+    alg = {"read_fwd": 2 * unit_per_layer, "read_bwd_dq": 3 * unit_per_layer, "read_bwd_dkdv": 4 * unit_per_layer}
+    dominant = max((k for k in kernels if k in alg), key=lambda k: kernels[k][0])
+    dom_ms = per[dominant][0]
+    ach = alg[dominant] / (dom_ms * 1e-3) / 1e12
+    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "avg_us": round(dom_ms * 1e3, 2), "alg_flop_per_launch": alg[dominant],
+            "note": "the path's dominant library kernel (the MoM read); trunk GEMMs and attention are torch's"}
+    # per-token weights: every matrix but the bank and its K/V projections (the tied
+    # embedding counts once, as the LM head); the bank projections run over the L slots
+    params_dense = sum(p.numel() for n, p in model.named_parameters()
+                       if p.dim() == 2 and n != "model.M_blocks" and ".mom.k_proj" not in n
+                       and ".mom.v_proj" not in n)
+    bank_flop = cfg["layers"] * 2 * 6.0 * E * BS * D * D
+    model_flop = decoder_flops(cfg, params_dense) + bank_flop + read_flop
+    model_tf = model_flop / (ms_per_step * 1e-3) / 1e12
+    line = {
+        "metric": DECODER_METRIC,
+        "value": round(B * T / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, token ids uniform over the vocabulary)",
+        "config": {"workload": f"config3: Naylis decoder fwd+bwd, {cfg['layers']} layers d={D} heads={H}x{D // H} "
+                               f"SwiGLU {cfg['ffn']} vocab {cfg['vocab']}, shared bank {E}x{BS} top-{cfg['K']} "
+                               f"rank {cfg['R']}, CE + 0.01 aux",
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "model": {"flop_per_step": model_flop, "tflops": round(model_tf, 1),
+                  "mfma_frac": round(model_tf / PEAK_BF16_TFLOPS, 4), "loss": round(float(loss), 4)},
+        "read": {"active_tile_blocks_all_layers": A_total, "alg_flop": read_flop, "ms": round(read_ms, 4),
+                 "tflops": round(read_tf, 2), "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
+        "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
+        "kernels_per_step": {k: round(v[1], 2) for k, v in sorted(per.items())},
+    }
+    if state_fp32 is not None:
+        del model
+        torch.cuda.empty_cache()
+        line["cpu_baseline"] = decoder_cpu_baseline(cfg, state_fp32)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -361,6 +512,8 @@ def main(argv=None):
     cfg = WORKLOADS[args.workload]
     if args.workload == "config5":
         return decode_bench(args, cfg, dev)
+    if args.workload == "config3":
+        return decoder_bench(args, cfg, dev)
     layer, M, x, dy = build(cfg, dev)
     B, T, D, H, E, BS = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS"))
     ntok = B * T

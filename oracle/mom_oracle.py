@@ -72,7 +72,7 @@ def prefix_mean(x):
     return cs / denom.view(1, -1, 1)
 
 
-def router(x, w_down, w_up, top_k, noise=None, noise_scale=1.0):
+def router(x, w_down, w_up, top_k, noise=None, noise_scale=1.0, force_idx=None):
     """Prefix-mean router: (logits, probs, top_idx, top_gates, h).
 
     Follows model.py:178-187 (h cast to the router weight dtype, two bias-free
@@ -81,12 +81,20 @@ def router(x, w_down, w_up, top_k, noise=None, noise_scale=1.0):
     descending, softmax of the selected values). ``noise`` is the
     already-drawn perturbation (the Gumbel sample of model.py:210 or any
     additive logit bias); ``noise_scale`` multiplies it as model.py:211 does.
+    ``force_idx`` (B, S, k) replaces the top-k selection (gates are still the
+    softmax of the selected noisy logits): whole-model comparisons use it to
+    give both sides the same routing when bf16 differences in a layer's input
+    move tokens across a selection boundary.
     """
     h = prefix_mean(x).to(w_down.dtype)
     logits = F.linear(torch.tanh(F.linear(h, w_down)), w_up).float()
     noisy = logits if noise is None else logits + noise_scale * noise
     probs = F.softmax(logits, dim=-1)
-    top_values, top_idx = noisy.topk(top_k, dim=-1)
+    if force_idx is None:
+        top_values, top_idx = noisy.topk(top_k, dim=-1)
+    else:
+        top_idx = force_idx.long()
+        top_values = noisy.gather(-1, top_idx)
     top_gates = F.softmax(top_values, dim=-1)
     return logits, probs, top_idx, top_gates, h
 
@@ -203,19 +211,20 @@ class OracleMoMLayer(nn.Module):
         return out
 
 
-def layer_forward(x, layer, M_blocks, noise=None):
+def layer_forward(x, layer, M_blocks, noise=None, force_idx=None):
     """Full causal layer forward: mom_kernels/reference.py:64-95.
 
     Returns (output, router_probs, top_idx, top_gates) with the router stats
     flattened to (B*S, ...) rows as the reference returns them. ``noise`` is
     the additive logit perturbation drawn by the caller (Gumbel in training,
-    reference.py:77-79), applied with ``layer.noise_scale``.
+    reference.py:77-79), applied with ``layer.noise_scale``; ``force_idx`` as
+    in ``router``.
     """
     B, S, D = x.shape
     q_sh = layer.q_proj(x).view(B, S, layer.n_heads, layer.head_dim)
     _, probs, top_idx, top_gates, _ = router(
         x, layer.router_down.weight, layer.router_up.weight, layer.top_blocks,
-        noise=noise, noise_scale=layer.noise_scale)
+        noise=noise, noise_scale=layer.noise_scale, force_idx=force_idx)
     k, v = bank_kv(M_blocks, layer.k_proj.weight, layer.v_proj.weight)
     bias = build_gate_bias(top_idx, top_gates, layer.num_blocks, layer.block_size, q_sh.dtype)
     out = mom_attention(q_sh, k, v, bias)

@@ -309,3 +309,19 @@ def test_decode_step_equals_full_sequence_rows():
         assert torch.equal(idx, idx_full[:, t])
         torch.testing.assert_close(gates, gates_full[:, t], rtol=0, atol=0)
         torch.testing.assert_close(out, out_full[:, t].float(), rtol=1e-5, atol=1e-6)
+
+
+def test_router_forced_selection_equals_free_selection():
+    """router(force_idx=its own top-k) reproduces every output bitwise, and a
+    forced different selection changes only top_idx / gates."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 40, 32, generator=g)
+    wd = torch.randn(8, 32, generator=g) * 0.2
+    wu = torch.randn(6, 8, generator=g) * 0.5
+    free = oracle.router(x, wd, wu, 2)
+    forced = oracle.router(x, wd, wu, 2, force_idx=free[2])
+    for a, b in zip(free, forced):
+        assert torch.equal(a, b)
+    other = torch.stack([free[2][..., 1], free[2][..., 0]], -1)     # same pair, swapped
+    sw = oracle.router(x, wd, wu, 2, force_idx=other)
+    assert torch.equal(sw[3], free[3].flip(-1)) and torch.equal(sw[1], free[1])
