@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 4
+#define NAYLIS_MOM_ABI_VERSION 5
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -33,6 +33,11 @@ extern "C" {
 
 #define NAYLIS_DTYPE_F32 0
 #define NAYLIS_DTYPE_BF16 1
+
+/* noise_kind of naylis_mom_router_fwd */
+#define NAYLIS_NOISE_ADDITIVE 0        /* noise holds the perturbation itself */
+#define NAYLIS_NOISE_GUMBEL_UNIFORM 1  /* noise holds the uniform draw u; the kernel applies
+                                          g = -log(-log(u + 1e-9) + 1e-9) (model.py:210) */
 
 #define NAYLIS_MAX_TOPK 8
 #define NAYLIS_MAX_BLOCKS 1024
@@ -113,8 +118,12 @@ int naylis_mom_read_order(const int32_t* top_idx, int32_t* order, void* workspac
  *   x          (B, T, D) fp32 or bf16 (x_dtype: NAYLIS_DTYPE_*)
  *   w_down     (R, D) fp32          router_down.weight
  *   w_up       (E, R) fp32          router_up.weight
- *   noise      (B, T, E) fp32 or NULL; topk ranks logits + noise_scale*noise
- *              (the Gumbel draw of model.py:210 or any additive logit bias)
+ *   noise      (B, T, E) fp32 or NULL; topk ranks logits + noise_scale*g with
+ *              g = noise (noise_kind NAYLIS_NOISE_ADDITIVE: any logit bias) or
+ *              g = -log(-log(noise + 1e-9) + 1e-9) (NAYLIS_NOISE_GUMBEL_UNIFORM:
+ *              noise is the torch.rand draw of model.py:210, transformed in the
+ *              kernel with the reference's fp32 steps); product and sum are
+ *              rounded separately, as the reference's two ops
  *   logits     (B, T, E) fp32       clean router logits
  *   probs      (B, T, E) fp32       softmax(logits)
  *   top_idx    (B, T, k) int32      descending by perturbed logit; ties ->
@@ -128,12 +137,15 @@ int naylis_mom_read_order(const int32_t* top_idx, int32_t* order, void* workspac
 size_t naylis_mom_router_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k);
 
 int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* noise,
-                          float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
-                          float* act, float* h_out, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
-                          int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream);
+                          int noise_kind, float noise_scale, float* logits, float* probs, int32_t* top_idx,
+                          float* top_gates, float* act, float* h_out, void* workspace, size_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream);
 
-/* Backward of the router: any of d_gates (B,T,k), d_probs (B,T,E), d_logits
- * (B,T,E) may be NULL (no gradient from that output).  Writes dx (same dtype
+/* Backward of the router: any of d_gates (B,T,k), d_probs, d_logits
+ * (B,T,E) may be NULL (no gradient from that output).  d_probs_stride is the
+ * distance between tokens' rows of d_probs: E for a (B,T,E) tensor, or 0 for
+ * one row of E values shared by every token (the gradient the load-balance
+ * aux term sends through mean_prob, without an (N, E) tensor).  Writes dx (same dtype
  * and shape as x), dw_down (R, D) and dw_up (E, R), both fp32, reduced over
  * all tokens in a fixed order.  dx_accumulate != 0 adds the router's input
  * gradient to the dx the caller passes (the sum of x's gradients from the
@@ -149,9 +161,24 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
  * itself and h_out is bit-exact. */
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                          const float* d_probs, const float* d_logits, void* dx, int dx_accumulate, float* dw_down,
-                          float* dw_up, void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D,
-                          int64_t R, int64_t E, int64_t top_k, void* stream);
+                          const float* d_probs, int64_t d_probs_stride, const float* d_logits, void* dx,
+                          int dx_accumulate, float* dw_down, float* dw_up, void* workspace, size_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream);
+
+/* Load-balance statistics of one layer's routing, replacing the per-layer
+ * torch ops of model.py:476-517 (_collect_mom_aux_loss) with one pass over
+ * probs (N, E) fp32 and top_idx (N, k) int32:
+ *   stats[0, E)   mean_prob_e = mean over tokens of probs[:, e]
+ *   stats[E, 2E)  frac_e      = fraction of tokens whose top-k contains e
+ *   stats[2E]     aux         = E * sum_e frac_e * mean_prob_e
+ *   stats[2E+1]   entropy     = mean over tokens of -sum_e p log(max(p, 1e-9))
+ *   stats[2E+2]   dead        = fraction of blocks no token selects
+ * (2E+3 floats).  Sums run in fp64 in a fixed order (deterministic).  The aux
+ * gradient with respect to probs is one row, d_aux * E * frac_e / N, for
+ * naylis_mom_router_bwd with d_probs_stride = 0. */
+size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E);
+int naylis_mom_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* workspace,
+                            size_t workspace_bytes, int64_t N, int64_t E, int64_t top_k, void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

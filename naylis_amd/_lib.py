@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -37,10 +37,12 @@ SIGNATURES = {
     "naylis_mom_read_order_workspace_bytes": (_size_t, [_i64] * 4),
     "naylis_mom_read_order": (_int, [_c_void_p, _c_void_p, _c_void_p, _size_t] + [_i64] * 4 + [_c_void_p]),
     "naylis_mom_router_workspace_bytes": (_size_t, [_i64] * 6),
-    "naylis_mom_router_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _float] + [_c_void_p] * 6
-                              + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
-    "naylis_mom_router_bwd": (_int, [_c_void_p, _int] + [_c_void_p] * 10 + [_int] + [_c_void_p] * 2
-                              + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
+    "naylis_mom_router_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _float]
+                              + [_c_void_p] * 6 + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
+    "naylis_mom_router_bwd": (_int, [_c_void_p, _int] + [_c_void_p] * 8 + [_i64] + [_c_void_p] * 2 + [_int]
+                              + [_c_void_p] * 2 + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
+    "naylis_mom_router_stats_workspace_bytes": (_size_t, [_i64] * 2),
+    "naylis_mom_router_stats": (_int, [_c_void_p] * 4 + [_size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_fwd": (_int, [_c_void_p] * 5 + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_linear_wgrad_workspace_bytes": (_size_t, [_i64] * 3),
     "naylis_mom_rezero_workspace_bytes": (_size_t, [_i64]),

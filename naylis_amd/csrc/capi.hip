@@ -246,13 +246,17 @@ size_t naylis_mom_router_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_
 }
 
 int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* noise,
-                          float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
-                          float* act, float* h_out, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
-                          int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream) {
+                          int noise_kind, float noise_scale, float* logits, float* probs, int32_t* top_idx,
+                          float* top_gates, float* act, float* h_out, void* workspace, size_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream) {
   RouterDims d;
   int rc = check_router_dims(B, T, D, R, E, top_k, &d);
   if (rc) return rc;
   if ((rc = check_dtype(x_dtype, "mom_route"))) return rc;
+  if (noise_kind != NAYLIS_NOISE_ADDITIVE && noise_kind != NAYLIS_NOISE_GUMBEL_UNIFORM)
+    return fail(NAYLIS_ERR_ARG, "mom_route_fwd: noise_kind %d must be %d (additive) or %d (uniform draw, Gumbel)",
+                noise_kind, NAYLIS_NOISE_ADDITIVE, NAYLIS_NOISE_GUMBEL_UNIFORM);
+  d.noise_kind = noise_kind;
   if (B * T == 0) return NAYLIS_OK;
   if (!x || !w_down || !w_up || !logits || !probs || !top_idx || !top_gates || !act || !workspace)
     return fail(NAYLIS_ERR_ARG, "mom_route_fwd: null pointer argument");
@@ -267,13 +271,17 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
 
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
-                          const float* d_probs, const float* d_logits, void* dx, int dx_accumulate, float* dw_down,
-                          float* dw_up, void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t D,
-                          int64_t R, int64_t E, int64_t top_k, void* stream) {
+                          const float* d_probs, int64_t d_probs_stride, const float* d_logits, void* dx,
+                          int dx_accumulate, float* dw_down, float* dw_up, void* workspace, size_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream) {
   RouterDims d;
   int rc = check_router_dims(B, T, D, R, E, top_k, &d);
   if (rc) return rc;
   if ((rc = check_dtype(x_dtype, "mom_route"))) return rc;
+  if (d_probs && d_probs_stride != 0 && d_probs_stride != E)
+    return fail(NAYLIS_ERR_ARG, "mom_route_bwd: d_probs_stride %lld must be num_blocks (%lld) or 0",
+                (long long)d_probs_stride, (long long)E);
+  d.dp_stride = (long)d_probs_stride;
   if (dx_accumulate && B * T > 0 && !router_fast_bwd_ok(x, x_dtype == NAYLIS_DTYPE_BF16, dx, d))
     return fail(NAYLIS_ERR_ARG,
                 "mom_route_bwd: dx_accumulate needs bf16 x, D a multiple of 128, R <= 64 and 16-byte aligned x / dx");
@@ -289,6 +297,32 @@ int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const
                                       d_gates, d_probs, d_logits, dx, dx_accumulate != 0, dw_down, dw_up, workspace, d,
                                       (hipStream_t)stream),
                     "mom_route_bwd");
+}
+
+size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E) {
+  if (N < 0 || N > ((int64_t)1 << 30) || E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS) return 0;
+  return router_stats_ws_bytes((long)N, (int)E);
+}
+
+int naylis_mom_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* workspace,
+                            size_t workspace_bytes, int64_t N, int64_t E, int64_t top_k, void* stream) {
+  if (N < 0 || N > ((int64_t)1 << 30))
+    return fail(NAYLIS_ERR_ARG, "mom_router_stats: bad token count N=%lld", (long long)N);
+  if (E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS)
+    return fail(NAYLIS_ERR_ARG, "mom_router_stats: num_blocks %lld must be in [1, %d]", (long long)E,
+                NAYLIS_ROUTER_MAX_BLOCKS);
+  if (top_k < 1 || top_k > NAYLIS_MAX_TOPK || top_k > E)
+    return fail(NAYLIS_ERR_ARG, "mom_router_stats: top_k %lld must be in [1, min(%d, num_blocks=%lld)]",
+                (long long)top_k, NAYLIS_MAX_TOPK, (long long)E);
+  if (!stats || !workspace || (N > 0 && (!probs || !top_idx)))
+    return fail(NAYLIS_ERR_ARG, "mom_router_stats: null pointer argument");
+  const size_t need = router_stats_ws_bytes((long)N, (int)E);
+  if (workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_router_stats: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  return hip_status(launch_router_stats(probs, top_idx, stats, workspace, (long)N, (int)E, (int)top_k,
+                                        (hipStream_t)stream),
+                    "mom_router_stats");
 }
 
 int naylis_mom_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, void* k_out, void* v_out, int64_t L,

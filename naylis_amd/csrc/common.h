@@ -24,6 +24,16 @@
 
 namespace naylis {
 
+// Routing logit perturbed as model.py:209-213 does it: logit + scale * g with
+// the product and the sum rounded separately (two torch ops).  kind 0: g is
+// the given noise; kind 1: the buffer holds the uniform draw u (torch.rand)
+// and g = -log(-log(u + 1e-9) + 1e-9), the Gumbel transform, each step an
+// fp32 operation like the reference's elementwise ops.
+__device__ __forceinline__ float noisy_logit(float lg, float nz, float scale, int kind) {
+  if (kind == 1) nz = -logf(__fadd_rn(-logf(__fadd_rn(nz, 1e-9f)), 1e-9f));
+  return __fadd_rn(lg, __fmul_rn(scale, nz));
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

@@ -8,6 +8,8 @@ namespace naylis {
 
 struct RouterDims {
   int B, T, D, R, E, topk;
+  int noise_kind = 0;   // 0: additive noise as given; 1: uniform draw, Gumbel-transformed in the kernel
+  long dp_stride = 0;   // d_probs row stride: E (one row per token) or 0 (one row for all tokens)
 };
 
 // Byte offsets into the caller's workspace.  The forward uses [0, fwd_total).
@@ -40,6 +42,10 @@ void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_u
 int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,
                             const float* dg, const float* dp, const float* dl, const float* w_up, float* w,
                             double* wcs, float* wt, float* dwup_part, const RouterDims& d, hipStream_t st);
+// Load-balance statistics of a routing (router_stats.hip): stats[2E + 3].
+size_t router_stats_ws_bytes(long N, int E);
+hipError_t launch_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* ws, long N, int E,
+                               int topk, hipStream_t st);
 void launch_router_fast_dx(const void* x, const float* wt, const float* w_down, const void* dx_in, void* dx,
                            float* dwd_part, const RouterDims& d, hipStream_t st);
 

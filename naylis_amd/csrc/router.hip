@@ -169,9 +169,10 @@ __global__ __launch_bounds__(256) void router_chunk_carry_kernel(double* __restr
 template <typename XT, int EMAX, int TK, bool VECW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void router_fwd_kernel(
     const XT* __restrict__ x, const double* __restrict__ carry, const float* __restrict__ w_down,
-    const float* __restrict__ w_up, const float* __restrict__ noise, float noise_scale, float* __restrict__ logits,
-    float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_gates,
-    float* __restrict__ act, float* __restrict__ h_out, int T, int D, int R, int E, int topk, int n_chunks) {
+    const float* __restrict__ w_up, const float* __restrict__ noise, float noise_scale, int noise_kind,
+    float* __restrict__ logits, float* __restrict__ probs, int32_t* __restrict__ top_idx,
+    float* __restrict__ top_gates, float* __restrict__ act, float* __restrict__ h_out, int T, int D, int R, int E,
+    int topk, int n_chunks) {
   constexpr int CT = kRouterChunk;   // 32 tokens: one MFMA row tile
   constexpr int WP = 65;             // wave tile pitch (floats)
   constexpr int LP = EMAX + 1;
@@ -320,7 +321,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void r
     // top-k of the (optionally perturbed) logits; ties -> lowest block id
     float nz[EMAX];
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e) nz[e] = (e < E) ? (noise ? fmaf(noise_scale, noise[tok * E + e], lg[e]) : lg[e]) : -INFINITY;
+    for (int e = 0; e < EMAX; ++e)
+      nz[e] = (e < E) ? (noise ? noisy_logit(lg[e], noise[tok * E + e], noise_scale, noise_kind) : lg[e]) : -INFINITY;
     int sel[TK];
     float val[TK];
 #pragma unroll
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(256) void router_bwd_token_kernel(
     const float* __restrict__ act, const float* __restrict__ probs, const int32_t* __restrict__ top_idx,
     const float* __restrict__ top_gates, const float* __restrict__ d_gates, const float* __restrict__ d_probs,
     const float* __restrict__ d_logits, const float* __restrict__ w_up, float* __restrict__ w_out,
-    float* __restrict__ dwup_part, int T, int R, int E, int topk, long ntok) {
+    float* __restrict__ dwup_part, int T, int R, int E, int topk, long ntok, long dps) {
   constexpr int TT = 64;
   constexpr int NW = (EMAX * 64 + 255) / 256;  // W_up elements per thread
   constexpr int NA = TT * 64 / 256;            // activation elements per thread
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(256) void router_bwd_token_kernel(
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) {
           pv[e] = e < E ? probs[tok * E + e] : 0.f;
-          dp[e] = e < E ? d_probs[tok * E + e] : 0.f;
+          dp[e] = e < E ? d_probs[tok * dps + e] : 0.f;
         }
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) dot = fmaf(pv[e], dp[e], dot);
@@ -772,12 +774,14 @@ static void fwd_launch(const void* x, const float* w_down, const float* w_up, co
   if (vecw)
     NAYLIS_TIMED("router_fwd", st,
                  hipLaunchKernelGGL((router_fwd_kernel<XT, EMAX, TK, true>), dim3(n_chunks, d.B), dim3(256), 0, st,
-                                    (const XT*)x, carry, w_down, w_up, noise, ns, logits, probs, idx, gates, act, h_out,
+                                    (const XT*)x, carry, w_down, w_up, noise, ns, d.noise_kind, logits, probs, idx,
+                                    gates, act, h_out,
                                     d.T, d.D, d.R, d.E, d.topk, n_chunks));
   else
     NAYLIS_TIMED("router_fwd", st,
                  hipLaunchKernelGGL((router_fwd_kernel<XT, EMAX, TK, false>), dim3(n_chunks, d.B), dim3(256), 0, st,
-                                    (const XT*)x, carry, w_down, w_up, noise, ns, logits, probs, idx, gates, act, h_out,
+                                    (const XT*)x, carry, w_down, w_up, noise, ns, d.noise_kind, logits, probs, idx,
+                                    gates, act, h_out,
                                     d.T, d.D, d.R, d.E, d.topk, n_chunks));
 }
 
@@ -820,7 +824,7 @@ static void bwd_token(const float* act, const float* probs, const int32_t* idx, 
                       const RouterDims& d, hipStream_t st) {
   const long ntok = (long)d.B * d.T;
   NAYLIS_TIMED("router_bwd_token", st, hipLaunchKernelGGL((router_bwd_token_kernel<EMAX, TK>), dim3((int)((ntok + 63) / 64)), dim3(256), 0, st, act, probs,
-                     idx, gates, dg, dp, dl, w_up, w_out, dwup_part, d.T, d.R, d.E, d.topk, ntok));
+                     idx, gates, dg, dp, dl, w_up, w_out, dwup_part, d.T, d.R, d.E, d.topk, ntok, d.dp_stride));
 }
 
 template <typename XT>

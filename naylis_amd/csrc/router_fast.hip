@@ -163,7 +163,8 @@ __global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restri
 template <int EMAX, int TK>
 __global__ __launch_bounds__(256) void router_head_kernel(
     const float* __restrict__ y, const double* __restrict__ ycs, const float* __restrict__ w_up,
-    const float* __restrict__ noise, float noise_scale, float* __restrict__ logits, float* __restrict__ probs,
+    const float* __restrict__ noise, float noise_scale, int noise_kind, float* __restrict__ logits,
+    float* __restrict__ probs,
     int32_t* __restrict__ top_idx, float* __restrict__ top_gates, float* __restrict__ act, int T, int R, int E,
     int topk, int n_ch) {
   constexpr int CT = kFastChunk;
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(256) void router_head_kernel(
     float nz[EMAX];
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
-      nz[e] = (e < E) ? (noise ? fmaf(noise_scale, noise[tok * E + e], lg[e]) : lg[e]) : -INFINITY;
+      nz[e] = (e < E) ? (noise ? noisy_logit(lg[e], noise[tok * E + e], noise_scale, noise_kind) : lg[e]) : -INFINITY;
     int sel[TK];
     float val[TK];
 #pragma unroll
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(256) void router_bwd_token_fast_kernel(
     const float* __restrict__ act, const float* __restrict__ probs, const int32_t* __restrict__ top_idx,
     const float* __restrict__ top_gates, const float* __restrict__ d_gates, const float* __restrict__ d_probs,
     const float* __restrict__ d_logits, const float* __restrict__ w_up, float* __restrict__ w_out,
-    double* __restrict__ wcs, float* __restrict__ dwup_part, int T, int R, int E, int topk, int n_ch) {
+    double* __restrict__ wcs, float* __restrict__ dwup_part, int T, int R, int E, int topk, int n_ch, long dps) {
   constexpr int CT = kFastChunk;
   __shared__ float dl_lds[CT * (EMAX + 1)];
   __shared__ float a_lds[CT * 65];
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(256) void router_bwd_token_fast_kernel(
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) {
           pv[e] = e < E ? probs[tok * E + e] : 0.f;
-          dp[e] = e < E ? d_probs[tok * E + e] : 0.f;
+          dp[e] = e < E ? d_probs[tok * dps + e] : 0.f;
         }
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) dot = fmaf(pv[e], dp[e], dot);
@@ -624,7 +625,8 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
     go(std::integral_constant<int, 16 / RT>{});  // router_fast_fwd_ok bounds nks by 16 / RT
   NAYLIS_TIMED("router_head", st,
                hipLaunchKernelGGL((router_head_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, y, ycs, w_up,
-                                  noise, ns, logits, probs, idx, gates, act, d.T, d.R, d.E, d.topk, n_ch));
+                                  noise, ns, d.noise_kind, logits, probs, idx, gates, act, d.T, d.R, d.E, d.topk,
+                                  n_ch));
 }
 
 template <int RT>
@@ -676,7 +678,7 @@ static void fast_token(const float* act, const float* probs, const int32_t* idx,
   NAYLIS_TIMED("router_bwd_token", st,
                hipLaunchKernelGGL((router_bwd_token_fast_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, act,
                                   probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d.T, d.R, d.E, d.topk,
-                                  n_ch));
+                                  n_ch, d.dp_stride));
 }
 
 int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,

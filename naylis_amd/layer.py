@@ -76,10 +76,12 @@ class MoMLayer(nn.Module):
         mom_kernels.announce(mode)
         return mode
 
-    def route(self, x, noise=None):
-        """Router outputs (logits, probs, top_idx, top_gates) — model.py:207-220."""
+    def route(self, x, noise=None, noise_is_uniform=False):
+        """Router outputs (logits, probs, top_idx, top_gates) — model.py:207-220.
+        ``noise``: additive logit noise, or with ``noise_is_uniform`` the
+        uniform draw that the kernel turns into the Gumbel sample."""
         return mom_kernels.mom_route(x, self.router_down.weight, self.router_up.weight, self.top_blocks,
-                                     noise=noise, noise_scale=self.noise_scale)
+                                     noise=noise, noise_scale=self.noise_scale, noise_is_uniform=noise_is_uniform)
 
     def forward(self, x, M_blocks):
         B, S, D = x.shape
@@ -87,9 +89,10 @@ class MoMLayer(nn.Module):
             self._kernel_mode = self._resolve_kernel(x)
         noise = None
         if self.training and self.noise_scale > 0:
-            # the Gumbel draw of model.py:210, same shape/dtype as the logits
-            u = torch.rand((B, S, self.num_blocks), device=x.device, dtype=torch.float32)
-            noise = -torch.log(-torch.log(u + 1e-9) + 1e-9)
+            # the uniform draw of model.py:210 (torch.rand_like of the fp32 logits: same shape,
+            # dtype and position in the RNG stream); the router kernel applies
+            # g = -log(-log(u + 1e-9) + 1e-9) and logits + noise_scale * g
+            noise = torch.rand((B, S, self.num_blocks), device=x.device, dtype=torch.float32)
         ckpt = self.mom_grad_ckpt and self.training and torch.is_grad_enabled()
         if not ckpt and fused_layer_supported(x, M_blocks, self.router_down.weight, self.router_up.weight,
                                               self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
@@ -99,12 +102,12 @@ class MoMLayer(nn.Module):
                 x, M_blocks, self.router_down.weight, self.router_up.weight, self.q_proj.weight,
                 self.k_proj.weight, self.v_proj.weight, self.o_proj.weight, self.mom_scale,
                 n_heads=self.n_heads, num_blocks=self.num_blocks, block_size=self.block_size,
-                top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale)
+                top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale, noise_is_uniform=True)
             if self.training:
                 self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
                 self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
             return y
-        _, router_probs, top_idx, top_gates = self.route(x, noise)
+        _, router_probs, top_idx, top_gates = self.route(x, noise, noise_is_uniform=True)
         if self.training:
             self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
             self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
@@ -127,24 +130,21 @@ class MoMLayer(nn.Module):
 
 def mom_aux_loss(layers):
     """Load-balance aux loss averaged over MoM layers, plus per-layer router
-    entropy / dead-block fraction — model.py:476-517 (`_collect_mom_aux_loss`),
-    consuming the router probs the fused kernel emits."""
+    entropy / dead-block fraction — model.py:476-517 (`_collect_mom_aux_loss`).
+    Each layer's statistics come from one library pass over the router probs
+    and top_idx it stashed (``mom_kernels.mom_router_stats``); the aux gradient
+    returns to the router as one row per layer, never an (N, E) tensor."""
     aux = None
     count = 0
     for m in layers:
         if not isinstance(m, MoMLayer) or m.last_router_probs is None or m.last_top_idx is None:
             continue
-        probs = m.last_router_probs.float()
-        top_idx = m.last_top_idx
-        blocks = torch.arange(m.num_blocks, device=top_idx.device)
-        sel_mask = (top_idx.unsqueeze(2) == blocks.view(1, 1, -1)).any(1)
-        frac_selected = sel_mask.to(probs.dtype).mean(dim=0)
-        mean_prob = probs.mean(dim=0)
-        term = m.num_blocks * (frac_selected * mean_prob).sum()
+        E = m.num_blocks
+        stats = mom_kernels.mom_router_stats(m.last_router_probs, m.last_top_idx)
+        term = stats[2 * E]
         aux = term if aux is None else aux + term
-        entropy = -(probs * probs.clamp_min(1e-9).log()).sum(-1).mean()
-        m.last_entropy = entropy.detach()
-        m.last_dead_frac = (~sel_mask.any(0)).to(probs.dtype).mean().detach()
+        m.last_entropy = stats[2 * E + 1].detach()
+        m.last_dead_frac = stats[2 * E + 2].detach()
         m.last_router_probs = None
         m.last_top_idx = None
         count += 1

@@ -22,7 +22,8 @@ from .. import _lib
 from .hip_read import mom_read as _hip_mom_read
 
 __all__ = ["HAS_HIP", "preflight", "resolve_mode", "mom_read", "announce", "mom_route",
-           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step"]
+           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step",
+           "mom_router_stats"]
 
 _ANNOUNCED = {"backend": None}
 
@@ -100,6 +101,11 @@ def announce(backend: str) -> None:
 def mom_route(*args, **kwargs):
     from .hip_router import mom_route as _route
     return _route(*args, **kwargs)
+
+
+def mom_router_stats(*args, **kwargs):
+    from .hip_router import mom_router_stats as _stats
+    return _stats(*args, **kwargs)
 
 
 def mom_bank_kv(*args, **kwargs):

@@ -19,6 +19,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from .hip_read import read_order
+from .hip_router import d_probs_arg
 
 _F32, _BF16 = 0, 1
 
@@ -54,7 +55,7 @@ class MomLayerFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, noise, noise_scale, geom):
-        n_heads, num_blocks, block_size, top_k = geom
+        n_heads, num_blocks, block_size, top_k, noise_kind = geom
         lib = _lib.load()
         B, T, D = x.shape
         R, E = w_down.shape[0], w_up.shape[0]
@@ -73,7 +74,8 @@ class MomLayerFunction(torch.autograd.Function):
             rws = _ws(lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, top_k), dev)
             _lib.check(lib.naylis_mom_router_fwd(
                 x.data_ptr(), _BF16, w_down.data_ptr(), w_up.data_ptr(),
-                noise.data_ptr() if noise is not None else None, float(noise_scale), logits.data_ptr(),
+                noise.data_ptr() if noise is not None else None, int(noise_kind), float(noise_scale),
+                logits.data_ptr(),
                 probs.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), act.data_ptr(), None, rws.data_ptr(),
                 rws.numel(), B, T, D, R, E, top_k, st))
             del rws
@@ -111,7 +113,7 @@ class MomLayerFunction(torch.autograd.Function):
     def backward(ctx, dy, d_probs, _d_idx):
         (x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order, out, lse,
          z) = ctx.saved_tensors
-        n_heads, num_blocks, block_size, top_k = ctx.geom
+        n_heads, num_blocks, block_size, top_k, _ = ctx.geom
         lib = _lib.load()
         B, T, D = x.shape
         R, E = w_down.shape[0], w_up.shape[0]
@@ -167,15 +169,14 @@ class MomLayerFunction(torch.autograd.Function):
             dx = torch.mm(dq2, w_q).view(B, T, D)
             dw_q = _wgrad(lib, x.view(N, D), dq2, w_q.dtype, dev, st)
             # ---- router, accumulating into dx
-            if d_probs is not None:
-                d_probs = d_probs.float().contiguous()
+            d_probs, dp_ptr, dp_stride = d_probs_arg(d_probs, E)
             dw_down = torch.empty((R, D), **f32)
             dw_up = torch.empty((E, R), **f32)
             rws = _ws(lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, top_k), dev)
             _lib.check(lib.naylis_mom_router_bwd(
                 x.data_ptr(), _BF16, w_down.data_ptr(), w_up.data_ptr(), act.data_ptr(), probs.data_ptr(),
                 top_idx.data_ptr(), gates.data_ptr(), dgates.data_ptr(),
-                d_probs.data_ptr() if d_probs is not None else None, None, dx.data_ptr(), 1, dw_down.data_ptr(),
+                dp_ptr, dp_stride, None, dx.data_ptr(), 1, dw_down.data_ptr(),
                 dw_up.data_ptr(), rws.data_ptr(), rws.numel(), B, T, D, R, E, top_k, st))
         return (dx, d_slots.view(m_shape), dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None,
                 None)
@@ -198,11 +199,13 @@ def _wgrad(lib, xin, dy, dtype, dev, st):
 
 
 def mom_layer(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, *, n_heads, num_blocks, block_size, top_k,
-              noise=None, noise_scale=1.0):
+              noise=None, noise_scale=1.0, noise_is_uniform=False):
     """The fused layer node; callers check fused_layer_supported() first.
-    Returns (y fp32, router probs, top_idx int32)."""
+    ``noise_is_uniform``: noise is the uniform draw and the router kernel
+    applies the Gumbel transform.  Returns (y fp32, router probs, top_idx int32)."""
     if noise is not None:
         noise = noise.detach().float().contiguous()
     return MomLayerFunction.apply(x, M_blocks, w_down.float().contiguous(), w_up.float().contiguous(), w_q, w_k,
                                   w_v, w_o, scale, noise, float(noise_scale),
-                                  (int(n_heads), int(num_blocks), int(block_size), int(top_k)))
+                                  (int(n_heads), int(num_blocks), int(block_size), int(top_k),
+                                   1 if noise_is_uniform else 0))

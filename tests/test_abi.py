@@ -83,8 +83,20 @@ def test_router_and_bank_reject_bad_arguments(lib):
     assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 65, 2) == 0     # blocks > 64
     assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 4, 5) == 0      # top_k > blocks
     assert lib.naylis_mom_router_workspace_bytes(2, 64, 32, 8, 4, 2) > 0
-    rc = lib.naylis_mom_router_fwd(1, 7, 1, 1, None, 1.0, 1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 64, 32, 8, 4, 2, None)
+    rc = lib.naylis_mom_router_fwd(1, 7, 1, 1, None, 0, 1.0, 1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 64, 32, 8, 4, 2,
+                                   None)
     assert rc == _lib.NAYLIS_ERR_ARG                                           # unknown dtype code
+    rc = lib.naylis_mom_router_fwd(1, 1, 1, 1, 1, 2, 1.0, 1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 64, 32, 8, 4, 2,
+                                   None)
+    assert rc == _lib.NAYLIS_ERR_ARG                                           # unknown noise kind
+    rc = lib.naylis_mom_router_bwd(1, 1, 1, 1, 1, 1, 1, 1, None, 1, 3, None, 1, 0, 1, 1, 1, 1 << 30, 2, 64, 32, 8,
+                                   4, 2, None)
+    assert rc == _lib.NAYLIS_ERR_ARG                                           # d_probs stride not E or 0
+    assert lib.naylis_mom_router_stats_workspace_bytes(100, 8) > 0
+    assert lib.naylis_mom_router_stats_workspace_bytes(100, 65) == 0
+    assert lib.naylis_mom_router_stats(1, 1, 1, 1, 1 << 20, 100, 8, 9, None) == _lib.NAYLIS_ERR_ARG  # top_k > E
+    assert lib.naylis_mom_router_stats(1, 1, 1, 1, 0, 100, 8, 2, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert lib.naylis_mom_router_stats(None, None, 1, None, 0, 0, 8, 2, None) == _lib.NAYLIS_ERR_ARG  # no workspace
     assert lib.naylis_mom_bank_kv_fwd(1, 1, 1, 1, 1, 64, 30, 32, None) == _lib.NAYLIS_ERR_ARG   # D_in % 8
     assert lib.naylis_mom_bank_kv_fwd(None, None, None, None, None, 0, 32, 32, None) == _lib.NAYLIS_OK
     assert lib.naylis_mom_bank_kv_bwd(1, 1, 1, 1, 1, 1, 9, 1, 1, 0, 64, 32, 32, None) == _lib.NAYLIS_ERR_ARG

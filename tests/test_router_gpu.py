@@ -193,7 +193,7 @@ def test_router_backward_accumulates_dx(dev):
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     lg, pr, ti, tg = (torch.empty_like(t) for t in (logits, probs, idx, gates))
     st = _lib.stream_of(dev)
-    assert lib.naylis_mom_router_fwd(xd.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(), None, 1.0, lg.data_ptr(),
+    assert lib.naylis_mom_router_fwd(xd.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(), None, 0, 1.0, lg.data_ptr(),
                                      pr.data_ptr(), ti.data_ptr(), tg.data_ptr(), act.data_ptr(), None,
                                      ws.data_ptr(), nbytes, B, T, D, R, E, k, st) == 0
     prior = (torch.randn(B, T, D, generator=g) * 0.01).bfloat16().to(dev)
@@ -203,7 +203,7 @@ def test_router_backward_accumulates_dx(dev):
         dwd = torch.empty(R, D, device=dev)
         dwu = torch.empty(E, R, device=dev)
         rc = lib.naylis_mom_router_bwd(xd.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(), act.data_ptr(), pr.data_ptr(),
-                                       ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, None, dx.data_ptr(), acc,
+                                       ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, E, None, dx.data_ptr(), acc,
                                        dwd.data_ptr(), dwu.data_ptr(), ws.data_ptr(), nbytes, B, T, D, R, E, k, st)
         assert rc == 0, lib.naylis_mom_last_error()
         outs.append((dx, dwd, dwu))
@@ -218,6 +218,6 @@ def test_router_backward_accumulates_dx(dev):
     # fp32 x cannot accumulate: rejected before any device work
     xf = x.float().to(dev)
     rc = lib.naylis_mom_router_bwd(xf.data_ptr(), 0, wd.data_ptr(), wu.data_ptr(), act.data_ptr(), pr.data_ptr(),
-                                   ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, None, xf.data_ptr(), 1,
+                                   ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, E, None, xf.data_ptr(), 1,
                                    dwd.data_ptr(), dwu.data_ptr(), ws.data_ptr(), nbytes, B, T, D, R, E, k, st)
     assert rc == _lib.NAYLIS_ERR_ARG
