@@ -85,6 +85,23 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& acc, int lo) {
   return r;
 }
 
+// hi = pack8(acc, lo) and the bf16 remainder lo_out = bf16(acc - float(hi)):
+// hi + lo_out carries acc to ~2^-16 relative.  float(hi) is read back from the
+// packed bits (low half << 16, high half masked), so each value costs one
+// subtraction and half a conversion beyond hi.
+__device__ __forceinline__ void pack8_hilo(const f32x16& acc, int lo, bf16x8& hi, bf16x8& lo_out) {
+  hi = pack8(acc, lo);
+  const uint4 hb = __builtin_bit_cast(uint4, hi);
+  const uint32_t w[4] = {hb.x, hb.y, hb.z, hb.w};
+  bf16x8 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    r[2 * p] = (__bf16)(acc[lo + 2 * p] - __uint_as_float(w[p] << 16));
+    r[2 * p + 1] = (__bf16)(acc[lo + 2 * p + 1] - __uint_as_float(w[p] & 0xffff0000u));
+  }
+  lo_out = r;
+}
+
 // ds_read_b64_tr_b16 (gfx950 transposing LDS read), checked on MI355X: within
 // each 16-lane group the 16 lanes x 4 halfwords read form a 16x4 matrix;
 // output lane i, element e is input lane (4e + i/4)'s halfword (i % 4).

@@ -362,7 +362,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t q_lds2[2][TT * PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t do_lds2[2][TT * PITCH];
   __shared__ __attribute__((aligned(16))) float add_lds2[2][4][TT];  // per quarter: c2 - lse, or -inf
-  __shared__ __attribute__((aligned(16))) float dl_lds2[2][TT];
+  __shared__ __attribute__((aligned(16))) float dl_lds2[2][TT];    // -delta per token
   __shared__ int32_t idx_lds2[2][TT * TK];
   __shared__ float lg_lds2[2][TT * TK];
   __shared__ float lse_lds2[2][TT];
@@ -507,7 +507,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
         lg_lds[tid * TK + t] = lg2[t];
       }
       lse_lds[tid] = plse;
-      dl_lds[tid] = pdl;
+      dl_lds[tid] = -pdl;
       if constexpr (ALIGNED) {
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
@@ -549,8 +549,15 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     const float* lg_lds = lg_lds2[buf];
     const float* lse_lds = lse_lds2[buf];
 
-    // ---- S = Q K^T and dP = dO V^T for this wave's 32 tokens x 32 slots
-    f32x16 acc_s = f32x16{}, acc_p = f32x16{};
+    // ---- S = Q K^T and dP - delta = dO V^T - delta for this wave's 32 tokens x
+    // 32 slots (the dP accumulator starts at -delta of each register's token)
+    f32x16 acc_s = f32x16{}, acc_p;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const f32x4 nd4 = *reinterpret_cast<const f32x4*>(&dl_lds[32 * half + 8 * j4 + 4 * g]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd4[u];
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int off = (32 * half + col) * PITCH + 16 * ks + 8 * g;
@@ -563,7 +570,6 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
 #pragma unroll
     for (int j4 = 0; j4 < 4; ++j4) {
       const int r0 = 32 * half + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
-      const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&dl_lds[r0]);
       f32x4 ad4;
       if constexpr (ALIGNED) {
         ad4 = *reinterpret_cast<const f32x4*>(&add_lds[quarter][r0]);
@@ -586,7 +592,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
         const int vv = 4 * j4 + u;
         const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, ad4[u]));
         acc_s[vv] = p;
-        acc_p[vv] = p * (acc_p[vv] - dl4[u]);
+        acc_p[vv] = p * acc_p[vv];
       }
     }
     // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = this wave's 32 tokens)
@@ -595,13 +601,12 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     // dominate the error of small dV entries.
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 bp = pack8(acc_s, 8 * kk);
+      bf16x8 bp, bp_lo;
+      if constexpr (SPLIT_V)
+        pack8_hilo(acc_s, 8 * kk, bp, bp_lo);
+      else
+        bp = pack8(acc_s, 8 * kk);
       const bf16x8 bd = pack8(acc_p, 8 * kk);
-      bf16x8 bp_lo;
-      if constexpr (SPLIT_V) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bp_lo[e] = (__bf16)(acc_s[8 * kk + e] - (float)bp[e]);
-      }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
         const bf16x8 a_do = lds_frag_T<true, true>(do_lds, PITCH, 32 * half + 16 * kk, 32 * j);
