@@ -9,8 +9,10 @@
 //
 // Layout: stats[0, E) mean_prob, [E, 2E) frac, [2E] aux, [2E+1] entropy,
 // [2E+2] dead fraction.  Two launches with a fixed-order reduction: each
-// 256-token workgroup writes fp64 partials (column sums of p, selection
-// counts, entropy sum), one workgroup sums them in workgroup order.
+// 256-token workgroup reduces its tokens per wave (butterfly sums of p and of
+// the entropy, ballot counts of the selections) and writes fp64 partials
+// (the four waves in order); one workgroup sums the partials in workgroup
+// order.
 #include "common.h"
 #include "launch_router.h"
 #include "timing.h"
@@ -24,46 +26,64 @@ __global__ __launch_bounds__(256) void router_stats_partial_kernel(const float* 
                                                                    const int32_t* __restrict__ top_idx,
                                                                    double* __restrict__ part, long N, int E,
                                                                    int topk) {
-  constexpr int P = EMAX + 1;
-  __shared__ float p_lds[kStatsTok * P];
-  __shared__ unsigned long long m_lds[kStatsTok];
-  __shared__ float h_lds[kStatsTok];
-  const int tid = threadIdx.x;
+  __shared__ float wsum[4][EMAX];
+  __shared__ int wcnt[4][EMAX];
+  __shared__ float went[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long tok = (long)blockIdx.x * kStatsTok + tid;
-  float ent = 0.f;
-  unsigned long long mask = 0;
-  if (tok < N) {
-    // entropy term by term in block order, as the reference's fp32 sum over the last axis
-    for (int e = 0; e < E; ++e) {
-      const float p = probs[tok * E + e];
-      p_lds[tid * P + e] = p;
-      ent -= __fmul_rn(p, logf(fmaxf(p, 1e-9f)));
+  const bool ok = tok < N;
+  // this token's probabilities (all loads issued before use)
+  float p[EMAX];
+  if (E % 4 == 0 && (((uintptr_t)probs) & 15) == 0) {
+#pragma unroll
+    for (int e = 0; e < EMAX; e += 4) {
+      const f32x4 v = (ok && e < E) ? *reinterpret_cast<const f32x4*>(probs + tok * E + e) : f32x4{};
+      p[e] = v[0];
+      p[e + 1] = v[1];
+      p[e + 2] = v[2];
+      p[e + 3] = v[3];
     }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) p[e] = (ok && e < E) ? probs[tok * E + e] : 0.f;
+  }
+  unsigned long long mask = 0;
+  if (ok)
     for (int t = 0; t < topk; ++t) {
       const int i = top_idx[tok * topk + t];
       if (i >= 0 && i < E) mask |= 1ull << i;
     }
-  } else {
-    for (int e = 0; e < E; ++e) p_lds[tid * P + e] = 0.f;
+  // entropy term by term in block order, as the reference's fp32 sum over the last axis
+  float ent = 0.f;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+    if (e < E) ent -= __fmul_rn(p[e], logf(fmaxf(p[e], 1e-9f)));
+  if (!ok) ent = 0.f;
+  // per wave: column sums (butterfly), selection counts (ballot), entropy sum
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    if (e < E) {
+      const float s = wave_allsum(p[e]);
+      const int c = __popcll(__ballot((mask >> e) & 1ull));
+      if (lane == 0) {
+        wsum[wave][e] = s;
+        wcnt[wave][e] = c;
+      }
+    }
   }
-  m_lds[tid] = mask;
-  h_lds[tid] = ent;
+  const float es = wave_allsum(ent);
+  if (lane == 0) went[wave] = es;
   __syncthreads();
+  // the workgroup's partials: the four waves in order, in fp64
   const int nv = 2 * E + 1;
   double* out = part + (long)blockIdx.x * nv;
   if (tid < E) {
-    double s = 0.0;
-    for (int i = 0; i < kStatsTok; ++i) s += (double)p_lds[i * P + tid];
-    out[tid] = s;
+    out[tid] = (double)wsum[0][tid] + (double)wsum[1][tid] + (double)wsum[2][tid] + (double)wsum[3][tid];
   } else if (tid >= 64 && tid - 64 < E) {
     const int e = tid - 64;
-    double c = 0.0;
-    for (int i = 0; i < kStatsTok; ++i) c += (double)((m_lds[i] >> e) & 1ull);
-    out[E + e] = c;
+    out[E + e] = (double)(wcnt[0][e] + wcnt[1][e] + wcnt[2][e] + wcnt[3][e]);
   } else if (tid == 128) {
-    double s = 0.0;
-    for (int i = 0; i < kStatsTok; ++i) s += (double)h_lds[i];
-    out[2 * E] = s;
+    out[2 * E] = (double)went[0] + (double)went[1] + (double)went[2] + (double)went[3];
   }
 }
 
@@ -74,8 +94,15 @@ __global__ __launch_bounds__(256) void router_stats_final_kernel(const double* _
   const int tid = threadIdx.x;
   const int nv = 2 * E + 1;
   if (tid < nv) {
+    // partials in workgroup order, 16 loads in flight at a time
     double s = 0.0;
-    for (int w = 0; w < nparts; ++w) s += part[(long)w * nv + tid];
+    for (int w0 = 0; w0 < nparts; w0 += 16) {
+      double v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = w0 + i < nparts ? part[(long)(w0 + i) * nv + tid] : 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += v[i];
+    }
     tot[tid] = s;
   }
   __syncthreads();
