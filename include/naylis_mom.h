@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 5
+#define NAYLIS_MOM_ABI_VERSION 6
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -179,6 +179,22 @@ int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const
 size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E);
 int naylis_mom_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* workspace,
                             size_t workspace_bytes, int64_t N, int64_t E, int64_t top_k, void* stream);
+
+/* ------------------------------------------------------------- RMSNorm ---
+ * The decoder's RMSNorm, fused: model.py:304-305 builds mom_norm (the MoM
+ * layer's pre-norm) and the Llama block's norms as LlamaRMSNorm (or Liger's
+ * fused RMSNorm with use_liger):
+ *   h = fp32(x) * rsqrt(mean(fp32(x)^2) + eps);  y = weight * h.to(dtype)
+ * x, weight, y, dy, dx share one dtype (NAYLIS_DTYPE_*); x (N, D) row-major,
+ * weight (D,), rstd (N,) fp32 written by the forward for the backward.
+ * D a multiple of 512 in [512, 4096]; x / weight / y / dy / dx 16-byte aligned.
+ * The backward writes dx and dweight (summed over rows in a fixed order). */
+int naylis_mom_rmsnorm_fwd(const void* x, int dtype, const void* weight, void* y, float* rstd, int64_t N, int64_t D,
+                           float eps, void* stream);
+size_t naylis_mom_rmsnorm_workspace_bytes(int64_t N, int64_t D);
+int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const float* rstd, const void* dy, void* dx,
+                           void* dweight, void* workspace, size_t workspace_bytes, int64_t N, int64_t D,
+                           void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

@@ -44,6 +44,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 bool pow2(long x) { return x > 0 && (x & (x - 1)) == 0; }
 
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 int check_read_dims(int64_t B, int64_t S, int64_t H, int64_t hd, int64_t num_blocks, int64_t block_size,
                     int64_t top_k, ReadDims* d) {
   if (B < 0 || S < 0 || H <= 0) return fail(NAYLIS_ERR_ARG, "mom_read: bad shape B=%lld S=%lld H=%lld",
@@ -299,6 +301,53 @@ int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const
                     "mom_route_bwd");
 }
 
+static int check_norm(int dtype, int64_t N, int64_t D, const char* who) {
+  int rc = check_dtype(dtype, who);
+  if (rc) return rc;
+  if (N < 0 || N > ((int64_t)1 << 31))
+    return fail(NAYLIS_ERR_ARG, "%s: bad row count N=%lld", who, (long long)N);
+  if (D < 512 || D > 4096 || D % 512 != 0)
+    return fail(NAYLIS_ERR_ARG, "%s: D=%lld must be a multiple of 512 in [512, 4096]", who, (long long)D);
+  return NAYLIS_OK;
+}
+
+int naylis_mom_rmsnorm_fwd(const void* x, int dtype, const void* weight, void* y, float* rstd, int64_t N, int64_t D,
+                           float eps, void* stream) {
+  int rc = check_norm(dtype, N, D, "mom_rmsnorm_fwd");
+  if (rc) return rc;
+  if (!(eps >= 0.f) || eps > 1.f) return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_fwd: eps %g must be in [0, 1]", (double)eps);
+  if (N == 0) return NAYLIS_OK;
+  if (!x || !weight || !y || !rstd) return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_fwd: null pointer argument");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(y))
+    return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_fwd: x, weight and y must be 16-byte aligned");
+  return hip_status(launch_rmsnorm_fwd(x, dtype == NAYLIS_DTYPE_BF16, weight, y, rstd, (long)N, (int)D, eps,
+                                       (hipStream_t)stream),
+                    "mom_rmsnorm_fwd");
+}
+
+size_t naylis_mom_rmsnorm_workspace_bytes(int64_t N, int64_t D) {
+  if (N < 0 || N > ((int64_t)1 << 31) || D < 512 || D > 4096 || D % 512 != 0) return 0;
+  return rmsnorm_ws_bytes((long)N, (int)D);
+}
+
+int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const float* rstd, const void* dy, void* dx,
+                           void* dweight, void* workspace, size_t workspace_bytes, int64_t N, int64_t D,
+                           void* stream) {
+  int rc = check_norm(dtype, N, D, "mom_rmsnorm_bwd");
+  if (rc) return rc;
+  if (!weight || !dweight || !workspace) return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_bwd: null pointer argument");
+  if (N > 0 && (!x || !rstd || !dy || !dx)) return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_bwd: null pointer argument");
+  if (N > 0 && (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dx)))
+    return fail(NAYLIS_ERR_ARG, "mom_rmsnorm_bwd: x, weight, dy and dx must be 16-byte aligned");
+  const size_t need = rmsnorm_ws_bytes((long)N, (int)D);
+  if (workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_rmsnorm_bwd: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  return hip_status(launch_rmsnorm_bwd(x, dtype == NAYLIS_DTYPE_BF16, weight, rstd, dy, dx, dweight, workspace,
+                                       (long)N, (int)D, (hipStream_t)stream),
+                    "mom_rmsnorm_bwd");
+}
+
 size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E) {
   if (N < 0 || N > ((int64_t)1 << 30) || E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS) return 0;
   return router_stats_ws_bytes((long)N, (int)E);
@@ -454,8 +503,6 @@ int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dty
 
 // ---------------------------------------------------------------- decode step
 namespace {
-
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 bool overlap(const void* a, const void* b, size_t bytes) {
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;

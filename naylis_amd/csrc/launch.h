@@ -57,6 +57,15 @@ hipError_t launch_decode_step(const double* state_in, double* state_out, const i
                               const uint8_t* k8, const uint8_t* v8, const float* k_scale, const float* v_scale,
                               void* out, int32_t* top_idx, float* top_gates, const DecodeDims& d, hipStream_t st);
 
+// Fused RMSNorm (rmsnorm.hip): rows of D features, D a multiple of 512 up to
+// 4096; x, w, y, dy, dx in one dtype (bf16 or fp32); rstd fp32 per row.
+int rmsnorm_bwd_parts(long N);
+size_t rmsnorm_ws_bytes(long N, int D);
+hipError_t launch_rmsnorm_fwd(const void* x, bool bf16, const void* w, void* y, float* rstd, long N, int D,
+                              float eps, hipStream_t st);
+hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy, void* dx,
+                              void* dw, void* ws, long N, int D, hipStream_t st);
+
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }

@@ -13,7 +13,10 @@ What differs from the reference is where the MoM work runs: ``self.mom`` is
 ``naylis_amd.layer.MoMLayer`` (router, bank K/V, read, ReZero on the library's
 kernels, one autograd node per layer) and the load-balance aux loss consumes
 the router probabilities that kernel emits (``naylis_amd.layer.mom_aux_loss``).
-There is no eager MoM path: off ROCm the MoM layers raise.
+There is no eager MoM path: off ROCm the MoM layers raise.  The norms
+(``mom_norm``, the block's two norms, the final norm) are the library's fused
+RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
+when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise.
 """
 from __future__ import annotations
 
@@ -26,9 +29,20 @@ from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaFo
                                                       LlamaRMSNorm)
 
 from .layer import MoMLayer, mom_aux_loss
+from .mom_kernels.hip_norm import NaylisRMSNorm
 
 __all__ = ["naylis_config", "NaylisDecoderLayer", "NaylisLlamaModel", "NaylisLlamaForCausalLM",
            "cast_for_training"]
+
+
+def _norm(config):
+    """RMSNorm module for the hidden size: the fused library norm where its
+    kernels apply (hidden a multiple of 512 in [512, 4096]), else LlamaRMSNorm;
+    both hold one ``weight`` (hidden,) and compute the same function."""
+    d = config.hidden_size
+    if d % 512 == 0 and 512 <= d <= 4096:
+        return NaylisRMSNorm(d, eps=config.rms_norm_eps)
+    return LlamaRMSNorm(d, eps=config.rms_norm_eps)
 
 
 def naylis_config(vocab_size=32768, d_model=1024, n_layers=20, n_heads=16, intermediate_size=2816, seq_len=2048,
@@ -67,7 +81,9 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
     def __init__(self, config, layer_idx, mem_size, mom_block_size, mom_top_blocks, mom_router_rank,
                  mom_grad_ckpt=False):
         super().__init__(config, layer_idx)
-        self.mom_norm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.input_layernorm = _norm(config)
+        self.post_attention_layernorm = _norm(config)
+        self.mom_norm = _norm(config)
         self.mom = MoMLayer(d_model=config.hidden_size, n_heads=config.num_attention_heads, mem_size=mem_size,
                             block_size=mom_block_size, top_blocks=mom_top_blocks, router_rank=mom_router_rank,
                             mom_grad_ckpt=mom_grad_ckpt)
@@ -101,6 +117,7 @@ class NaylisLlamaModel(LlamaModel):
             raise ValueError(f"mem_size ({mem_size}) must be a multiple of mom_block_size ({mom_block_size})")
         num_blocks = mem_size // mom_block_size
         self.M_blocks = nn.Parameter(torch.randn(num_blocks, mom_block_size * config.hidden_size) * 0.02)
+        self.norm = _norm(config)
         self.layers = nn.ModuleList([
             NaylisDecoderLayer(config, i, mem_size, mom_block_size, mom_top_blocks, mom_router_rank, mom_grad_ckpt)
             for i in range(config.num_hidden_layers)])

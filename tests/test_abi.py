@@ -97,6 +97,19 @@ def test_router_and_bank_reject_bad_arguments(lib):
     assert lib.naylis_mom_router_stats(1, 1, 1, 1, 1 << 20, 100, 8, 9, None) == _lib.NAYLIS_ERR_ARG  # top_k > E
     assert lib.naylis_mom_router_stats(1, 1, 1, 1, 0, 100, 8, 2, None) == _lib.NAYLIS_ERR_WORKSPACE
     assert lib.naylis_mom_router_stats(None, None, 1, None, 0, 0, 8, 2, None) == _lib.NAYLIS_ERR_ARG  # no workspace
+
+
+def test_rmsnorm_rejects_bad_arguments(lib):
+    p = 0x1000
+    assert lib.naylis_mom_rmsnorm_workspace_bytes(16384, 1024) > 0
+    assert lib.naylis_mom_rmsnorm_workspace_bytes(16384, 1000) == 0
+    assert lib.naylis_mom_rmsnorm_fwd(p, 1, p, p, p, 8, 1000, 1e-5, None) == _lib.NAYLIS_ERR_ARG    # D % 512
+    assert lib.naylis_mom_rmsnorm_fwd(p, 1, p, p, p, 8, 8192, 1e-5, None) == _lib.NAYLIS_ERR_ARG    # D > 4096
+    assert lib.naylis_mom_rmsnorm_fwd(p, 3, p, p, p, 8, 1024, 1e-5, None) == _lib.NAYLIS_ERR_ARG    # dtype
+    assert lib.naylis_mom_rmsnorm_fwd(p, 1, p, p, p, 8, 1024, -1.0, None) == _lib.NAYLIS_ERR_ARG    # eps
+    assert lib.naylis_mom_rmsnorm_fwd(p + 2, 1, p, p, p, 8, 1024, 1e-5, None) == _lib.NAYLIS_ERR_ARG  # alignment
+    assert lib.naylis_mom_rmsnorm_fwd(None, 1, None, None, None, 0, 1024, 1e-5, None) == _lib.NAYLIS_OK
+    assert lib.naylis_mom_rmsnorm_bwd(p, 1, p, p, p, p, p, p, 0, 8, 1024, None) == _lib.NAYLIS_ERR_WORKSPACE
     assert lib.naylis_mom_bank_kv_fwd(1, 1, 1, 1, 1, 64, 30, 32, None) == _lib.NAYLIS_ERR_ARG   # D_in % 8
     assert lib.naylis_mom_bank_kv_fwd(None, None, None, None, None, 0, 32, 32, None) == _lib.NAYLIS_OK
     assert lib.naylis_mom_bank_kv_bwd(1, 1, 1, 1, 1, 1, 9, 1, 1, 0, 64, 32, 32, None) == _lib.NAYLIS_ERR_ARG

@@ -122,10 +122,11 @@ def _oracle_grads(cfg, state, ids, dtype, routing):
                                               if p.grad is not None}
 
 
-def _tiny_gpu_model(dev, **over):
+def _tiny_gpu_model(dev, d_model=256, **over):
+    """d_model 256 keeps transformers' LlamaRMSNorm, 512 uses the fused norm."""
     torch.manual_seed(0)
-    cfg = naylis_config(**dict(TINY, d_model=256, n_heads=4, intermediate_size=512, mem_size=256,
-                               mom_block_size=64, mom_router_rank=16, **over))
+    cfg = naylis_config(**dict(TINY, d_model=d_model, n_heads=d_model // 64, intermediate_size=2 * d_model,
+                               mem_size=256, mom_block_size=64, mom_router_rank=16, **over))
     model = NaylisLlamaForCausalLM(cfg)
     with torch.no_grad():
         for layer in model.model.layers:
@@ -137,7 +138,8 @@ def _tiny_gpu_model(dev, **over):
 
 
 @pytest.mark.gpu
-def test_decoder_mom_layers_match_oracle_on_their_inputs(dev):
+@pytest.mark.parametrize("d_model", [256, 512])
+def test_decoder_mom_layers_match_oracle_on_their_inputs(d_model, dev):
     """Every MoM layer of the bf16 decoder, on the input the decoder gave it:
     routing equal to the fp64 oracle router outside near-ties (margin
     1e-5 max|logit|) and output within 1e-2 relative Frobenius of the fp32
@@ -145,7 +147,7 @@ def test_decoder_mom_layers_match_oracle_on_their_inputs(dev):
     moves tokens whose top-2 margin is below ~1 % to another block in any
     bf16 implementation, so whole-model comparisons force the routing.)"""
     from naylis_amd.layer import MoMLayer
-    cfg, model = _tiny_gpu_model(dev)
+    cfg, model = _tiny_gpu_model(dev, d_model)
     ids = torch.randint(0, cfg.vocab_size, (2, 128), generator=torch.Generator().manual_seed(5))
     caps = {}
     moms = [m for m in model.modules() if isinstance(m, MoMLayer)]
@@ -175,7 +177,8 @@ def test_decoder_mom_layers_match_oracle_on_their_inputs(dev):
 
 
 @pytest.mark.gpu
-def test_decoder_loss_and_grads_match_oracle(dev):
+@pytest.mark.parametrize("d_model", [256, 512])
+def test_decoder_loss_and_grads_match_oracle(d_model, dev):
     """bf16 decoder on the GPU vs the fp32 oracle on the CPU: same bf16-valued
     weights, Gumbel off, training mode (aux loss on), the oracle's routing
     forced to the decoder's (see the test above).  Loss and aux agree to 1e-2
@@ -185,7 +188,10 @@ def test_decoder_loss_and_grads_match_oracle(dev):
     weights, the shared bank) carry several percent of bf16 error in the eager
     reference itself."""
     from naylis_amd.layer import MoMLayer
-    cfg, model = _tiny_gpu_model(dev)
+    from naylis_amd.mom_kernels.hip_norm import NaylisRMSNorm
+    cfg, model = _tiny_gpu_model(dev, d_model)
+    fused_norms = sum(isinstance(m, NaylisRMSNorm) for m in model.modules())
+    assert fused_norms == (3 * cfg.num_hidden_layers + 1 if d_model == 512 else 0)
     state = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
     ids = torch.randint(0, cfg.vocab_size, (2, 128), generator=torch.Generator().manual_seed(5))
     with torch.no_grad():
