@@ -572,6 +572,27 @@ def main(argv=None):
     read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
     read_flop = 14.0 * D * BS * 128 * A
     read_tf = read_flop / (read_ms * 1e-3) / 1e12
+    # library GEMMs on the MFMA (bank K/V and its gradients, q/o weight gradients)
+    gemms = {k: {"us": round(per[k][0] * 1e3, 2), "tflops": round(alg[k] / (per[k][0] * 1e-3) / 1e12, 1),
+                 "mfma_frac": round(alg[k] / (per[k][0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+             for k in ("bank_kv_fwd", "bank_kv_bwd_dslots", "bank_kv_bwd_dw", "linear_wgrad") if k in per}
+    # the prefix-mean router against HBM: forward reads x once and writes logits / probs / top-k /
+    # gates / activations (plus the (N, R) projection written and read back); the backward reads x,
+    # the incoming dx and writes dx (the accumulating input gradient), plus the (N, R) and (N, E)
+    # per-token terms
+    R_, E_, K_ = cfg["R"], E, cfg["K"]
+    f_bytes = ntok * D * 2 + ntok * (2 * E_ + 2 * K_ + R_ + 2 * R_) * 4
+    b_bytes = 3 * ntok * D * 2 + ntok * (3 * R_ + 2 * E_ + 3 * K_) * 4
+    f_us = sum(per[k][0] * per[k][1] for k in ("router_proj", "router_head") if k in per) * 1e3
+    b_us = sum(per[k][0] * per[k][1] for k in ("router_bwd_token", "router_bwd_scan", "router_bwd_dx",
+                                               "router_reduce") if k in per) * 1e3
+    router = {"fwd_alg_bytes": f_bytes, "fwd_us": round(f_us, 2), "bwd_alg_bytes": b_bytes, "bwd_us": round(b_us, 2)}
+    if f_us > 0:
+        router["fwd_gbs"] = round(f_bytes / (f_us * 1e-6) / 1e9, 1)
+        router["fwd_hbm_frac"] = round(router["fwd_gbs"] / PEAK_HBM_GBS, 4)
+    if b_us > 0:
+        router["bwd_gbs"] = round(b_bytes / (b_us * 1e-6) / 1e9, 1)
+        router["bwd_hbm_frac"] = round(router["bwd_gbs"] / PEAK_HBM_GBS, 4)
     line = {
         "metric": METRIC,
         "value": round(ntok / (ms_per_step * 1e-3), 1),
@@ -593,6 +614,8 @@ def main(argv=None):
                  "token_order": order_mode, "executed_tile_blocks": A_exec,
                  "alg_flop": read_flop, "ms": round(read_ms, 4), "tflops": round(read_tf, 2),
                  "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
+        "gemms": gemms,
+        "router": router,
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
         "kernels_timing": f"HIP events per launch over a second region of {args.steps} steps "
                           f"({ms_per_step_events:.4f} ms/step with the events)",
