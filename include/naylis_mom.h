@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 6
+#define NAYLIS_MOM_ABI_VERSION 7
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -195,6 +195,21 @@ size_t naylis_mom_rmsnorm_workspace_bytes(int64_t N, int64_t D);
 int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const float* rstd, const void* dy, void* dx,
                            void* dweight, void* workspace, size_t workspace_bytes, int64_t N, int64_t D,
                            void* stream);
+
+/* ---------------------------------------------------------------- RoPE ---
+ * Rotary position embedding of the decoder attention's q and k
+ * (transformers' apply_rotary_pos_emb inside the Llama attention of each
+ * Naylis decoder layer, model.py:279-345):
+ *   out = x * cos + rotate_half(x) * sin,  rotate_half(a | b) = (-b | a)
+ * with each product rounded to the dtype before the sum, as the reference's
+ * elementwise ops.  backward != 0 applies the transposed rotation to incoming
+ * gradients: out = dy * cos + rotate_half^T(dy * sin), rotate_half^T(a | b) =
+ * (b | -a).  q, k, q_out, k_out (B, S, H, head_dim) row-major, outputs not
+ * overlapping the inputs, cos / sin (cos_batch, S, head_dim) with cos_batch 1 or B;
+ * head_dim 32, 64 or 128; one dtype (NAYLIS_DTYPE_*) for all. */
+int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* sin, void* q_out, void* k_out,
+                    int dtype, int backward, int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t cos_batch,
+                    void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

@@ -348,6 +348,39 @@ int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const f
                     "mom_rmsnorm_bwd");
 }
 
+int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* sin, void* q_out, void* k_out,
+                    int dtype, int backward, int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t cos_batch,
+                    void* stream) {
+  int rc = check_dtype(dtype, "mom_rope");
+  if (rc) return rc;
+  if (B < 0 || S < 0 || H < 0 || B * S * H > ((int64_t)1 << 30))
+    return fail(NAYLIS_ERR_ARG, "mom_rope: bad shape B=%lld S=%lld H=%lld", (long long)B, (long long)S, (long long)H);
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(NAYLIS_ERR_ARG, "mom_rope: head_dim %lld must be 32, 64 or 128", (long long)head_dim);
+  if (cos_batch != 1 && cos_batch != B)
+    return fail(NAYLIS_ERR_ARG, "mom_rope: cos / sin batch %lld must be 1 or B=%lld", (long long)cos_batch,
+                (long long)B);
+  if (B * S * H == 0) return NAYLIS_OK;
+  if (!q || !k || !cos || !sin || !q_out || !k_out) return fail(NAYLIS_ERR_ARG, "mom_rope: null pointer argument");
+  {
+    const size_t bytes = (size_t)(B * S * H * head_dim) * (dtype == NAYLIS_DTYPE_BF16 ? 2 : 4);
+    const void* ins[2] = {q, k};
+    const void* outs[2] = {q_out, k_out};
+    for (const void* o : outs)
+      for (const void* in : ins) {
+        const uintptr_t a = (uintptr_t)o, b = (uintptr_t)in;
+        if (a < b + bytes && b < a + bytes)
+          return fail(NAYLIS_ERR_ARG, "mom_rope: outputs must not overlap q or k");
+      }
+    if (!aligned16(q) || !aligned16(k) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) ||
+        !aligned16(k_out))
+      return fail(NAYLIS_ERR_ARG, "mom_rope: all tensors must be 16-byte aligned");
+  }
+  return hip_status(launch_rope(q, k, cos, sin, q_out, k_out, dtype == NAYLIS_DTYPE_BF16, backward != 0, (long)B,
+                                (int)S, (int)H, (int)head_dim, (int)cos_batch, (hipStream_t)stream),
+                    "mom_rope");
+}
+
 size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E) {
   if (N < 0 || N > ((int64_t)1 << 30) || E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS) return 0;
   return router_stats_ws_bytes((long)N, (int)E);

@@ -24,14 +24,27 @@
 
 namespace naylis {
 
+// fp32 product / sum rounded on their own: HIP compiles with fp contraction
+// on, and __fmul_rn / __fadd_rn are plain operators there, so a product
+// followed by a sum may become one fused multiply-add.  These carry no
+// contraction flag, which keeps the two roundings of a torch expression.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 // Routing logit perturbed as model.py:209-213 does it: logit + scale * g with
 // the product and the sum rounded separately (two torch ops).  kind 0: g is
 // the given noise; kind 1: the buffer holds the uniform draw u (torch.rand)
 // and g = -log(-log(u + 1e-9) + 1e-9), the Gumbel transform, each step an
 // fp32 operation like the reference's elementwise ops.
 __device__ __forceinline__ float noisy_logit(float lg, float nz, float scale, int kind) {
-  if (kind == 1) nz = -logf(__fadd_rn(-logf(__fadd_rn(nz, 1e-9f)), 1e-9f));
-  return __fadd_rn(lg, __fmul_rn(scale, nz));
+  if (kind == 1) nz = -logf(add_rn(-logf(add_rn(nz, 1e-9f)), 1e-9f));
+  return add_rn(lg, mul_rn(scale, nz));
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -66,6 +66,12 @@ hipError_t launch_rmsnorm_fwd(const void* x, bool bf16, const void* w, void* y, 
 hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy, void* dx,
                               void* dw, void* ws, long N, int D, hipStream_t st);
 
+// Rotary position embedding of q and k (rope.hip): x (B, S, H, HD) for HD in
+// {32, 64, 128}, cos / sin (cos_batch, S, HD) with cos_batch 1 or B; bwd applies
+// the transposed rotation to the incoming gradients.
+hipError_t launch_rope(const void* q, const void* k, const void* cs, const void* sn, void* qo, void* ko, bool bf16,
+                       bool bwd, long B, int S, int H, int HD, int cos_batch, hipStream_t st);
+
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }

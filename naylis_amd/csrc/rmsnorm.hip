@@ -87,13 +87,13 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss = fmaf(xc[c].get(e), xc[c].get(e), ss);
   ss = wave_allsum(ss);
-  const float r = rsqrtf(__fadd_rn(__fmul_rn(ss, 1.0f / (float)D), eps));
+  const float r = rsqrtf(add_rn(mul_rn(ss, 1.0f / (float)D), eps));
   T* yr = y + row * D;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(wc[c].get(e), round_to<T>(__fmul_rn(xc[c].get(e), r)));
+    for (int e = 0; e < 8; ++e) v[e] = mul_rn(wc[c].get(e), round_to<T>(mul_rn(xc[c].get(e), r)));
     store8(yr + (c * 64 + lane) * 8, v);
   }
   if (lane == 0) rstd[row] = r;
@@ -130,9 +130,9 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
     for (int c = 0; c < CH; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        h[c][e] = __fmul_rn(xc[c].get(e), r);
+        h[c][e] = mul_rn(xc[c].get(e), r);
         dwa[c][e] = fmaf(gc[c].get(e), round_to<T>(h[c][e]), dwa[c][e]);
-        dh[c][e] = round_to<T>(__fmul_rn(gc[c].get(e), wc[c].get(e)));
+        dh[c][e] = round_to<T>(mul_rn(gc[c].get(e), wc[c].get(e)));
         m = fmaf(dh[c][e], h[c][e], m);
       }
     m = wave_allsum(m) * (1.0f / (float)D);

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void router_stats_partial_kernel(const float* 
   float ent = 0.f;
 #pragma unroll
   for (int e = 0; e < EMAX; ++e)
-    if (e < E) ent -= __fmul_rn(p[e], logf(fmaxf(p[e], 1e-9f)));
+    if (e < E) ent -= mul_rn(p[e], logf(fmaxf(p[e], 1e-9f)));
   if (!ok) ent = 0.f;
   // per wave: column sums (butterfly), selection counts (ballot), entropy sum
 #pragma unroll
@@ -116,10 +116,10 @@ __global__ __launch_bounds__(256) void router_stats_final_kernel(const double* _
     float aux = 0.f;
     int dead = 0;
     for (int e = 0; e < E; ++e) {
-      aux = __fadd_rn(aux, __fmul_rn((float)(tot[E + e] * inv), (float)(tot[e] * inv)));
+      aux = add_rn(aux, mul_rn((float)(tot[E + e] * inv), (float)(tot[e] * inv)));
       dead += tot[E + e] == 0.0;
     }
-    stats[2 * E] = __fmul_rn((float)E, aux);
+    stats[2 * E] = mul_rn((float)E, aux);
     stats[2 * E + 1] = (float)(tot[2 * E] * inv);
     stats[2 * E + 2] = (float)dead / (float)E;
   }

@@ -16,7 +16,9 @@ the router probabilities that kernel emits (``naylis_amd.layer.mom_aux_loss``).
 There is no eager MoM path: off ROCm the MoM layers raise.  The norms
 (``mom_norm``, the block's two norms, the final norm) are the library's fused
 RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
-when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise.
+when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise;
+the attention applies the rotary embedding with the library's fused kernel
+(``NaylisAttention``, same parameters and SDPA backend).
 """
 from __future__ import annotations
 
@@ -30,6 +32,7 @@ from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaFo
 
 from .layer import MoMLayer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm
+from .mom_kernels.hip_rope import NaylisAttention
 
 __all__ = ["naylis_config", "NaylisDecoderLayer", "NaylisLlamaModel", "NaylisLlamaForCausalLM",
            "cast_for_training"]
@@ -81,6 +84,7 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
     def __init__(self, config, layer_idx, mem_size, mom_block_size, mom_top_blocks, mom_router_rank,
                  mom_grad_ckpt=False):
         super().__init__(config, layer_idx)
+        self.self_attn = NaylisAttention(config, layer_idx)
         self.input_layernorm = _norm(config)
         self.post_attention_layernorm = _norm(config)
         self.mom_norm = _norm(config)

@@ -206,3 +206,14 @@ def test_layer_constructor_contract():
                      "o_proj.weight", "mom_scale"}                               # checkpoint-compatible names
     with pytest.raises(RuntimeError):
         layer(torch.zeros(1, 4, 32), torch.zeros(4, 16 * 32))                   # CPU tensors: no fallback
+
+
+def test_rope_rejects_bad_arguments(lib):
+    p = 0x1000
+    assert lib.naylis_mom_rope(p, p, p, p, p, p, 1, 0, 2, 8, 4, 48, 1, None) == _lib.NAYLIS_ERR_ARG   # head_dim
+    assert lib.naylis_mom_rope(p, p, p, p, p, p, 1, 0, 2, 8, 4, 64, 3, None) == _lib.NAYLIS_ERR_ARG   # cos batch
+    assert lib.naylis_mom_rope(p, p, p, p, p, p, 5, 0, 2, 8, 4, 64, 1, None) == _lib.NAYLIS_ERR_ARG   # dtype
+    assert lib.naylis_mom_rope(None, p, p, p, p, p, 1, 0, 2, 8, 4, 64, 1, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_rope(None, None, None, None, None, None, 1, 0, 0, 8, 4, 64, 1, None) == _lib.NAYLIS_OK
+    q, k, c, o = 0x100000, 0x200000, 0x300000, 0x400000
+    assert lib.naylis_mom_rope(q, k, c, c, q, o, 1, 0, 2, 8, 4, 64, 1, None) == _lib.NAYLIS_ERR_ARG   # in place
