@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 7
+#define NAYLIS_MOM_ABI_VERSION 8
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -210,6 +210,16 @@ int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const f
 int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* sin, void* q_out, void* k_out,
                     int dtype, int backward, int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t cos_batch,
                     void* stream);
+
+/* -------------------------------------------------------------- SwiGLU ---
+ * The decoder MLP's activation (transformers' LlamaMLP inside each Naylis
+ * decoder layer, model.py:279-345): h = silu(gate) * up, silu(g) =
+ * g / (1 + exp(-g)), silu rounded to the dtype before the product.  The
+ * backward writes dgate = silu'(gate) * T(dh * up) and dup = dh * T(silu(gate)).
+ * n elements (a multiple of 8) of one dtype, 16-byte aligned. */
+int naylis_mom_swiglu_fwd(const void* gate, const void* up, void* h, int dtype, int64_t n, void* stream);
+int naylis_mom_swiglu_bwd(const void* gate, const void* up, const void* dh, void* dgate, void* dup, int dtype,
+                          int64_t n, void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

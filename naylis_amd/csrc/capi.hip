@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <string>
+#include <initializer_list>
 
 #include "../../include/naylis_mom.h"
 #include "launch.h"
@@ -379,6 +380,36 @@ int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* s
   return hip_status(launch_rope(q, k, cos, sin, q_out, k_out, dtype == NAYLIS_DTYPE_BF16, backward != 0, (long)B,
                                 (int)S, (int)H, (int)head_dim, (int)cos_batch, (hipStream_t)stream),
                     "mom_rope");
+}
+
+static int check_swiglu(int dtype, int64_t n, std::initializer_list<const void*> ptrs, const char* who) {
+  int rc = check_dtype(dtype, who);
+  if (rc) return rc;
+  if (n < 0 || n % 8 != 0 || n > ((int64_t)1 << 36))
+    return fail(NAYLIS_ERR_ARG, "%s: element count %lld must be a non-negative multiple of 8", who, (long long)n);
+  if (n == 0) return NAYLIS_OK;
+  for (const void* p : ptrs) {
+    if (!p) return fail(NAYLIS_ERR_ARG, "%s: null pointer argument", who);
+    if (!aligned16(p)) return fail(NAYLIS_ERR_ARG, "%s: every tensor must be 16-byte aligned", who);
+  }
+  return NAYLIS_OK;
+}
+
+int naylis_mom_swiglu_fwd(const void* gate, const void* up, void* h, int dtype, int64_t n, void* stream) {
+  int rc = check_swiglu(dtype, n, {gate, up, h}, "mom_swiglu_fwd");
+  if (rc || n == 0) return rc;
+  return hip_status(launch_swiglu(gate, up, nullptr, h, nullptr, dtype == NAYLIS_DTYPE_BF16, false, (long)n,
+                                  (hipStream_t)stream),
+                    "mom_swiglu_fwd");
+}
+
+int naylis_mom_swiglu_bwd(const void* gate, const void* up, const void* dh, void* dgate, void* dup, int dtype,
+                          int64_t n, void* stream) {
+  int rc = check_swiglu(dtype, n, {gate, up, dh, dgate, dup}, "mom_swiglu_bwd");
+  if (rc || n == 0) return rc;
+  return hip_status(launch_swiglu(gate, up, dh, dgate, dup, dtype == NAYLIS_DTYPE_BF16, true, (long)n,
+                                  (hipStream_t)stream),
+                    "mom_swiglu_bwd");
 }
 
 size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E) {

@@ -72,6 +72,11 @@ hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const flo
 hipError_t launch_rope(const void* q, const void* k, const void* cs, const void* sn, void* qo, void* ko, bool bf16,
                        bool bwd, long B, int S, int H, int HD, int cos_batch, hipStream_t st);
 
+// SwiGLU of the decoder MLP (swiglu.hip): h = silu(g) * u forward; backward
+// writes dg and du from dh; n elements, a multiple of 8.
+hipError_t launch_swiglu(const void* g, const void* u, const void* dh, void* h_or_dg, void* du, bool bf16, bool bwd,
+                         long n, hipStream_t st);
+
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }

@@ -18,7 +18,8 @@ There is no eager MoM path: off ROCm the MoM layers raise.  The norms
 RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
 when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise;
 the attention applies the rotary embedding with the library's fused kernel
-(``NaylisAttention``, same parameters and SDPA backend).
+(``NaylisAttention``, same parameters and SDPA backend) and the MLP its fused
+SwiGLU (``NaylisMLP``).
 """
 from __future__ import annotations
 
@@ -32,6 +33,7 @@ from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaFo
 
 from .layer import MoMLayer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm
+from .mom_kernels.hip_mlp import NaylisMLP
 from .mom_kernels.hip_rope import NaylisAttention
 
 __all__ = ["naylis_config", "NaylisDecoderLayer", "NaylisLlamaModel", "NaylisLlamaForCausalLM",
@@ -85,6 +87,7 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
                  mom_grad_ckpt=False):
         super().__init__(config, layer_idx)
         self.self_attn = NaylisAttention(config, layer_idx)
+        self.mlp = NaylisMLP(config)
         self.input_layernorm = _norm(config)
         self.post_attention_layernorm = _norm(config)
         self.mom_norm = _norm(config)

@@ -217,3 +217,12 @@ def test_rope_rejects_bad_arguments(lib):
     assert lib.naylis_mom_rope(None, None, None, None, None, None, 1, 0, 0, 8, 4, 64, 1, None) == _lib.NAYLIS_OK
     q, k, c, o = 0x100000, 0x200000, 0x300000, 0x400000
     assert lib.naylis_mom_rope(q, k, c, c, q, o, 1, 0, 2, 8, 4, 64, 1, None) == _lib.NAYLIS_ERR_ARG   # in place
+
+
+def test_swiglu_rejects_bad_arguments(lib):
+    p = 0x1000
+    assert lib.naylis_mom_swiglu_fwd(p, p, p, 1, 12, None) == _lib.NAYLIS_ERR_ARG          # n % 8
+    assert lib.naylis_mom_swiglu_fwd(p, p, p, 4, 16, None) == _lib.NAYLIS_ERR_ARG          # dtype
+    assert lib.naylis_mom_swiglu_fwd(p + 4, p, p, 1, 16, None) == _lib.NAYLIS_ERR_ARG      # alignment
+    assert lib.naylis_mom_swiglu_bwd(p, p, None, p, p, 1, 16, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_swiglu_fwd(None, None, None, 1, 0, None) == _lib.NAYLIS_OK
