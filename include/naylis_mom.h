@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 8
+#define NAYLIS_MOM_ABI_VERSION 9
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -220,6 +220,19 @@ int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* s
 int naylis_mom_swiglu_fwd(const void* gate, const void* up, void* h, int dtype, int64_t n, void* stream);
 int naylis_mom_swiglu_bwd(const void* gate, const void* up, const void* dh, void* dgate, void* dup, int dtype,
                           int64_t n, void* stream);
+
+/* ------------------------------------------------------- cross-entropy ---
+ * The LM head loss of the decoder (model.py:536-545: F.cross_entropy of the
+ * fp32 logits, reduction "sum", ignore_index) from bf16 logits (N, V) in one
+ * pass: the forward writes each row's loss (log-sum-exp minus the label's
+ * logit; 0 for rows labelled ignore_index) and its log-sum-exp; the backward
+ * writes dlogits (N, V) bf16 = (softmax - one_hot(label)) * grad_rows[r *
+ * grad_stride] (grad_stride 1: one gradient per row, 0: one for all rows).
+ * V a multiple of 2048; labels int64; logits / dlogits 16-byte aligned. */
+int naylis_mom_xent_fwd(const void* logits, const int64_t* labels, float* loss_rows, float* lse, int64_t N, int64_t V,
+                        int64_t ignore_index, void* stream);
+int naylis_mom_xent_bwd(const void* logits, const int64_t* labels, const float* lse, const float* grad_rows,
+                        int64_t grad_stride, void* dlogits, int64_t N, int64_t V, int64_t ignore_index, void* stream);
 
 /* ------------------------------------------------------------ bank K/V ---
  * Projection of the shared bank, once per layer and shared by the batch:

@@ -412,6 +412,39 @@ int naylis_mom_swiglu_bwd(const void* gate, const void* up, const void* dh, void
                     "mom_swiglu_bwd");
 }
 
+static int check_xent(int64_t N, int64_t V, const char* who) {
+  if (N < 0 || N > ((int64_t)1 << 31)) return fail(NAYLIS_ERR_ARG, "%s: bad row count N=%lld", who, (long long)N);
+  if (V < 2048 || V % 2048 != 0 || V > (1 << 24))
+    return fail(NAYLIS_ERR_ARG, "%s: vocabulary %lld must be a multiple of 2048 up to 2^24", who, (long long)V);
+  return NAYLIS_OK;
+}
+
+int naylis_mom_xent_fwd(const void* logits, const int64_t* labels, float* loss_rows, float* lse, int64_t N, int64_t V,
+                        int64_t ignore_index, void* stream) {
+  int rc = check_xent(N, V, "mom_xent_fwd");
+  if (rc || N == 0) return rc;
+  if (!logits || !labels || !loss_rows || !lse) return fail(NAYLIS_ERR_ARG, "mom_xent_fwd: null pointer argument");
+  if (!aligned16(logits)) return fail(NAYLIS_ERR_ARG, "mom_xent_fwd: logits must be 16-byte aligned");
+  return hip_status(launch_xent(logits, labels, loss_rows, lse, nullptr, 0, nullptr, false, (long)N, (int)V,
+                                (long)ignore_index, (hipStream_t)stream),
+                    "mom_xent_fwd");
+}
+
+int naylis_mom_xent_bwd(const void* logits, const int64_t* labels, const float* lse, const float* grad_rows,
+                        int64_t grad_stride, void* dlogits, int64_t N, int64_t V, int64_t ignore_index, void* stream) {
+  int rc = check_xent(N, V, "mom_xent_bwd");
+  if (rc || N == 0) return rc;
+  if (grad_stride != 0 && grad_stride != 1)
+    return fail(NAYLIS_ERR_ARG, "mom_xent_bwd: grad_stride %lld must be 0 or 1", (long long)grad_stride);
+  if (!logits || !labels || !lse || !grad_rows || !dlogits)
+    return fail(NAYLIS_ERR_ARG, "mom_xent_bwd: null pointer argument");
+  if (!aligned16(logits) || !aligned16(dlogits))
+    return fail(NAYLIS_ERR_ARG, "mom_xent_bwd: logits and dlogits must be 16-byte aligned");
+  return hip_status(launch_xent(logits, labels, nullptr, const_cast<float*>(lse), grad_rows, (long)grad_stride,
+                                dlogits, true, (long)N, (int)V, (long)ignore_index, (hipStream_t)stream),
+                    "mom_xent_bwd");
+}
+
 size_t naylis_mom_router_stats_workspace_bytes(int64_t N, int64_t E) {
   if (N < 0 || N > ((int64_t)1 << 30) || E < 1 || E > NAYLIS_ROUTER_MAX_BLOCKS) return 0;
   return router_stats_ws_bytes((long)N, (int)E);

@@ -77,6 +77,12 @@ hipError_t launch_rope(const void* q, const void* k, const void* cs, const void*
 hipError_t launch_swiglu(const void* g, const void* u, const void* dh, void* h_or_dg, void* du, bool bf16, bool bwd,
                          long n, hipStream_t st);
 
+// Cross-entropy of the LM head (xent.hip): bf16 logits (N, V), V a multiple of
+// 2048; forward writes per-row loss and log-sum-exp, backward the bf16
+// gradient scaled by g[row * g_stride].
+hipError_t launch_xent(const void* logits, const int64_t* labels, float* loss, float* lse, const float* g,
+                       long g_stride, void* dlogits, bool bwd, long N, int V, long ignore_index, hipStream_t st);
+
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }

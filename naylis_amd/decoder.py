@@ -18,8 +18,9 @@ There is no eager MoM path: off ROCm the MoM layers raise.  The norms
 RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
 when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise;
 the attention applies the rotary embedding with the library's fused kernel
-(``NaylisAttention``, same parameters and SDPA backend) and the MLP its fused
-SwiGLU (``NaylisMLP``).
+(``NaylisAttention``, same parameters and SDPA backend), the MLP its fused
+SwiGLU (``NaylisMLP``), and the LM loss reads the bf16 logits once
+(``cross_entropy_rows``) when the vocabulary is a multiple of 2048.
 """
 from __future__ import annotations
 
@@ -35,6 +36,7 @@ from .layer import MoMLayer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm
 from .mom_kernels.hip_mlp import NaylisMLP
 from .mom_kernels.hip_rope import NaylisAttention
+from .mom_kernels.hip_xent import cross_entropy_rows, xent_supported
 
 __all__ = ["naylis_config", "NaylisDecoderLayer", "NaylisLlamaModel", "NaylisLlamaForCausalLM",
            "cast_for_training"]
@@ -180,7 +182,11 @@ class NaylisLlamaForCausalLM(LlamaForCausalLM):
         shift_h = h[:, :-1, :].contiguous()
         shift_labels = labels[:, 1:].contiguous().view(-1)
         logits = self.lm_head(shift_h).view(-1, self.config.vocab_size)
-        loss = F.cross_entropy(logits.float(), shift_labels, reduction="sum")
+        if xent_supported(logits, shift_labels):
+            # the library's one-pass loss over the bf16 logits (same sum as below)
+            loss = cross_entropy_rows(logits, shift_labels).sum()
+        else:
+            loss = F.cross_entropy(logits.float(), shift_labels, reduction="sum")
         if num_items_in_batch is not None:
             loss = loss / num_items_in_batch
         else:

@@ -226,3 +226,11 @@ def test_swiglu_rejects_bad_arguments(lib):
     assert lib.naylis_mom_swiglu_fwd(p + 4, p, p, 1, 16, None) == _lib.NAYLIS_ERR_ARG      # alignment
     assert lib.naylis_mom_swiglu_bwd(p, p, None, p, p, 1, 16, None) == _lib.NAYLIS_ERR_ARG
     assert lib.naylis_mom_swiglu_fwd(None, None, None, 1, 0, None) == _lib.NAYLIS_OK
+
+
+def test_xent_rejects_bad_arguments(lib):
+    p = 0x1000
+    assert lib.naylis_mom_xent_fwd(p, p, p, p, 8, 1000, -100, None) == _lib.NAYLIS_ERR_ARG          # V % 2048
+    assert lib.naylis_mom_xent_fwd(p + 2, p, p, p, 8, 2048, -100, None) == _lib.NAYLIS_ERR_ARG      # alignment
+    assert lib.naylis_mom_xent_bwd(p, p, p, p, 2, p, 8, 2048, -100, None) == _lib.NAYLIS_ERR_ARG     # grad stride
+    assert lib.naylis_mom_xent_fwd(None, None, None, None, 0, 2048, -100, None) == _lib.NAYLIS_OK

@@ -123,10 +123,13 @@ def _oracle_grads(cfg, state, ids, dtype, routing):
 
 
 def _tiny_gpu_model(dev, d_model=256, **over):
-    """d_model 256 keeps transformers' LlamaRMSNorm, 512 uses the fused norm."""
+    """d_model 256 keeps transformers' LlamaRMSNorm and torch's cross-entropy
+    (vocabulary 256); 512 uses the fused norm and the fused loss (vocabulary
+    2048)."""
     torch.manual_seed(0)
     cfg = naylis_config(**dict(TINY, d_model=d_model, n_heads=d_model // 64, intermediate_size=2 * d_model,
-                               mem_size=256, mom_block_size=64, mom_router_rank=16, **over))
+                               mem_size=256, mom_block_size=64, mom_router_rank=16,
+                               vocab_size=256 if d_model == 256 else 2048, **over))
     model = NaylisLlamaForCausalLM(cfg)
     with torch.no_grad():
         for layer in model.model.layers:
