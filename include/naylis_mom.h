@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 9
+#define NAYLIS_MOM_ABI_VERSION 10
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -195,6 +195,17 @@ size_t naylis_mom_rmsnorm_workspace_bytes(int64_t N, int64_t D);
 int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const float* rstd, const void* dy, void* dx,
                            void* dweight, void* workspace, size_t workspace_bytes, int64_t N, int64_t D,
                            void* stream);
+/* The residual add that precedes every norm of the decoder block, fused:
+ * s = x + dtype(a) (a in the stream's dtype or fp32 — the ReZero output is
+ * fp32) is written to s_out and y = RMSNorm(s).  The backward takes the
+ * gradient arriving at s from the residual stream (dres, may be NULL) and
+ * writes ds = dres + the norm's input gradient (one rounding), which is the
+ * gradient of both x and a. */
+int naylis_mom_add_rmsnorm_fwd(const void* x, const void* a, int a_dtype, const void* weight, void* s_out, void* y,
+                               float* rstd, int dtype, int64_t N, int64_t D, float eps, void* stream);
+int naylis_mom_add_rmsnorm_bwd(const void* s, const void* weight, const float* rstd, const void* dy, const void* dres,
+                               void* ds, void* dweight, void* workspace, size_t workspace_bytes, int dtype, int64_t N,
+                               int64_t D, void* stream);
 
 /* ---------------------------------------------------------------- RoPE ---
  * Rotary position embedding of the decoder attention's q and k

@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -47,6 +47,9 @@ SIGNATURES = {
     "naylis_mom_rmsnorm_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _float,
                                       _c_void_p]),
     "naylis_mom_rmsnorm_workspace_bytes": (_size_t, [_i64] * 2),
+    "naylis_mom_add_rmsnorm_fwd": (_int, [_c_void_p, _c_void_p, _int] + [_c_void_p] * 4 + [_int, _i64, _i64, _float,
+                                                                                          _c_void_p]),
+    "naylis_mom_add_rmsnorm_bwd": (_int, [_c_void_p] * 8 + [_size_t, _int, _i64, _i64, _c_void_p]),
     "naylis_mom_rope": (_int, [_c_void_p] * 6 + [_int, _int] + [_i64] * 5 + [_c_void_p]),
     "naylis_mom_swiglu_fwd": (_int, [_c_void_p] * 3 + [_int, _i64, _c_void_p]),
     "naylis_mom_xent_fwd": (_int, [_c_void_p] * 4 + [_i64] * 3 + [_c_void_p]),

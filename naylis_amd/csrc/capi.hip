@@ -344,9 +344,47 @@ int naylis_mom_rmsnorm_bwd(const void* x, int dtype, const void* weight, const f
   if (workspace_bytes < need)
     return fail(NAYLIS_ERR_WORKSPACE, "mom_rmsnorm_bwd: workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
-  return hip_status(launch_rmsnorm_bwd(x, dtype == NAYLIS_DTYPE_BF16, weight, rstd, dy, dx, dweight, workspace,
-                                       (long)N, (int)D, (hipStream_t)stream),
+  return hip_status(launch_rmsnorm_bwd(x, dtype == NAYLIS_DTYPE_BF16, weight, rstd, dy, nullptr, dx, dweight,
+                                       workspace, (long)N, (int)D, (hipStream_t)stream),
                     "mom_rmsnorm_bwd");
+}
+
+int naylis_mom_add_rmsnorm_fwd(const void* x, const void* a, int a_dtype, const void* weight, void* s_out, void* y,
+                               float* rstd, int dtype, int64_t N, int64_t D, float eps, void* stream) {
+  int rc = check_norm(dtype, N, D, "mom_add_rmsnorm_fwd");
+  if (rc) return rc;
+  if ((rc = check_dtype(a_dtype, "mom_add_rmsnorm_fwd"))) return rc;
+  if (dtype == NAYLIS_DTYPE_F32 && a_dtype != NAYLIS_DTYPE_F32)
+    return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_fwd: an fp32 stream takes an fp32 residual branch");
+  if (!(eps >= 0.f) || eps > 1.f)
+    return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_fwd: eps %g must be in [0, 1]", (double)eps);
+  if (N == 0) return NAYLIS_OK;
+  if (!x || !a || !weight || !s_out || !y || !rstd)
+    return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_fwd: null pointer argument");
+  if (!aligned16(x) || !aligned16(a) || !aligned16(weight) || !aligned16(s_out) || !aligned16(y))
+    return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_fwd: x, a, weight, s_out and y must be 16-byte aligned");
+  return hip_status(launch_add_rmsnorm_fwd(x, a, a_dtype == NAYLIS_DTYPE_F32, dtype == NAYLIS_DTYPE_BF16, weight,
+                                           s_out, y, rstd, (long)N, (int)D, eps, (hipStream_t)stream),
+                    "mom_add_rmsnorm_fwd");
+}
+
+int naylis_mom_add_rmsnorm_bwd(const void* s, const void* weight, const float* rstd, const void* dy, const void* dres,
+                               void* ds, void* dweight, void* workspace, size_t workspace_bytes, int dtype, int64_t N,
+                               int64_t D, void* stream) {
+  int rc = check_norm(dtype, N, D, "mom_add_rmsnorm_bwd");
+  if (rc) return rc;
+  if (!weight || !dweight || !workspace) return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_bwd: null pointer argument");
+  if (N > 0 && (!s || !rstd || !dy || !ds)) return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_bwd: null pointer argument");
+  if (N > 0 && (!aligned16(s) || !aligned16(weight) || !aligned16(dy) || !aligned16(ds) ||
+                (dres && !aligned16(dres))))
+    return fail(NAYLIS_ERR_ARG, "mom_add_rmsnorm_bwd: s, weight, dy, dres and ds must be 16-byte aligned");
+  const size_t need = rmsnorm_ws_bytes((long)N, (int)D);
+  if (workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_add_rmsnorm_bwd: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  return hip_status(launch_rmsnorm_bwd(s, dtype == NAYLIS_DTYPE_BF16, weight, rstd, dy, dres, ds, dweight, workspace,
+                                       (long)N, (int)D, (hipStream_t)stream),
+                    "mom_add_rmsnorm_bwd");
 }
 
 int naylis_mom_rope(const void* q, const void* k, const void* cos, const void* sin, void* q_out, void* k_out,

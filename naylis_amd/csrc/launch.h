@@ -63,8 +63,12 @@ int rmsnorm_bwd_parts(long N);
 size_t rmsnorm_ws_bytes(long N, int D);
 hipError_t launch_rmsnorm_fwd(const void* x, bool bf16, const void* w, void* y, float* rstd, long N, int D,
                               float eps, hipStream_t st);
-hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy, void* dx,
-                              void* dw, void* ws, long N, int D, hipStream_t st);
+// add variant: s = x + T(a) (a bf16 or fp32) written to s_out, then y = norm(s)
+hipError_t launch_add_rmsnorm_fwd(const void* x, const void* a, bool a_f32, bool bf16, const void* w, void* s_out,
+                                  void* y, float* rstd, long N, int D, float eps, hipStream_t st);
+// dres (may be null) is added to dx
+hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy,
+                              const void* dres, void* dx, void* dw, void* ws, long N, int D, hipStream_t st);
 
 // Rotary position embedding of q and k (rope.hip): x (B, S, H, HD) for HD in
 // {32, 64, 128}, cos / sin (cos_batch, S, HD) with cos_batch 1 or B; bwd applies

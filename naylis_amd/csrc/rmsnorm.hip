@@ -11,6 +11,8 @@
 // a fixed grid (a function of N only), keeps the weight-gradient partial of
 // its rows in registers, sums the four waves of a workgroup in order and the
 // workgroups in order in a second launch: deterministic.
+#include <type_traits>
+
 #include "common.h"
 #include "timing.h"
 
@@ -67,25 +69,47 @@ __device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
 
 constexpr int kNormBwdWgs = 512;  // workgroups of the backward (fewer when N is small)
 
-template <typename T, int CH>
-__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
+// AT: dtype of the residual branch a (void: no add).  With a, the row is
+// first s = x + T(a) (the residual add of the decoder block, a rounded to
+// the stream's dtype first), written to s_out, and s is normalised.
+template <typename T, typename AT, int CH>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x, const AT* __restrict__ a,
+                                                          const T* __restrict__ w, T* __restrict__ s_out,
                                                           T* __restrict__ y, float* __restrict__ rstd, long N, int D,
                                                           float eps) {
+  constexpr bool ADD = !std::is_same<AT, void>::value;
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= N) return;
   const T* xr = x + row * D;
   Chunk<T> xc[CH], wc[CH];
+  float xv[CH][8];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     xc[c].load(xr + (c * 64 + lane) * 8);
     wc[c].load(w + (c * 64 + lane) * 8);
   }
+  if constexpr (ADD) {
+    Chunk<AT> ac[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) ac[c].load(a + row * D + (c * 64 + lane) * 8);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[c][e] = round_to<T>(add_rn(xc[c].get(e), round_to<T>(ac[c].get(e))));
+      store8(s_out + row * D + (c * 64 + lane) * 8, xv[c]);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[c][e] = xc[c].get(e);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(xc[c].get(e), xc[c].get(e), ss);
+    for (int e = 0; e < 8; ++e) ss = fmaf(xv[c][e], xv[c][e], ss);
   ss = wave_allsum(ss);
   const float r = rsqrtf(add_rn(mul_rn(ss, 1.0f / (float)D), eps));
   T* yr = y + row * D;
@@ -93,17 +117,19 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
   for (int c = 0; c < CH; ++c) {
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = mul_rn(wc[c].get(e), round_to<T>(mul_rn(xc[c].get(e), r)));
+    for (int e = 0; e < 8; ++e) v[e] = mul_rn(wc[c].get(e), round_to<T>(mul_rn(xv[c][e], r)));
     store8(yr + (c * 64 + lane) * 8, v);
   }
   if (lane == 0) rstd[row] = r;
 }
 
+// dres (optional): gradient arriving at x from elsewhere (the residual
+// stream), added to the norm's input gradient before the one rounding
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
                                                           const float* __restrict__ rstd, const T* __restrict__ dy,
-                                                          T* __restrict__ dx, float* __restrict__ dw_part, long N,
-                                                          int D) {
+                                                          const T* __restrict__ dres, T* __restrict__ dx,
+                                                          float* __restrict__ dw_part, long N, int D) {
   __shared__ float red[3][CH * 512];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const long stride = (long)gridDim.x * 4;
@@ -136,12 +162,20 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
         m = fmaf(dh[c][e], h[c][e], m);
       }
     m = wave_allsum(m) * (1.0f / (float)D);
-    // dx = r (dh - h mean(dh h))
+    // dx = r (dh - h mean(dh h)) (+ dres)
+    Chunk<T> rc[CH];
+    if (dres != nullptr) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) rc[c].load(dres + row * D + (c * 64 + lane) * 8);
+    }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = r * fmaf(-h[c][e], m, dh[c][e]);
+      for (int e = 0; e < 8; ++e) {
+        v[e] = r * fmaf(-h[c][e], m, dh[c][e]);
+        if (dres != nullptr) v[e] += rc[c].get(e);
+      }
       store8(dx + row * D + (c * 64 + lane) * 8, v);
     }
   }
@@ -215,16 +249,18 @@ int rmsnorm_bwd_parts(long N) {
 
 size_t rmsnorm_ws_bytes(long N, int D) { return (size_t)rmsnorm_bwd_parts(N) * D * sizeof(float); }
 
-template <typename T>
-static hipError_t fwd_t(const void* x, const void* w, void* y, float* rstd, long N, int D, float eps,
-                        hipStream_t st) {
+template <typename T, typename AT>
+static hipError_t fwd_t(const void* x, const void* a, const void* w, void* s_out, void* y, float* rstd, long N, int D,
+                        float eps, hipStream_t st) {
   const dim3 grid((unsigned)((N + 3) / 4));
   const int ch = D / 512;
+  constexpr bool kAdd = !std::is_same<AT, void>::value;
+  const char* kname = kAdd ? "add_rmsnorm_fwd" : "rmsnorm_fwd";
 #define NAYLIS_NORM_FWD(C)                                                                                    \
   case C:                                                                                                     \
-    NAYLIS_TIMED("rmsnorm_fwd", st,                                                                           \
-                 hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, C>), grid, dim3(256), 0, st, (const T*)x, (const T*)w, \
-                                    (T*)y, rstd, N, D, eps));                                                 \
+    NAYLIS_TIMED(kname, st,                                                                                   \
+                 hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, AT, C>), grid, dim3(256), 0, st, (const T*)x,      \
+                                    (const AT*)a, (const T*)w, (T*)s_out, (T*)y, rstd, N, D, eps));           \
     break;
   switch (ch) {
     NAYLIS_NORM_FWD(1)
@@ -243,15 +279,15 @@ static hipError_t fwd_t(const void* x, const void* w, void* y, float* rstd, long
 }
 
 template <typename T>
-static hipError_t bwd_t(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw,
-                        float* part, long N, int D, hipStream_t st) {
+static hipError_t bwd_t(const void* x, const void* w, const float* rstd, const void* dy, const void* dres, void* dx,
+                        void* dw, float* part, long N, int D, hipStream_t st) {
   const int parts = rmsnorm_bwd_parts(N);
   const int ch = D / 512;
 #define NAYLIS_NORM_BWD(C)                                                                                     \
   case C:                                                                                                      \
     NAYLIS_TIMED("rmsnorm_bwd", st,                                                                            \
                  hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, C>), dim3(parts), dim3(256), 0, st, (const T*)x,    \
-                                    (const T*)w, rstd, (const T*)dy, (T*)dx, part, N, D));                     \
+                                    (const T*)w, rstd, (const T*)dy, (const T*)dres, (T*)dx, part, N, D));     \
     break;
   switch (ch) {
     NAYLIS_NORM_BWD(1)
@@ -275,11 +311,21 @@ static hipError_t bwd_t(const void* x, const void* w, const float* rstd, const v
 hipError_t launch_rmsnorm_fwd(const void* x, bool bf16, const void* w, void* y, float* rstd, long N, int D,
                               float eps, hipStream_t st) {
   if (N == 0) return hipSuccess;
-  return bf16 ? fwd_t<bf16_t>(x, w, y, rstd, N, D, eps, st) : fwd_t<float>(x, w, y, rstd, N, D, eps, st);
+  return bf16 ? fwd_t<bf16_t, void>(x, nullptr, w, nullptr, y, rstd, N, D, eps, st)
+              : fwd_t<float, void>(x, nullptr, w, nullptr, y, rstd, N, D, eps, st);
 }
 
-hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy, void* dx,
-                              void* dw, void* ws, long N, int D, hipStream_t st) {
+hipError_t launch_add_rmsnorm_fwd(const void* x, const void* a, bool a_f32, bool bf16, const void* w, void* s_out,
+                                  void* y, float* rstd, long N, int D, float eps, hipStream_t st) {
+  if (N == 0) return hipSuccess;
+  if (bf16)
+    return a_f32 ? fwd_t<bf16_t, float>(x, a, w, s_out, y, rstd, N, D, eps, st)
+                 : fwd_t<bf16_t, bf16_t>(x, a, w, s_out, y, rstd, N, D, eps, st);
+  return fwd_t<float, float>(x, a, w, s_out, y, rstd, N, D, eps, st);
+}
+
+hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const float* rstd, const void* dy,
+                              const void* dres, void* dx, void* dw, void* ws, long N, int D, hipStream_t st) {
   float* part = (float*)ws;
   if (N == 0) {
     // no rows: dw = 0 (the reduction over zero partials)
@@ -291,8 +337,8 @@ hipError_t launch_rmsnorm_bwd(const void* x, bool bf16, const void* w, const flo
                          (float*)dw, 0, D);
     return hipGetLastError();
   }
-  return bf16 ? bwd_t<bf16_t>(x, w, rstd, dy, dx, dw, part, N, D, st)
-              : bwd_t<float>(x, w, rstd, dy, dx, dw, part, N, D, st);
+  return bf16 ? bwd_t<bf16_t>(x, w, rstd, dy, dres, dx, dw, part, N, D, st)
+              : bwd_t<float>(x, w, rstd, dy, dres, dx, dw, part, N, D, st);
 }
 
 }  // namespace naylis

@@ -33,7 +33,7 @@ from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaFo
                                                       LlamaRMSNorm)
 
 from .layer import MoMLayer, mom_aux_loss
-from .mom_kernels.hip_norm import NaylisRMSNorm
+from .mom_kernels.hip_norm import NaylisRMSNorm, add_rms_norm
 from .mom_kernels.hip_mlp import NaylisMLP
 from .mom_kernels.hip_rope import NaylisAttention
 from .mom_kernels.hip_xent import cross_entropy_rows, xent_supported
@@ -83,6 +83,12 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
     With ``mom_grad_ckpt`` the attention and the MLP run in checkpoint
     regions (no RNG inside either, so the recompute is exact) and the MoM
     layer checkpoints its read.
+
+    Every residual add is followed by a norm (the next sub-block's, or the
+    next layer's ``input_layernorm``, or the final norm), so the layer hands
+    its MLP output on un-added (``pending``) and each add runs fused with the
+    norm after it (``add_rms_norm``): forward(h, M, pos, pending) returns
+    (h, mlp_out); h + mlp_out is the reference layer's output.
     """
 
     def __init__(self, config, layer_idx, mem_size, mom_block_size, mom_top_blocks, mom_router_rank,
@@ -103,18 +109,21 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
             return torch.utils.checkpoint.checkpoint(fn, *tensors, use_reentrant=False, preserve_rng_state=False)
         return fn(*tensors)
 
-    def forward(self, hidden_states, M_blocks=None, position_embeddings=None, **kwargs):
+    def forward(self, hidden_states, M_blocks=None, position_embeddings=None, pending=None, **kwargs):
         if M_blocks is None:
             raise ValueError("M_blocks is required: the MoM layer cannot run without the shared memory bank")
         h = hidden_states
+        if pending is None:
+            x = self.input_layernorm(h)
+        else:
+            h, x = add_rms_norm(h, pending, self.input_layernorm)
         a = self._maybe_ckpt(lambda t: self.self_attn(hidden_states=t, position_embeddings=position_embeddings,
-                                                      **kwargs)[0], self.input_layernorm(h))
-        h = h + a
-        # the ReZero product promotes to the fp32 scale's dtype; the residual
-        # stream keeps its own (bf16 in bf16 training, fp32 under autocast)
-        h = h + self.mom(self.mom_norm(h), M_blocks).to(h.dtype)
-        h = h + self._maybe_ckpt(self.mlp, self.post_attention_layernorm(h))
-        return h
+                                                      **kwargs)[0], x)
+        h, x = add_rms_norm(h, a, self.mom_norm)
+        # the ReZero product promotes to the fp32 scale's dtype; the add rounds
+        # it to the residual stream's (bf16 in bf16 training, fp32 under autocast)
+        h, x = add_rms_norm(h, self.mom(x, M_blocks), self.post_attention_layernorm)
+        return h, self._maybe_ckpt(self.mlp, x)
 
 
 class NaylisLlamaModel(LlamaModel):
@@ -139,9 +148,12 @@ class NaylisLlamaModel(LlamaModel):
         if position_ids is None:
             position_ids = torch.arange(S, device=h.device).unsqueeze(0).expand(B, -1)
         pos = self.rotary_emb(h, position_ids)
+        pending = None
         for layer in self.layers:
-            h = layer(h, M_blocks=self.M_blocks, position_embeddings=pos, attention_mask=attention_mask, **kwargs)
-        return BaseModelOutputWithPast(last_hidden_state=self.norm(h))
+            h, pending = layer(h, M_blocks=self.M_blocks, position_embeddings=pos, pending=pending,
+                               attention_mask=attention_mask, **kwargs)
+        out = self.norm(h) if pending is None else add_rms_norm(h, pending, self.norm)[1]
+        return BaseModelOutputWithPast(last_hidden_state=out)
 
 
 class NaylisLlamaForCausalLM(LlamaForCausalLM):

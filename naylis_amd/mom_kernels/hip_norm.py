@@ -83,3 +83,58 @@ class NaylisRMSNorm(nn.Module):
 
     def extra_repr(self):
         return f"{tuple(self.weight.shape)}, eps={self.variance_epsilon}"
+
+
+class AddRMSNormFunction(torch.autograd.Function):
+    """(s, y) = (x + a.to(x.dtype), RMSNorm(s)) in one pass each way."""
+
+    @staticmethod
+    def forward(ctx, x, a, weight, eps):
+        lib = _lib.load()
+        D = x.shape[-1]
+        x2 = x.contiguous().view(-1, D)
+        a2 = a.contiguous().view(-1, D)
+        N = x2.shape[0]
+        dev = x.device
+        s = torch.empty_like(x2)
+        y = torch.empty_like(x2)
+        rstd = torch.empty(N, device=dev, dtype=torch.float32)
+        with _lib.on_device(dev):
+            _lib.check(lib.naylis_mom_add_rmsnorm_fwd(x2.data_ptr(), a2.data_ptr(), _DT[a.dtype], weight.data_ptr(),
+                                                      s.data_ptr(), y.data_ptr(), rstd.data_ptr(), _DT[x.dtype], N, D,
+                                                      float(eps), _lib.stream_of(dev)))
+        ctx.save_for_backward(s, weight, rstd)
+        ctx.shape = x.shape
+        return s.view(x.shape), y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, ds_out, dy):
+        lib = _lib.load()
+        s, weight, rstd = ctx.saved_tensors
+        N, D = s.shape
+        dev = s.device
+        if dy is None:
+            dy = torch.zeros_like(s)
+        dy2 = dy.to(s.dtype).contiguous().view(N, D)
+        dres = ds_out.to(s.dtype).contiguous().view(N, D) if ds_out is not None else None
+        ds = torch.empty_like(s)
+        dw = torch.empty_like(weight)
+        ws = torch.empty(max(lib.naylis_mom_rmsnorm_workspace_bytes(N, D), 1), dtype=torch.uint8, device=dev)
+        with _lib.on_device(dev):
+            _lib.check(lib.naylis_mom_add_rmsnorm_bwd(s.data_ptr(), weight.data_ptr(), rstd.data_ptr(), dy2.data_ptr(),
+                                                      dres.data_ptr() if dres is not None else None, ds.data_ptr(),
+                                                      dw.data_ptr(), ws.data_ptr(), ws.numel(), _DT[s.dtype], N, D,
+                                                      _lib.stream_of(dev)))
+        ds = ds.view(ctx.shape)
+        return ds, ds, dw, None
+
+
+def add_rms_norm(x, a, norm):
+    """Residual add followed by ``norm``: returns (s, norm(s)) with
+    s = x + a.to(x.dtype).  One fused pass when ``norm`` is a NaylisRMSNorm and
+    the kernels apply (a in x's dtype or fp32), else the two torch steps."""
+    if (isinstance(norm, NaylisRMSNorm) and rmsnorm_supported(x, norm.weight) and a.shape == x.shape
+            and a.device == x.device and (a.dtype == x.dtype or a.dtype == torch.float32)):
+        return AddRMSNormFunction.apply(x, a, norm.weight, float(norm.variance_epsilon))
+    s = x + a.to(x.dtype)
+    return s, norm(s)

@@ -234,3 +234,11 @@ def test_xent_rejects_bad_arguments(lib):
     assert lib.naylis_mom_xent_fwd(p + 2, p, p, p, 8, 2048, -100, None) == _lib.NAYLIS_ERR_ARG      # alignment
     assert lib.naylis_mom_xent_bwd(p, p, p, p, 2, p, 8, 2048, -100, None) == _lib.NAYLIS_ERR_ARG     # grad stride
     assert lib.naylis_mom_xent_fwd(None, None, None, None, 0, 2048, -100, None) == _lib.NAYLIS_OK
+
+
+def test_add_rmsnorm_rejects_bad_arguments(lib):
+    p = 0x1000
+    # fp32 stream with a bf16 residual branch
+    assert lib.naylis_mom_add_rmsnorm_fwd(p, p, 1, p, p, p, p, 0, 8, 1024, 1e-5, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_add_rmsnorm_fwd(p, p, 0, p, p, p, p, 1, 8, 1000, 1e-5, None) == _lib.NAYLIS_ERR_ARG  # D
+    assert lib.naylis_mom_add_rmsnorm_bwd(p, p, p, p, None, p, p, p, 0, 1, 8, 1024, None) == _lib.NAYLIS_ERR_WORKSPACE

@@ -79,3 +79,31 @@ def test_rmsnorm_rejects_unsupported(dev):
     w = torch.ones(1000, device=dev)
     with pytest.raises(RuntimeError, match="multiple of 512"):
         rms_norm(torch.randn(4, 1000, device=dev), w)
+
+
+@pytest.mark.parametrize("a_dtype", [torch.bfloat16, torch.float32])
+def test_add_rmsnorm_matches_add_then_norm(a_dtype, dev):
+    """s = x + a.to(x.dtype); y = norm(s) fused, against the two torch steps
+    the decoder block would run (model.py:330-345), forward and backward."""
+    from naylis_amd.mom_kernels.hip_norm import add_rms_norm
+    ref, got = _pair(1024, torch.bfloat16, dev, seed=9)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4096, 1024, generator=g).bfloat16().to(dev)
+    a = torch.randn(4096, 1024, generator=g).to(a_dtype).to(dev)
+    ds = torch.randn(4096, 1024, generator=g).bfloat16().to(dev)
+    dy = torch.randn(4096, 1024, generator=g).bfloat16().to(dev)
+    xr, ar = x.clone().requires_grad_(True), a.clone().requires_grad_(True)
+    sr = xr + ar.to(torch.bfloat16)
+    yr = ref(sr)
+    torch.autograd.backward((sr, yr), (ds, dy))
+    xg, ag = x.clone().requires_grad_(True), a.clone().requires_grad_(True)
+    sg, yg = add_rms_norm(xg, ag, got)
+    torch.autograd.backward((sg, yg), (ds, dy))
+    torch.cuda.synchronize()
+    assert torch.equal(sg, sr)                                   # the add rounds like torch's
+    two_ulp = (yr.float().abs() * 2.0 ** -6).clamp_min(1e-30)
+    assert bool(((yg.float() - yr.float()).abs() <= two_ulp).all())
+    # torch rounds the norm's input gradient to bf16 before adding ds; the kernel adds first
+    assert _rel(xg.grad, xr.grad) <= 1e-2 and _rel(ag.grad, ar.grad) <= 1e-2
+    assert ag.grad.dtype == a_dtype
+    assert _rel(got.weight.grad, ref.weight.grad) <= 1e-2
