@@ -19,8 +19,10 @@ RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
 when the hidden size is a multiple of 512 up to 4096, LlamaRMSNorm otherwise;
 the attention applies the rotary embedding with the library's fused kernel
 (``NaylisAttention``, same parameters and SDPA backend), the MLP its fused
-SwiGLU (``NaylisMLP``), and the LM loss reads the bf16 logits once
-(``cross_entropy_rows``) when the vocabulary is a multiple of 2048.
+SwiGLU (``NaylisMLP``), the bias-free projections of both take their
+weight gradient from the library's split-K GEMM (``use_library_wgrad``), and
+the LM loss reads the bf16 logits once (``cross_entropy_rows``) when the
+vocabulary is a multiple of 2048.
 """
 from __future__ import annotations
 
@@ -34,6 +36,7 @@ from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaFo
 
 from .layer import MoMLayer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm, add_rms_norm
+from .mom_kernels.hip_linear import use_library_wgrad
 from .mom_kernels.hip_mlp import NaylisMLP
 from .mom_kernels.hip_rope import NaylisAttention
 from .mom_kernels.hip_xent import cross_entropy_rows, xent_supported
@@ -94,8 +97,8 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
     def __init__(self, config, layer_idx, mem_size, mom_block_size, mom_top_blocks, mom_router_rank,
                  mom_grad_ckpt=False):
         super().__init__(config, layer_idx)
-        self.self_attn = NaylisAttention(config, layer_idx)
-        self.mlp = NaylisMLP(config)
+        self.self_attn = use_library_wgrad(NaylisAttention(config, layer_idx))
+        self.mlp = use_library_wgrad(NaylisMLP(config))
         self.input_layernorm = _norm(config)
         self.post_attention_layernorm = _norm(config)
         self.mom_norm = _norm(config)

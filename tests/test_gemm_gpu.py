@@ -7,6 +7,8 @@ Tolerance: |got - ref| <= 2e-2 |ref| + 2e-3 max(1, max|ref|) (a sum over up to
 16384 tokens has magnitudes >> 1; the atol scales with it as for the other
 parameter gradients); results must be bitwise reproducible.
 """
+import copy
+
 import pytest
 import torch
 
@@ -73,3 +75,37 @@ def test_mom_linear_autograd_matches_torch(dev):
     assert_close(y, yr, "y")
     assert_close(x.grad, xr.grad, "dx")
     assert_close(w.grad, wr.grad, "dW", atol=2e-3 * max(1.0, float(wr.grad.abs().max())))
+
+
+def test_naylis_linear_module_swap(dev):
+    """use_library_wgrad turns the bias-free nn.Linear of a block into
+    NaylisLinear in place: same parameters and keys, the same forward and
+    input gradient as nn.Linear, the weight gradient from the library (to the
+    bf16 GEMM bound); a biased Linear is left alone."""
+    from naylis_amd.mom_kernels.hip_linear import NaylisLinear, use_library_wgrad
+    torch.manual_seed(7)
+    block = torch.nn.Sequential(torch.nn.Linear(256, 704, bias=False), torch.nn.Linear(704, 256, bias=True))
+    block = block.to(dev, torch.bfloat16)
+    ref = copy.deepcopy(block)
+    keys = list(block.state_dict())
+    use_library_wgrad(block)
+    assert type(block[0]) is NaylisLinear and type(block[1]) is torch.nn.Linear
+    assert list(block.state_dict()) == keys
+    x = torch.randn(2, 512, 256, device=dev, dtype=torch.bfloat16)
+    dy = torch.randn(2, 512, 256, device=dev, dtype=torch.bfloat16)
+    xa, xb = x.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    ya = block(xa)
+    ya.backward(dy)
+    hb = ref[0](xb)
+    hb.retain_grad()
+    yb = ref[1](hb)
+    yb.backward(dy)
+    assert torch.equal(ya, yb)
+    assert_close(xa.grad, xb.grad, "dx")
+    # the first layer's exact weight gradient from the bf16 gradient reaching it
+    gw = torch.mm(hb.grad.reshape(-1, 704).float().t(), x.reshape(-1, 256).float())
+    # bf16 output rounding (half an ulp, at most 2^-8 relative) plus the accumulation
+    tol = 2.0 ** -8 * gw.abs() + 2e-3 * max(1.0, float(gw.abs().max()))
+    assert bool(((block[0].weight.grad.float() - gw).abs() <= tol).all())
+    assert bool(((ref[0].weight.grad.float() - gw).abs() <= tol).all())
+    assert_close(block[1].weight.grad, ref[1].weight.grad, "dW (nn.Linear)")
