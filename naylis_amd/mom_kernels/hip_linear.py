@@ -25,6 +25,21 @@ from .. import _lib
 _DT = {torch.float32: 0, torch.bfloat16: 1}
 
 
+def _library_wgrad(x2, dy2, weight):
+    """dW = dy2^T x2 (rows = tokens) on the library's split-K GEMM."""
+    lib = _lib.load()
+    D_out, D_in = weight.shape
+    N = x2.shape[0]
+    dev = x2.device
+    ws = torch.empty(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), device=dev, dtype=torch.uint8)
+    dw = torch.empty((D_out, D_in), device=dev, dtype=weight.dtype)
+    with _lib.on_device(dev):
+        rc = lib.naylis_mom_linear_wgrad(x2.data_ptr(), dy2.data_ptr(), dw.data_ptr(), _DT[weight.dtype],
+                                         ws.data_ptr(), ws.numel(), N, D_in, D_out, _lib.stream_of(dev))
+    _lib.check(rc)
+    return dw
+
+
 class MomLinearFunction(torch.autograd.Function):
 
     @staticmethod
@@ -42,18 +57,7 @@ class MomLinearFunction(torch.autograd.Function):
             dx = torch.mm(dy2, weight).view(x.shape)
         dw = None
         if ctx.needs_input_grad[1]:
-            lib = _lib.load()
-            x2 = x.reshape(-1, D_in).contiguous()
-            N = x2.shape[0]
-            dev = x.device
-            ws = torch.empty(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), device=dev,
-                             dtype=torch.uint8)
-            dw = torch.empty((D_out, D_in), device=dev, dtype=weight.dtype)
-            with _lib.on_device(dev):
-                rc = lib.naylis_mom_linear_wgrad(x2.data_ptr(), dy2.data_ptr(), dw.data_ptr(), _DT[weight.dtype],
-                                                 ws.data_ptr(), ws.numel(), N, D_in, D_out,
-                                                 _lib.stream_of(dev))
-            _lib.check(rc)
+            dw = _library_wgrad(x.reshape(-1, D_in).contiguous(), dy2, weight)
         return dx, dw
 
 
@@ -67,6 +71,49 @@ def mom_linear(x, weight):
             and weight.requires_grad):
         return MomLinearFunction.apply(x, weight)
     return F.linear(x, weight)
+
+
+def _library_ok(x, weight):
+    D_out, D_in = weight.shape
+    return (x.is_cuda and torch.version.hip is not None and x.dtype == torch.bfloat16
+            and weight.dtype == torch.bfloat16 and weight.device == x.device and D_in % 8 == 0 and D_out % 8 == 0
+            and x.shape[-1] == D_in and (x.numel() // D_in) % 8 == 0)
+
+
+class SharedInputLinearFunction(torch.autograd.Function):
+    """y_i = x W_i^T for several bias-free projections of one input (the
+    attention's q/k/v, the MLP's gate/up).  Autograd would sum their input
+    gradients with separate elementwise adds; here each further product
+    accumulates into the first in the GEMM's epilogue (``addmm_``, one
+    rounding of the sum).  Weight gradients: the library's split-K GEMM."""
+
+    @staticmethod
+    def forward(ctx, x, *weights):
+        ctx.save_for_backward(x, *weights)
+        return tuple(F.linear(x, w) for w in weights)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        x, *weights = ctx.saved_tensors
+        x2 = x.reshape(-1, x.shape[-1]).contiguous() if any(ctx.needs_input_grad[1:]) else None
+        dx, dws = None, []
+        for i, (dy, w) in enumerate(zip(dys, weights)):
+            dy2 = dy.reshape(-1, w.shape[0]).contiguous()
+            if ctx.needs_input_grad[0]:
+                dx = torch.mm(dy2, w) if dx is None else dx.addmm_(dy2, w)
+            dws.append(_library_wgrad(x2, dy2, w) if ctx.needs_input_grad[1 + i] else None)
+        return (dx.view(x.shape) if dx is not None else None, *dws)
+
+
+def shared_input_linear(x, linears):
+    """The outputs of several bias-free linear layers applied to one input,
+    as a tuple.  One autograd node (``SharedInputLinearFunction``) for bf16
+    activations and weights on a ROCm device with dimensions that are
+    multiples of 8; otherwise each layer applied in turn."""
+    if (torch.is_grad_enabled() and all(m.bias is None and _library_ok(x, m.weight) for m in linears)
+            and any(m.weight.requires_grad for m in linears)):
+        return SharedInputLinearFunction.apply(x, *(m.weight for m in linears))
+    return tuple(m(x) for m in linears)
 
 
 class NaylisLinear(nn.Linear):

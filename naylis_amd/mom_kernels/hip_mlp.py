@@ -12,6 +12,7 @@ import torch
 from transformers.models.llama.modeling_llama import LlamaMLP
 
 from .. import _lib
+from .hip_linear import shared_input_linear
 
 _DT = {torch.float32: 0, torch.bfloat16: 1}
 
@@ -63,8 +64,7 @@ class NaylisMLP(LlamaMLP):
     def forward(self, x):
         if self.config.hidden_act != "silu":
             return super().forward(x)
-        g = self.gate_proj(x)
-        u = self.up_proj(x)
+        g, u = shared_input_linear(x, (self.gate_proj, self.up_proj))
         if not swiglu_supported(g, u):
             return self.down_proj(self.act_fn(g) * u)
         return self.down_proj(swiglu(g, u))

@@ -13,6 +13,7 @@ import torch
 from transformers.models.llama.modeling_llama import ALL_ATTENTION_FUNCTIONS, LlamaAttention, eager_attention_forward
 
 from .. import _lib
+from .hip_linear import shared_input_linear
 
 _DT = {torch.float32: 0, torch.bfloat16: 1}
 
@@ -94,9 +95,8 @@ class NaylisAttention(LlamaAttention):
                 not _shape_ok(dtype, hidden_states.device, B, S, self.head_dim, cos, sin):
             return super().forward(hidden_states, position_embeddings=position_embeddings,
                                    attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
-        q = self.q_proj(hidden_states).view(shape)
-        k = self.k_proj(hidden_states).view(shape)
-        v = self.v_proj(hidden_states).view(shape).transpose(1, 2)
+        q, k, v = shared_input_linear(hidden_states, (self.q_proj, self.k_proj, self.v_proj))
+        q, k, v = q.view(shape), k.view(shape), v.view(shape).transpose(1, 2)
         q, k = rope(q, k, cos, sin)
         interface = ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation, eager_attention_forward)
         out, weights = interface(self, q.transpose(1, 2), k.transpose(1, 2), v, attention_mask,

@@ -109,3 +109,44 @@ def test_naylis_linear_module_swap(dev):
     assert bool(((block[0].weight.grad.float() - gw).abs() <= tol).all())
     assert bool(((ref[0].weight.grad.float() - gw).abs() <= tol).all())
     assert_close(block[1].weight.grad, ref[1].weight.grad, "dW (nn.Linear)")
+
+
+def test_shared_input_linear_matches_separate_layers(dev):
+    """shared_input_linear (q/k/v, gate/up of the decoder): the same outputs as
+    applying the layers one by one; the input gradient is the sum of the
+    products accumulated in one GEMM epilogue (close to autograd's sum of
+    rounded products), weight gradients to the bf16 GEMM bound."""
+    from naylis_amd.mom_kernels.hip_linear import shared_input_linear
+    torch.manual_seed(11)
+    layers = [torch.nn.Linear(256, n, bias=False).to(dev, torch.bfloat16) for n in (256, 512, 256)]
+    x = torch.randn(2, 512, 256, device=dev, dtype=torch.bfloat16)
+    dys = [torch.randn(2, 512, m.out_features, device=dev, dtype=torch.bfloat16) for m in layers]
+    xa = x.clone().requires_grad_(True)
+    outs = shared_input_linear(xa, layers)
+    torch.autograd.backward(outs, dys)
+    wgrads = [m.weight.grad.clone() for m in layers]
+    for m in layers:
+        m.weight.grad = None
+    for o, m in zip(outs, layers):
+        assert torch.equal(o, m(x))
+    x32 = x.reshape(-1, 256).float()
+    parts = [torch.mm(d.reshape(-1, m.out_features).float(), m.weight.detach().float()) for d, m in zip(dys, layers)]
+    dx = sum(parts)
+    # three bf16 roundings of partial sums (here, and in autograd's sum of rounded products), each at most
+    # 2^-9 of the sum of the products' magnitudes, plus the GEMMs' accumulation
+    tol = 2.0 ** -7 * sum(q.abs() for q in parts) + 1e-3
+    assert bool(((xa.grad.reshape(-1, 256).float() - dx).abs() <= tol).all())
+    # and no further from the fp32 sum than autograd's own sum over the separate layers
+    xb = x.clone().requires_grad_(True)
+    torch.autograd.backward([m(xb) for m in layers], dys)
+    err_lib = float((xa.grad.reshape(-1, 256).float() - dx).abs().max())
+    err_torch = float((xb.grad.reshape(-1, 256).float() - dx).abs().max())
+    assert err_lib <= 1.5 * err_torch + 1e-3, (err_lib, err_torch)
+    for d, m, g in zip(dys, layers, wgrads):
+        gw = torch.mm(d.reshape(-1, m.out_features).float().t(), x32)
+        tol = 2.0 ** -8 * gw.abs() + 2e-3 * max(1.0, float(gw.abs().max()))
+        assert bool(((g.float() - gw).abs() <= tol).all())
+    # no grad: the plain layers
+    with torch.no_grad():
+        outs = shared_input_linear(x, layers)
+    assert all(o.grad_fn is None for o in outs)
