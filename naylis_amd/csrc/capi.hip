@@ -545,13 +545,14 @@ int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, 
 
 // ---------------------------------------------------- projection weight grad
 static int wgrad_splits(int64_t N, int64_t D_in, int64_t D_out) {
-  // enough workgroups for two per CU, each reducing at least 1024 tokens
+  // enough workgroups for two per CU, each reducing at least 1024 tokens, as a power of two: the
+  // token range then splits into equal whole K tiles (3, 5 or 6 splits measure 10-25 % slower than
+  // the neighbouring power of two at 16384 tokens)
   const int64_t tiles = ((D_out + 127) / 128) * ((D_in + 127) / 128);
-  int64_t s = (512 + tiles - 1) / tiles;
-  const int64_t smax = N / 1024 > 1 ? N / 1024 : 1;
-  if (s > smax) s = smax;
-  if (s > 64) s = 64;
-  return (int)(s < 1 ? 1 : s);
+  const int64_t want = (512 + tiles - 1) / tiles;
+  int64_t s = 1;
+  while (s < want && s < 64 && 2 * s * 1024 <= N) s *= 2;
+  return (int)s;
 }
 
 static int check_wgrad_dims(int64_t N, int64_t D_in, int64_t D_out) {
