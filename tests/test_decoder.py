@@ -7,6 +7,8 @@ the config-3 decoder has the stated size.  GPU: loss and gradients of the
 product decoder (bf16, fused MoM nodes) against the fp32 CPU oracle on the
 same weights, and gradient-checkpoint exactness.
 """
+import copy
+
 import pytest
 import torch
 
@@ -242,3 +244,19 @@ def test_decoder_grad_ckpt_matches(dev):
     assert g0.keys() == g1.keys()
     for n in g0:
         assert _rel(g1[n], g0[n]) <= 1e-2, n
+
+
+def test_trunk_linear_modules_fall_back_off_rocm():
+    """NaylisLinear / shared_input_linear keep nn.Linear's parameters, keys and
+    results where the library does not apply (CPU tensors here)."""
+    from naylis_amd.mom_kernels.hip_linear import NaylisLinear, shared_input_linear, use_library_wgrad
+    torch.manual_seed(3)
+    block = torch.nn.Sequential(torch.nn.Linear(16, 24, bias=False), torch.nn.Linear(24, 16, bias=False))
+    ref = copy.deepcopy(block)
+    use_library_wgrad(block)
+    assert all(type(m) is NaylisLinear for m in block)
+    assert list(block.state_dict()) == list(ref.state_dict())
+    x = torch.randn(3, 8, 16)
+    assert torch.equal(block(x), ref(x))
+    outs = shared_input_linear(x, (block[0], ref[0]))
+    assert torch.equal(outs[0], ref[0](x)) and torch.equal(outs[1], ref[0](x))
