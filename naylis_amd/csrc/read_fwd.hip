@@ -18,8 +18,6 @@
 // from LDS, Q^T resident in registers), online softmax per token column,
 // O^T += V_g^T P^T with P^T taken straight from the accumulator registers and
 // V^T read from the natural-layout V tile with the transposing LDS read.
-#include <stdlib.h>
-
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
@@ -285,19 +283,23 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Wide forward: 4 waves x 64 tokens per workgroup (256 positions of the token
-// order), for block sizes that are multiples of 32 and head_dim 32/64/128.
-// Each wave owns two 32-token MFMA column tiles (a: tokens 0..31, b: 32..63 of
-// its 64), so every K fragment and every V^T fragment read from LDS feeds two
-// MFMAs; the bank is streamed through LDS one SG-slot stage (a slice of one
-// block) at a time, double-buffered, with one barrier per stage.  Inside a
-// stage the wave walks 32-slot chunks and computes S^T of chunk c+1 before
-// the softmax of chunk c, so the MFMA pipe has independent work while the
-// exp2 / max / convert instructions of the previous chunk issue.  The running
-// max follows the same lazy rule as the narrow kernel (moves only by more
-// than 8 in log2 units); the per-lane row sums stay lane-local until the
-// epilogue, and the one cross-lane step per chunk (max over the two lane
-// halves that hold one token column) is a v_permlane32_swap.
+// Fast forward: head_dim 64, block sizes that are multiples of 32 (every
+// Naylis configuration).  One workgroup = (h, 256 consecutive positions of the
+// token order), 8 waves x 32 tokens (one MFMA column tile each).
+//
+// The workgroup's active 32-slot chunks (every chunk of every block one of its
+// tokens selects, ascending) pass through LDS in stages of up to 8 chunks (K
+// and V of 256 slots: 72 KiB, two workgroups per CU), so a stage costs one
+// barrier pair instead of a barrier per slot group; inside a stage each wave
+// walks the chunks some token of its 32 selects with no barrier.
+//
+// Softmax: a token's running max m is the exact max of the first chunk it
+// selects and afterwards moves only when a chunk would give it p > 2^64
+// (p <= 2^64 is exact in fp32 and in range for bf16; O and l carry the same
+// scale), so the common chunk needs one fma and one exp2 per score and no
+// rescale of O.  The row sum l adds the bf16 weights that multiply V
+// (v_dot2c_f32_bf16), so O / l is a convex combination of V rows exactly as
+// the MFMA sees them.
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -306,292 +308,229 @@ __device__ __forceinline__ float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+__device__ __forceinline__ float max16(const f32x16& x) {
+  float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+  for (int v = 3; v < 15; v += 2) m = fmaxf(fmaxf(m, x[v]), x[v + 1]);
+  return fmaxf(m, x[15]);
+}
+// Sum of 8 bf16 values into an fp32 accumulator (v_dot2c_f32_bf16 against 1.0).
+__device__ __forceinline__ float add_bf16x8(const bf16x8& p, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  const uint4 u = __builtin_bit_cast(uint4, p);
+  float s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.x), one, acc, false);
+  float s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.y), one, 0.f, false);
+  s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.z), one, s0, false);
+  s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.w), one, s1, false);
+  return s0 + s1;
+}
 
-template <int HD>
-struct WideFwdCfg {
-  static constexpr int SG = HD >= 128 ? 64 : 128;  // slots per LDS stage
-  static constexpr int MINB = HD >= 128 ? 1 : 2;   // workgroups per CU the registers allow
-};
-
-template <int HD, int TK>
-__global__ __launch_bounds__(256, WideFwdCfg<HD>::MINB) void read_fwd_wide_kernel(
+template <int TK>
+__global__ __launch_bounds__(512, 4) void read_fwd_fast_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
     float* __restrict__ lse, const int32_t* __restrict__ order, long N, int H, int L, int E, int block_size,
     int topk, float alpha, int n_tiles) {
-  constexpr int SG = WideFwdCfg<HD>::SG;
-  constexpr int NT = 256;
-  constexpr int TM = 256;           // positions per workgroup
-  constexpr int KS = HD / 16;       // K-steps of Q.K^T
-  constexpr int NC = SG / 32;       // 32-slot chunks per stage
-  constexpr int NO = HD / 32;       // 32-feature output tiles
-  constexpr int PITCH = HD + 8;     // LDS row pitch (bf16): conflict-free 16-byte row reads
-  constexpr int TILE = SG * PITCH;
-  constexpr int VEC = SG * HD / 8;  // 16-byte vectors per K (or V) stage
-  constexpr int PER = VEC / NT;
-  static_assert(VEC % NT == 0, "stage copy must tile the workgroup");
+  constexpr int HD = 64, KS = HD / 16, NO = HD / 32, PITCH = HD + 8;
+  constexpr int NW = 8, NT = 64 * NW, TM = 32 * NW;  // 8 waves x 32 tokens
+  constexpr int SCH = 8;                     // 32-slot chunks per LDS stage
+  constexpr int TILE = SCH * 32 * PITCH;     // bf16 elements of one staged tensor
+  constexpr int PER = SCH * 32 * HD / 8 / NT;  // 16-byte pieces per thread per tensor
+  static_assert(PER * NT * 8 == SCH * 32 * HD, "stage copy must tile the workgroup");
 
-  __shared__ __attribute__((aligned(16))) bf16_t k_lds[2 * TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t v_lds[2 * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[TILE];
   __shared__ uint8_t flags[kMaxBlocks];
-  __shared__ uint16_t blist[kMaxBlocks];
-  __shared__ int n_blk;
-
-  const int G = H * n_tiles;
-  const int wid = xcd_remap(blockIdx.x, G);
-  const int tile = wid % n_tiles;
-  const int h = wid / n_tiles;
+  __shared__ uint32_t chunks[kMaxGroups];  // (block << 16) | chunk index (slot / 32)
+  __shared__ int n_chunks_s;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const long pos_a = (long)tile * TM + wave * 64 + col;
-  const long pos_b = pos_a + 32;
-  const bool ok_a = pos_a < N, ok_b = pos_b < N;
   const int32_t* ord = order_table(order);
-  const long tok_a = ok_a ? order_token(ord, pos_a, N) : 0;
-  const long tok_b = ok_b ? order_token(ord, pos_b, N) : 0;
   const int D = H * HD;
-
-  TokenRoute<TK> ra, rb;
-  load_route<TK>(ra, top_idx, top_gates, tok_a, ok_a, topk);
-  load_route<TK>(rb, top_idx, top_gates, tok_b, ok_b, topk);
-  // Q^T fragments (B operand) of both token tiles, issued right after the
-  // routing loads (loads retire in issue order, so the routing can be used
-  // while these are still in flight across the LDS barriers below)
-  bf16x8 qa[KS], qb[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const long col_off = (long)h * HD + 16 * ks + 8 * g;
-    qa[ks] = ok_a ? *reinterpret_cast<const bf16x8*>(q + tok_a * D + col_off) : bf16x8{};
-    qb[ks] = ok_b ? *reinterpret_cast<const bf16x8*>(q + tok_b * D + col_off) : bf16x8{};
-  }
-
-  for (int e = tid; e < E; e += NT) flags[e] = 0;
-  lds_barrier();
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(k, (uint32_t)L * (uint32_t)D * 2u);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v, (uint32_t)L * (uint32_t)D * 2u);
   {
-    const TokenRoute<TK>& r = g == 0 ? ra : rb;
-    const bool ok = g == 0 ? ok_a : ok_b;
-    if (ok) {
+    const int wid = xcd_remap(blockIdx.x, H * n_tiles);
+    const int h = wid / n_tiles;
+    const int tile = wid % n_tiles;
+    const int hoff = h * HD * 2;  // byte offset of head h in a row
+
+    // ---- this lane's token, routing and q
+    const long pos = (long)tile * TM + wave * 32 + col;
+    const bool ok = pos < N;
+    const long tok = ok ? order_token(ord, pos, N) : 0;
+    TokenRoute<TK> rt;
+    load_route<TK>(rt, top_idx, top_gates, tok, ok, topk);
+    bf16x8 qf[KS];
 #pragma unroll
-      for (int t = 0; t < TK; ++t)
-        if (t < topk && r.idx[t] >= 0 && r.idx[t] < E) flags[r.idx[t]] = 1;
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = ok ? *reinterpret_cast<const bf16x8*>(q + tok * D + (long)h * HD + 16 * ks + 8 * g) : bf16x8{};
+
+    // ---- the item's active chunks, ascending
+    for (int e = tid; e < E; e += NT) flags[e] = 0;
+    lds_barrier();
+    if (g == 0 && ok) {
+#pragma unroll
+      for (int s = 0; s < TK; ++s)
+        if (s < topk && rt.idx[s] >= 0 && rt.idx[s] < E) flags[rt.idx[s]] = 1;
     }
-  }
-  lds_barrier();
-  if (wave == 0) {
-    int total = 0;
-    for (int base = 0; base < E; base += 64) {
-      const int e = base + lane;
-      const bool act = e < E && flags[e] != 0;
-      const unsigned long long m = __ballot(act);
-      if (act) blist[total + __popcll(m & ((1ull << lane) - 1ull))] = (uint16_t)e;
-      total += __popcll(m);
-    }
-    if (lane == 0) n_blk = total;
-  }
-
-
-  f32x16 oa[NO], ob[NO];
-#pragma unroll
-  for (int j = 0; j < NO; ++j) {
-    oa[j] = f32x16{};
-    ob[j] = f32x16{};
-  }
-  float ma = kNegBig, mb = kNegBig, la = 0.f, lb = 0.f;  // la/lb: this lane's share of the row sums
-
-  lds_barrier();
-  const int spb = block_size / SG > 0 ? block_size / SG : 1;  // stages per block (block_size % SG == 0)
-  const int sg_eff = block_size < SG ? block_size : SG;       // slots a stage covers
-  const int n_stage = n_blk * spb;
-
-  uint4 kreg[PER], vreg[PER];
-  auto load_stage = [&](int s) {
-    const int e = blist[s / spb];
-    const int s0 = e * block_size + (s % spb) * sg_eff;
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int vi = tid + NT * r;
-      const int row = vi / (HD / 8), c8 = vi % (HD / 8);
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (row < sg_eff) {
-        const long off = (long)(s0 + row) * D + (long)h * HD + 8 * c8;
-        kv = *reinterpret_cast<const uint4*>(k + off);
-        vv = *reinterpret_cast<const uint4*>(v + off);
+    lds_barrier();
+    if (wave == 0) {
+      const int cpb = block_size >> 5;  // chunks per block
+      int total = 0;
+      for (int base = 0; base < E; base += 64) {
+        const int e = base + lane;
+        const bool act = e < E && flags[e] != 0;
+        const unsigned long long m = __ballot(act);
+        if (act) {
+          const int p0 = (total + __popcll(m & ((1ull << lane) - 1ull))) * cpb;
+          for (int j = 0; j < cpb; ++j) chunks[p0 + j] = ((uint32_t)e << 16) | (uint32_t)(e * cpb + j);
+        }
+        total += __popcll(m);
       }
-      kreg[r] = kv;
-      vreg[r] = vv;
+      if (lane == 0) n_chunks_s = total * cpb;
     }
-  };
-  auto store_stage = [&](int buf) {
+    f32x16 o[NO];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int vi = tid + NT * r;
-      const int row = vi / (HD / 8), c8 = vi % (HD / 8);
-      *reinterpret_cast<uint4*>(&k_lds[buf * TILE + row * PITCH + 8 * c8]) = kreg[r];
-      *reinterpret_cast<uint4*>(&v_lds[buf * TILE + row * PITCH + 8 * c8]) = vreg[r];
-    }
-  };
+    for (int j = 0; j < NO; ++j) o[j] = f32x16{};
+    float m_run = kNegBig, l_run = 0.f;  // l_run: this lane's share of the row sum
+    lds_barrier();
+    const int n_ch = n_chunks_s;
 
-  if (n_stage > 0) {
-    load_stage(0);
-    store_stage(0);
-  }
-  lds_barrier();
-
-  for (int s = 0; s < n_stage; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < n_stage) load_stage(s + 1);  // in flight during the math below
-    const int e = blist[s / spb];
-    bool sa_sel, sb_sel;
-    const float ca = route_bias<TK>(ra, e, topk, sa_sel);
-    const float cb = route_bias<TK>(rb, e, topk, sb_sel);
-    if (__any(sa_sel || sb_sel)) {
-      const bf16_t* kt = k_lds + buf * TILE;
-      const bf16_t* vt = v_lds + buf * TILE;
-      f32x16 sa[2], sb[2];
-      auto qk = [&](int c, f32x16& xa, f32x16& xb) {
-        xa = f32x16{};
-        xb = f32x16{};
+    auto qk = [&](int c, f32x16& x) {
+      x = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kt[(32 * c + col) * PITCH + 16 * ks + 8 * g]);
-          xa = mfma32(a, qa[ks], xa);
-          xb = mfma32(a, qb[ks], xb);
-        }
-      };
-      qk(0, sa[0], sb[0]);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (32 * c >= sg_eff) break;  // a 32- or 64-slot block fills part of a stage
-        f32x16& xa = sa[c & 1];
-        f32x16& xb = sb[c & 1];
-        if (c + 1 < NC && 32 * (c + 1) < sg_eff) qk(c + 1, sa[(c + 1) & 1], sb[(c + 1) & 1]);
-
-        // ---- online softmax (lazy running max), both token tiles
-        float mxa = -INFINITY, mxb = -INFINITY;
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) {
-          mxa = fmaxf(mxa, xa[vv]);
-          mxb = fmaxf(mxb, xb[vv]);
-        }
-        mxa = pair_max(mxa);
-        mxb = pair_max(mxb);
-        float na = ma, nb = mb;
-        if (sa_sel) {
-          const float cand = fmaf(mxa, alpha, ca);
-          if (cand > ma + 8.f) na = cand;
-        }
-        if (sb_sel) {
-          const float cand = fmaf(mxb, alpha, cb);
-          if (cand > mb + 8.f) nb = cand;
-        }
-        const bool mva = na != ma, mvb = nb != mb;
-        if (__any((mva && ma != kNegBig) || (mvb && mb != kNegBig))) {
-          const float cra = mva ? __builtin_amdgcn_exp2f(ma - na) : 1.f;
-          const float crb = mvb ? __builtin_amdgcn_exp2f(mb - nb) : 1.f;
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * c + col) * PITCH + 16 * ks + 8 * g]);
+        x = mfma32(a, qf[ks], x);
+      }
+    };
+    // VALU phase: softmax of the scores in x into bf16 weights pk
+    auto softmax = [&](int s0, int c, f32x16& x, bf16x8 (&pk)[2]) {
+      const int e = (int)(chunks[s0 + c] >> 16);
+      bool sl;
+      const float cb = route_bias<TK>(rt, e, topk, sl);
+      const float cand = fmaf(pair_max(max16(x)), alpha, cb);
+      // the running max moves on the token's first selected chunk, or when
+      // this chunk would give p > 2^64
+      if (__any(sl && (m_run == kNegBig || cand > m_run + 64.f))) {
+        if (sl && (m_run == kNegBig || cand > m_run + 64.f)) {
+          const float cr = __builtin_amdgcn_exp2f(m_run - cand);
 #pragma unroll
           for (int j = 0; j < NO; ++j)
 #pragma unroll
-            for (int vv = 0; vv < 16; ++vv) {
-              oa[j][vv] *= cra;
-              ob[j][vv] *= crb;
-            }
-          la *= cra;
-          lb *= crb;
-        }
-        ma = na;
-        mb = nb;
-        const float adda = sa_sel ? ca - ma : -INFINITY;
-        const float addb = sb_sel ? cb - mb : -INFINITY;
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) {
-          const float pa = __builtin_amdgcn_exp2f(fmaf(xa[vv], alpha, adda));
-          const float pb = __builtin_amdgcn_exp2f(fmaf(xb[vv], alpha, addb));
-          xa[vv] = pa;
-          xb[vv] = pb;
-          la += pa;
-          lb += pb;
-        }
-
-        // ---- O^T += V^T P^T for both tiles; each V^T fragment feeds two MFMAs
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const bf16x8 bpa = pack8(xa, 8 * kk);
-          const bf16x8 bpb = pack8(xb, 8 * kk);
-#pragma unroll
-          for (int j = 0; j < NO; ++j) {
-            const bf16x8 a = lds_frag_T<true, true>(vt, PITCH, 32 * c + 16 * kk, 32 * j);
-            oa[j] = mfma32(a, bpa, oa[j]);
-            ob[j] = mfma32(a, bpb, ob[j]);
-          }
+            for (int vv = 0; vv < 16; ++vv) o[j][vv] *= cr;
+          l_run *= cr;
+          m_run = cand;
         }
       }
+      const float add = sl ? cb - m_run : -INFINITY;
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
+      pk[0] = pack8(x, 0);
+      pk[1] = pack8(x, 8);
+      l_run = add_bf16x8(pk[1], add_bf16x8(pk[0], l_run));
+    };
+    // MFMA phase part: O^T += V^T P^T with V^T read transposed from the stage
+    auto pv = [&](int c, const bf16x8 (&pk)[2]) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+          const bf16x8 a = lds_frag_T<true, true>(v_lds, PITCH, 32 * c + 16 * kk, 32 * j);
+          o[j] = mfma32(a, pk[kk], o[j]);
+        }
+    };
+
+    for (int s0 = 0; s0 < n_ch; s0 += SCH) {
+      const int nst = min(SCH, n_ch - s0);
+      if (s0 > 0) lds_barrier();  // every wave is done with the previous stage
+      {
+        uint4 kr[PER], vr[PER];
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+          const int p = tid + NT * r;
+          const int row = p >> 3, c8 = p & 7, ch = row >> 5;
+          // rows of chunks beyond the stage read past the buffer's end, which
+          // a buffer load returns as zeros
+          const uint32_t slot = ch < nst ? (chunks[s0 + ch] & 0xffffu) * 32u + (uint32_t)(row & 31) : (uint32_t)L;
+          const uint32_t off = (slot * (uint32_t)D + 8u * (uint32_t)c8) * 2u;
+          kr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, hoff, 0));
+          vr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, hoff, 0));
+        }
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+          const int p = tid + NT * r;
+          const int row = p >> 3, c8 = p & 7;
+          *reinterpret_cast<uint4*>(&k_lds[row * PITCH + 8 * c8]) = kr[r];
+          *reinterpret_cast<uint4*>(&v_lds[row * PITCH + 8 * c8]) = vr[r];
+        }
+      }
+      // chunks of this stage that some token of the wave selects
+      unsigned mine = 0;
+      for (int c = 0; c < nst; ++c) {
+        const int e = (int)(chunks[s0 + c] >> 16);
+        bool sel = false;
+#pragma unroll
+        for (int s = 0; s < TK; ++s) sel |= s < topk && rt.idx[s] == e;
+        if (__any(sel)) mine |= 1u << c;
+      }
+      lds_barrier();
+
+      // the wave's chunks of the stage, with no barrier in between
+      while (mine) {
+        const int c = __builtin_ctz(mine);
+        mine &= mine - 1;
+        f32x16 x;
+        bf16x8 pk[2];
+        qk(c, x);
+        softmax(s0, c, x, pk);
+        pv(c, pk);
+      }
     }
-    if (s + 1 < n_stage) store_stage(buf ^ 1);  // that buffer was last read before the previous barrier
-    lds_barrier();
+
+    // ---- epilogue: row sum over both lane halves, normalise, store o and lse
+    const float l = pair_sum(l_run);
+    if (ok) {
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int f0 = 32 * j + 16 * g;
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          lo[e2] = (__bf16)(o[j][e2] * inv);
+          hi[e2] = (__bf16)(o[j][8 + e2] * inv);
+        }
+        bf16_t* dst = out + tok * D + (long)h * HD + f0;
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+      }
+      if (g == 0) lse[(long)h * N + tok] = m_run + log2f(l);
+    }
   }
-
-  // ---- epilogue: row sums over both lane halves, normalise, store o and lse
-  la = pair_sum(la);
-  lb = pair_sum(lb);
-  auto store_tok = [&](const f32x16* o, float l, float m, long tok, bool ok) {
-    if (!ok) return;
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-#pragma unroll
-    for (int j = 0; j < NO; ++j) {
-      const int f0 = 32 * j + 16 * g;
-      bf16x8 lo, hi;
-#pragma unroll
-      for (int e2 = 0; e2 < 8; ++e2) {
-        lo[e2] = (__bf16)(o[j][e2] * inv);
-        hi[e2] = (__bf16)(o[j][8 + e2] * inv);
-      }
-      bf16_t* dst = out + tok * D + (long)h * HD + f0;
-      *reinterpret_cast<bf16x8*>(dst) = lo;
-      *reinterpret_cast<bf16x8*>(dst + 8) = hi;
-    }
-    if (g == 0) lse[(long)h * N + tok] = m + log2f(l);
-  };
-  store_tok(oa, la, ma, tok_a, ok_a);
-  store_tok(ob, lb, mb, tok_b, ok_b);
 }
 
-template <int HD, int TK>
-static void fwd_wide_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
+// The fast kernel covers head_dim 64 with block sizes that are multiples of 32.
+static bool fwd_fast_fits(const ReadDims& d) { return d.HD == 64 && d.block_size % 32 == 0; }
+
+template <int TK>
+static void fwd_fast_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                           float* lse, const ReadDims& d, hipStream_t st) {
   const long N = (long)d.B * d.S;
   const int n_tiles = (int)((N + 255) / 256);
-  const float alpha = (float)(1.0 / __builtin_sqrt((double)HD)) * kLog2e;
+  const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL((read_fwd_wide_kernel<HD, TK>), dim3(d.H * n_tiles), dim3(256), 0, st,
+               hipLaunchKernelGGL((read_fwd_fast_kernel<TK>), dim3(d.H * n_tiles), dim3(512), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (bf16_t*)out, lse,
                                   d.order, N, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
 }
 
-// The wide kernel covers block sizes that are multiples of 32 whose stage
-// slices tile the block (block_size % SG == 0, or block_size < SG dividing it)
-// and head_dim 32/64/128.  It is opt-in (NAYLIS_READ_FWD_WIDE=1): on MI355X at
-// config 2 the narrow kernel measured faster (47 vs 53 us), its per-workgroup
-// latency (route -> Q -> first stage) being spread over more workgroups.
-static bool fwd_wide_enabled() {
-  static const bool v = [] {
-    const char* e = getenv("NAYLIS_READ_FWD_WIDE");
-    return e && e[0] == '1';
-  }();
-  return v;
-}
-
-template <int HD>
-static bool fwd_wide_fits(const ReadDims& d) {
-  constexpr int SG = WideFwdCfg<HD>::SG;
-  if (d.block_size % 32 != 0) return false;
-  return d.block_size % SG == 0 || SG % d.block_size == 0;
-}
-
-// ---------------------------------------------------------------------------
 template <int HD, int SG, bool AL, int TK>
 static void fwd_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                      float* lse, const ReadDims& d, hipStream_t st) {
@@ -604,24 +543,11 @@ static void fwd_inst(const void* q, const void* k, const void* v, const int32_t*
                                   d.order, N, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
 }
 
-// Slot-group size of the forward: NAYLIS_READ_FWD_SG=128 selects 128-slot
-// groups instead of the default 64 (read once per process; a tuning knob like
-// the reference's NAYLIS_TRITON_BLOCK_N, mom_kernels/triton_gpu.py:48-55).
-static int fwd_sg_override() {
-  static const int v = [] {
-    const char* e = getenv("NAYLIS_READ_FWD_SG");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
 template <int HD, int TK>
 static void fwd_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                     float* lse, const ReadDims& d, hipStream_t st) {
   constexpr int SGMAX = 64;  // measured faster than 128 on MI355X (fewer registers, 2 workgroups per CU)
-  if (fwd_sg_override() == 128 && HD <= 64 && d.block_size % 128 == 0)
-    fwd_inst<HD, (HD <= 64 ? 128 : 64), true, TK>(q, k, v, ti, tg, out, lse, d, st);
-  else if (d.block_size % SGMAX == 0)
+  if (d.block_size % SGMAX == 0)
     fwd_inst<HD, SGMAX, true, TK>(q, k, v, ti, tg, out, lse, d, st);
   else if (d.block_size % 64 == 0)
     fwd_inst<HD, 64, true, TK>(q, k, v, ti, tg, out, lse, d, st);
@@ -634,10 +560,12 @@ static void fwd_hdk(const void* q, const void* k, const void* v, const int32_t* 
 template <int HD>
 static void fwd_hd(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                    float* lse, const ReadDims& d, hipStream_t st) {
-  // wide kernel: head_dim 32/64 and top-k <= 2 fit its registers without spills
-  if constexpr (HD == 32 || HD == 64) {
-    if (fwd_wide_enabled() && d.topk <= 2 && fwd_wide_fits<HD>(d)) {
-      fwd_wide_inst<HD, 2>(q, k, v, ti, tg, out, lse, d, st);
+  if constexpr (HD == 64) {
+    if (fwd_fast_fits(d)) {
+      if (d.topk <= 2)
+        fwd_fast_inst<2>(q, k, v, ti, tg, out, lse, d, st);
+      else
+        fwd_fast_inst<kMaxTopK>(q, k, v, ti, tg, out, lse, d, st);
       return;
     }
   }

@@ -149,10 +149,11 @@ def bank_kv(M_blocks, w_k, w_v):
 
 
 def aux_loss(probs, top_idx, num_blocks):
-    """Load-balance aux term of one MoM layer: model.py:216-228.
+    """Load-balance aux term of one MoM layer: model.py:476-517
+    (``_collect_mom_aux_loss``, the per-layer term at model.py:494-503).
 
     num_blocks * sum_e frac_selected_e * mean_prob_e, with the selection mask
-    built by comparison + any (model.py:219-221).
+    built by comparison + any (model.py:498-499).
     """
     probs = probs.reshape(-1, num_blocks).float()
     top_idx = top_idx.reshape(probs.shape[0], -1)
@@ -164,7 +165,7 @@ def aux_loss(probs, top_idx, num_blocks):
 
 
 def router_stats(probs, top_idx, num_blocks):
-    """Router entropy and dead-block fraction: model.py:226-228."""
+    """Router entropy and dead-block fraction: model.py:505-507."""
     probs = probs.reshape(-1, num_blocks).float()
     top_idx = top_idx.reshape(probs.shape[0], -1)
     blocks = torch.arange(num_blocks, device=top_idx.device)

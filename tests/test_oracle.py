@@ -279,6 +279,36 @@ def test_aux_loss_closed_form_and_scatter():
                                rtol=0, atol=1e-6)
 
 
+def router_stats_closed_forms():
+    """(probs, top_idx, E, entropy, dead fraction) cases whose statistics are
+    fixed by the mathematics, not by the formula under test: uniform probs
+    have entropy log E, one-hot probs 0 (0 * log(1e-9) = 0), a two-point
+    distribution (a, 1-a, 0, ...) the binary entropy; a block no token
+    selects is dead."""
+    E = 8
+    cases = []
+    N = 40
+    idx = torch.stack([torch.arange(N) % E, (torch.arange(N) + 3) % E], -1)
+    cases.append((torch.full((N, E), 1.0 / E), idx, E, math.log(E), 0.0))
+    onehot = torch.zeros(N, E)
+    onehot[torch.arange(N), torch.arange(N) % 5] = 1.0
+    idx1 = torch.stack([torch.arange(N) % 5, (torch.arange(N) % 5 + 1) % 5], -1)  # blocks 5..7 never selected
+    cases.append((onehot, idx1, E, 0.0, 3.0 / E))
+    a = 0.25  # exact in fp32
+    two = torch.zeros(N, E)
+    two[:, 0], two[:, 1] = a, 1.0 - a
+    cases.append((two, torch.tensor([[0, 1]]).expand(N, 2), E, -(a * math.log(a) + (1 - a) * math.log(1 - a)),
+                  6.0 / E))
+    return cases
+
+
+def test_router_stats_closed_forms():
+    for probs, idx, E, ent_want, dead_want in router_stats_closed_forms():
+        ent, dead = oracle.router_stats(probs.double(), idx, E)
+        assert abs(float(ent) - ent_want) <= 1e-6 * max(1.0, ent_want)  # fp32 arithmetic, as model.py:505
+        assert float(dead) == dead_want
+
+
 def test_active_tile_blocks_brute_force():
     g = torch.Generator().manual_seed(9)
     top = torch.randint(0, 6, (3, 300, 2), generator=g)

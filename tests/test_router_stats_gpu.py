@@ -48,6 +48,23 @@ def test_router_stats_match_reference_formulas(N, E, k, dead, dev):
     assert float(stats[2 * E + 2]) == float(dead_frac) == dead / E
 
 
+def test_router_stats_closed_forms(dev):
+    """Entropy and dead fraction where the mathematics fixes them: log E for
+    uniform probs, 0 for one-hot probs, the binary entropy for a two-point
+    distribution; blocks no token selects are dead (aux = k at uniform
+    routing, the closed form of METHODOLOGY.md:90)."""
+    from test_oracle import router_stats_closed_forms
+
+    from naylis_amd import mom_kernels
+    for probs, idx, E, ent_want, dead_want in router_stats_closed_forms():
+        stats = mom_kernels.mom_router_stats(probs.to(dev), idx.to(torch.int32).contiguous().to(dev)).cpu()
+        assert abs(float(stats[2 * E + 1]) - ent_want) <= 1e-6 * max(ent_want, 1.0), (float(stats[2 * E + 1]), ent_want)
+        assert float(stats[2 * E + 2]) == dead_want
+    probs, idx, E = router_stats_closed_forms()[0][:3]
+    stats = mom_kernels.mom_router_stats(probs.to(dev), idx.to(torch.int32).contiguous().to(dev)).cpu()
+    assert abs(float(stats[2 * E]) - idx.shape[1]) <= 1e-6
+
+
 def test_router_stats_deterministic(dev):
     from naylis_amd import mom_kernels
     probs, idx = _routing(20000, 8, 2, seed=1)
