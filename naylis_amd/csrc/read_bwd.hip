@@ -14,7 +14,8 @@
 //  2. read_tile_flags / read_tile_lists — which 64-token tiles select any
 //     block of each 128-slot group, as compact ascending lists.
 //  3. read_bwd_dkdv_kernel — one workgroup per (h, 128-slot group, share of
-//     that group's active tiles); K/V rows of its slots stay in registers;
+//     that group's active tiles), 4 waves of 32 slots; K/V rows of its slots
+//     stay in registers;
 //     S, dP, dS per tile, dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
 //     read transposed from the natural-layout tiles; fp32 partials per share.
 //  4. read_bwd_reduce kernels — partials summed over shares in a fixed order
@@ -337,13 +338,17 @@ __global__ __launch_bounds__(256) void read_tile_lists_kernel(const uint8_t* __r
   if (threadIdx.x == 0) count[sg] = total;
 }
 
-// dK / dV over the shared bank.  8 waves: wave w owns slots
-// 128 sg + 32 (w & 3) + lane%32 and the token half (w >> 2) of each 64-token
-// tile.  Lanes own slots (S = Q K^T orientation), so P and dS come out of the
+// dK / dV over the shared bank.  Wave w owns slots 128 sg + 32 (w & 3) +
+// lane%32.  NH = 2: 8 waves, the token half (w >> 2) of each 64-token tile,
+// one workgroup per CU at head_dim 64.  NH = 1: 4 waves, each walking both
+// token halves, so two workgroups share a CU and the two waves on a SIMD
+// belong to different workgroups: they drift apart and one's MFMA work
+// overlaps the other's exp2 work instead of both waiting on the same phase.
+// Lanes own slots (S = Q K^T orientation), so P and dS come out of the
 // accumulators already in the B-operand layout of dV^T = dO^T P and
 // dK^T = Q^T dS, whose A operands are read transposed from the tiles.
-template <int HD, bool ALIGNED, int TK, bool SPLIT_V>
-__global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
+template <int HD, bool ALIGNED, int TK, bool SPLIT_V, int NH>
+__global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, const int32_t* __restrict__ tile_list,
@@ -355,8 +360,9 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   constexpr int NO = HDP / 32;
   constexpr int TT = kDkdvTile;
   constexpr int PITCH = HDP + 8;
+  constexpr int NT = 256 * NH;
   constexpr int VEC = TT * HD / 8;        // 16-byte vectors per staged tensor tile
-  constexpr int PER = (VEC + 511) / 512;
+  constexpr int PER = (VEC + NT - 1) / NT;
 
   // two buffers: tile it + 1 is stored while tile it is read, one barrier per tile
   __shared__ __attribute__((aligned(16))) bf16_t q_lds2[2][TT * PITCH];
@@ -366,7 +372,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   __shared__ int32_t idx_lds2[2][TT * TK];
   __shared__ float lg_lds2[2][TT * TK];
   __shared__ float lse_lds2[2][TT];
-  __shared__ __attribute__((aligned(16))) float red[4 * NO * 16 * 64];  // half-1 partials for the final sum
+  __shared__ __attribute__((aligned(16))) float red[NH == 2 ? 4 * NO * 16 * 64 : 1];  // half-1 partials (NH = 2)
 
   const int n_sg = Lq / 128;
   const int G = H * n_sg * n_chunks;
@@ -378,7 +384,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int quarter = wave & 3, half = wave >> 2;
+  const int quarter = wave & 3, half = NH == 2 ? wave >> 2 : 0;
   const int g = lane >> 5;
   const int col = lane & 31;
   const int slot = sg * 128 + quarter * 32 + col;
@@ -411,7 +417,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     acc_dv[j] = f32x16{};
   }
   if constexpr (HD < 32) {
-    for (int i = tid; i < 2 * TT * PITCH; i += 512) {
+    for (int i = tid; i < 2 * TT * PITCH; i += NT) {
       q_lds2[i / (TT * PITCH)][i % (TT * PITCH)] = 0;
       do_lds2[i / (TT * PITCH)][i % (TT * PITCH)] = 0;
     }
@@ -425,7 +431,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
   int cp_row[PER], cp_col[PER];
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
-    const int vi = tid + 512 * r;
+    const int vi = tid + NT * r;
     cp_row[r] = vi < VEC ? vi / (HD / 8) : TT;
     cp_col[r] = h * HD + 8 * (vi % (HD / 8));
   }
@@ -491,7 +497,7 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     float* lse_lds = lse_lds2[buf];
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int vi = tid + 512 * r;
+      const int vi = tid + NT * r;
       if (vi < VEC) {
         const int row = vi / (HD / 8), c8 = vi % (HD / 8);
         *reinterpret_cast<uint4*>(&q_lds[row * PITCH + 8 * c8]) = qreg[r];
@@ -549,77 +555,82 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
     const float* lg_lds = lg_lds2[buf];
     const float* lse_lds = lse_lds2[buf];
 
-    // ---- S = Q K^T and dP - delta = dO V^T - delta for this wave's 32 tokens x
-    // 32 slots (the dP accumulator starts at -delta of each register's token)
-    f32x16 acc_s = f32x16{}, acc_p;
+    // NH = 2: this wave's token half; NH = 1: both halves in turn
 #pragma unroll
-    for (int j4 = 0; j4 < 4; ++j4) {
-      const f32x4 nd4 = *reinterpret_cast<const f32x4*>(&dl_lds[32 * half + 8 * j4 + 4 * g]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd4[u];
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int off = (32 * half + col) * PITCH + 16 * ks + 8 * g;
-      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
-      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[off]);
-      acc_s = mfma32(aq, kf[ks], acc_s);
-      acc_p = mfma32(ad, vf[ks], acc_p);
-    }
-    // ---- P and dS, registers indexed by token
-#pragma unroll
-    for (int j4 = 0; j4 < 4; ++j4) {
-      const int r0 = 32 * half + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
-      f32x4 ad4;
-      if constexpr (ALIGNED) {
-        ad4 = *reinterpret_cast<const f32x4*>(&add_lds[quarter][r0]);
-      } else {
-#pragma unroll
+    for (int hh = (NH == 2 ? half : 0); hh < (NH == 2 ? half + 1 : 2); ++hh) {
+      // ---- S = Q K^T and dP - delta = dO V^T - delta for this wave's 32 tokens x
+      // 32 slots (the dP accumulator starts at -delta of each register's token)
+      f32x16 acc_s = f32x16{}, acc_p;
+  #pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const f32x4 nd4 = *reinterpret_cast<const f32x4*>(&dl_lds[32 * hh + 8 * j4 + 4 * g]);
+  #pragma unroll
+        for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd4[u];
+      }
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (32 * hh + col) * PITCH + 16 * ks + 8 * g;
+        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
+        const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[off]);
+        acc_s = mfma32(aq, kf[ks], acc_s);
+        acc_p = mfma32(ad, vf[ks], acc_p);
+      }
+      // ---- P and dS, registers indexed by token
+  #pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int r0 = 32 * hh + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
+        f32x4 ad4;
+        if constexpr (ALIGNED) {
+          ad4 = *reinterpret_cast<const f32x4*>(&add_lds[quarter][r0]);
+        } else {
+  #pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float c = 0.f;
+            bool sel = false;
+  #pragma unroll
+            for (int t = 0; t < TK; ++t)
+              if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
+                c += lg_lds[(r0 + u) * TK + t];
+                sel = true;
+              }
+            ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
+          }
+        }
+  #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          float c = 0.f;
-          bool sel = false;
-#pragma unroll
-          for (int t = 0; t < TK; ++t)
-            if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
-              c += lg_lds[(r0 + u) * TK + t];
-              sel = true;
-            }
-          ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
+          const int vv = 4 * j4 + u;
+          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, ad4[u]));
+          acc_s[vv] = p;
+          acc_p[vv] = p * acc_p[vv];
         }
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int vv = 4 * j4 + u;
-        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, ad4[u]));
-        acc_s[vv] = p;
-        acc_p[vv] = p * acc_p[vv];
-      }
-    }
-    // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = this wave's 32 tokens)
-    // dV sums P over thousands of tokens, so P enters as hi + lo bf16 parts
-    // (hi = bf16(P), lo = bf16(P - hi)); bf16 rounding of P would otherwise
-    // dominate the error of small dV entries.
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      bf16x8 bp, bp_lo;
-      if constexpr (SPLIT_V)
-        pack8_hilo(acc_s, 8 * kk, bp, bp_lo);
-      else
-        bp = pack8(acc_s, 8 * kk);
-      const bf16x8 bd = pack8(acc_p, 8 * kk);
-#pragma unroll
-      for (int j = 0; j < NO; ++j) {
-        const bf16x8 a_do = lds_frag_T<true, true>(do_lds, PITCH, 32 * half + 16 * kk, 32 * j);
-        const bf16x8 a_q = lds_frag_T<true, true>(q_lds, PITCH, 32 * half + 16 * kk, 32 * j);
-        acc_dv[j] = mfma32(a_do, bp, acc_dv[j]);
-        if constexpr (SPLIT_V) acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
-        acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
+      // ---- dV^T += dO^T P ; dK^T += Q^T dS   (K = this wave's 32 tokens)
+      // dV sums P over thousands of tokens, so P enters as hi + lo bf16 parts
+      // (hi = bf16(P), lo = bf16(P - hi)); bf16 rounding of P would otherwise
+      // dominate the error of small dV entries.
+  #pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        bf16x8 bp, bp_lo;
+        if constexpr (SPLIT_V)
+          pack8_hilo(acc_s, 8 * kk, bp, bp_lo);
+        else
+          bp = pack8(acc_s, 8 * kk);
+        const bf16x8 bd = pack8(acc_p, 8 * kk);
+  #pragma unroll
+        for (int j = 0; j < NO; ++j) {
+          const bf16x8 a_do = lds_frag_T<true, true>(do_lds, PITCH, 32 * hh + 16 * kk, 32 * j);
+          const bf16x8 a_q = lds_frag_T<true, true>(q_lds, PITCH, 32 * hh + 16 * kk, 32 * j);
+          acc_dv[j] = mfma32(a_do, bp, acc_dv[j]);
+          if constexpr (SPLIT_V) acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
+          acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
+        }
       }
     }
     lds_barrier();  // every wave is done with buffer buf before it is refilled
   }
 
-  // ---- sum the two token halves (fixed order), write this share's partials
+  // ---- sum the two token halves (fixed order, NH = 2), write this share's partials
+  if constexpr (NH == 2) {
   lds_barrier();
   if (half == 1) {
 #pragma unroll
@@ -642,11 +653,16 @@ __global__ __launch_bounds__(512) void read_bwd_dkdv_kernel(
       for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dv[j][vv];
   }
   lds_barrier();
+  if (half == 0) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) acc_dv[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
+  }
+  }
   if (half == 0 && slot_ok) {
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) acc_dv[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
       const int f0 = 32 * j + 16 * g;
       if (f0 < HD) {
         const long base = ((long)chunk * Lq + slot) * D + (long)h * HD + f0;
@@ -774,6 +790,9 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
   return hipGetLastError();
 }
 
+// four waves per workgroup, two workgroups per CU (NH = 1): measured 4 % faster
+// than one 8-wave workgroup per CU at config 2 and 6 % at config 4
+constexpr int kDkdvNH = 1;
 template <int HD, bool AL, int TK>
 static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg,
                       const void* dout, const float* lse, const float* delta, const int32_t* list,
@@ -781,7 +800,8 @@ static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t
   const int Lq = read_lq(d.L);
   const float alpha = read_scale(HD) * kLog2e;
   NAYLIS_TIMED("read_bwd_dkdv", st,
-               hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * (Lq / 128) * nc), dim3(512), 0,
+               hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true, kDkdvNH>), dim3(d.H * (Lq / 128) * nc),
+                                  dim3(256 * kDkdvNH), 0,
                                   st, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
                                   (const bf16_t*)dout, lse, delta, list, count, dkp, dvp, d.order,
                                   (long)d.B * d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc,
