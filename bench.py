@@ -50,6 +50,9 @@ METRIC = "MoM layer fwd+bwd tokens/s at d=1024, 8x128 slots; % bf16 MFMA peak"
 
 WORKLOADS = {
     # B, T, d, heads, blocks, block_size, top_k, rank
+    # config1 (the reference's CPU case): x ~ N(0, 1), bank N(0, 0.02) as drawn
+    "config1": dict(B=2, T=512, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=None, tile_bias=None,
+                    x_rmsnorm=False),
     "config2": dict(B=8, T=2048, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, tile_bias=None),
     "config4": dict(B=4, T=4096, D=1536, H=24, E=32, BS=128, K=2, R=32, bank_fro=None, tile_bias=(3, 6)),
     "config5": dict(B=64, D=1024, H=16, E=8, BS=128, K=2, R=32, bank_fro=63.0, max_prior=4096),
@@ -82,7 +85,8 @@ def build(cfg, device):
     M = M.bfloat16().to(device).requires_grad_(True)
     gx = torch.Generator().manual_seed(1)
     x = torch.randn(B, T, D, generator=gx)
-    x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+    if cfg.get("x_rmsnorm", True):
+        x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
     x = x.bfloat16().to(device).requires_grad_(True)
     gd = torch.Generator().manual_seed(2)
     dy = torch.randn(B, T, D, generator=gd).to(device)  # fp32: the dtype of y (ReZero promotes to fp32)
