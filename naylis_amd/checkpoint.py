@@ -20,7 +20,7 @@ import re
 
 import torch
 
-from .layer import MoMLayer
+from .layer import MoMLayer, cast_mom_layer
 
 __all__ = ["LEGACY_TOP_BLOCKS", "LEGACY_AUX_WEIGHT", "remap_legacy_keys", "mom_kwargs_from_state_dict",
            "mom_layer_indices", "mom_layer_state_dict", "mom_layers_from_state_dict"]
@@ -124,7 +124,10 @@ def mom_layers_from_state_dict(state_dict, hidden_size, n_heads, config=None, pr
 
     Legacy keys are remapped first.  ``strict=True`` raises on any missing or
     unexpected key of a layer, which is the reference's strict check
-    (evaluate.py:187-195) restricted to the MoM read.
+    (evaluate.py:187-195) restricted to the MoM read.  ``dtype`` applies to
+    the q/k/v/o projections and the bank only; the router weights and the
+    ReZero scale stay fp32 (cast_mom_layer), so a layer loaded with
+    dtype=torch.bfloat16 runs the fused HIP node directly.
     """
     state_dict = remap_legacy_keys(state_dict)
     kw = mom_kwargs_from_state_dict(state_dict, hidden_size, config)
@@ -138,8 +141,10 @@ def mom_layers_from_state_dict(state_dict, hidden_size, n_heads, config=None, pr
         layer = MoMLayer(hidden_size, n_heads, kw["mem_size"], kw["mom_block_size"], kw["mom_top_blocks"],
                          kw["mom_router_rank"])
         layer.load_state_dict(mom_layer_state_dict(state_dict, i, prefix), strict=True)
-        if device is not None or dtype is not None:
-            layer = layer.to(device=device, dtype=dtype)
+        if device is not None:
+            layer = layer.to(device=device)
+        if dtype is not None:
+            cast_mom_layer(layer, dtype)
         layers[i] = layer
     bank = bank.detach().clone()
     if device is not None or dtype is not None:

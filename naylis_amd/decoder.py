@@ -34,7 +34,7 @@ from transformers.modeling_outputs import BaseModelOutputWithPast, CausalLMOutpu
 from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaForCausalLM, LlamaModel,
                                                       LlamaRMSNorm)
 
-from .layer import MoMLayer, mom_aux_loss
+from .layer import MoMLayer, cast_mom_layer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm, add_rms_norm
 from .mom_kernels.hip_linear import use_library_wgrad
 from .mom_kernels.hip_mlp import NaylisMLP
@@ -225,7 +225,5 @@ def cast_for_training(model, dtype=torch.bfloat16):
     model.to(dtype)
     for m in model.modules():
         if isinstance(m, MoMLayer):
-            m.router_down.float()
-            m.router_up.float()
-            m.mom_scale.data = m.mom_scale.data.float()
+            cast_mom_layer(m, dtype)
     return model

@@ -32,6 +32,18 @@ from .mom_kernels.hip_layer import fused_layer_supported, mom_layer
 __all__ = ["MoMLayer", "mom_aux_loss"]
 
 
+def cast_mom_layer(layer, dtype):
+    """Cast a MoMLayer for the fused HIP node: the q/k/v/o projections to
+    ``dtype``, the router weights and the ReZero scale kept in fp32 (routing
+    and the prefix mean run in fp32, model.py:169-187)."""
+    for lin in (layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+        lin.to(dtype)
+    layer.router_down.float()
+    layer.router_up.float()
+    layer.mom_scale.data = layer.mom_scale.data.float()
+    return layer
+
+
 class MoMLayer(nn.Module):
     """Mixture-of-Memory read over a shared learnable bank, causal routing."""
 

@@ -166,22 +166,21 @@ def test_state_dict_moves_between_oracle_and_hip_layer():
 @pytest.mark.gpu
 def test_legacy_loaded_layer_output_bitwise(dev):
     """Section 15a of the reference's test on the HIP layer: a layer loaded
-    from the legacy layout gives the bitwise output of the original."""
+    from the legacy layout with dtype=bf16 (no manual casts) gives the bitwise
+    output of the original."""
+    from naylis_amd.layer import cast_mom_layer
     torch.manual_seed(3)
     Dg, Hg = 256, 4
-    orig = MoMLayer(Dg, Hg, 4 * 64, 64, 2, 16).to(dev)
+    orig = cast_mom_layer(MoMLayer(Dg, Hg, 4 * 64, 64, 2, 16).to(dev), torch.bfloat16)
     with torch.no_grad():
         orig.mom_scale.fill_(0.5)
-    for lin in (orig.q_proj, orig.k_proj, orig.v_proj, orig.o_proj):
-        lin.to(torch.bfloat16)
     bank = (torch.randn(4, 64 * Dg, device=dev) * 0.5).bfloat16()
     sd = {"model.M_blocks": bank.cpu()}
     for k, v in orig.state_dict().items():
         sd["model.layers.5.mom." + k] = v.cpu()
-    bank2, layers = ck.mom_layers_from_state_dict(_to_legacy(sd), Dg, Hg, device=dev)
-    for lin in (layers[5].q_proj, layers[5].k_proj, layers[5].v_proj, layers[5].o_proj):
-        lin.to(torch.bfloat16)
+    bank2, layers = ck.mom_layers_from_state_dict(_to_legacy(sd), Dg, Hg, device=dev, dtype=torch.bfloat16)
     assert bank2.dtype == torch.bfloat16 and layers[5].q_proj.weight.dtype == torch.bfloat16
+    assert layers[5].router_down.weight.dtype == torch.float32 and layers[5].mom_scale.dtype == torch.float32
     x = torch.randn(2, 128, Dg, device=dev, dtype=torch.bfloat16)
     orig.eval()
     layers[5].eval()
@@ -190,3 +189,64 @@ def test_legacy_loaded_layer_output_bitwise(dev):
         b = layers[5](x, bank2)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_legacy_checkpoint_file_hip_layer_matches_oracle(dev):
+    """A legacy-layout fp32 checkpoint file (safetensors, the reference's
+    graph_mem / graph_scale names, evaluate.py:198-289) loaded into the HIP
+    layer with dtype=bf16 and into the fp32 oracle layer: forward and
+    backward through the fused node agree at the north-star tolerance,
+    parameter gradients by the reference's scaled_max metric
+    (the oracle sees the bf16-rounded projections and bank the HIP layer
+    holds)."""
+    from safetensors.torch import load_file, save_file
+
+    from naylis_amd.mom_kernels.hip_layer import fused_layer_supported
+    from tests._tol import assert_close, scaled_max
+    Dg, Hg, NBg, BSg, Kg, Rg = 256, 4, 8, 64, 2, 32
+    g = torch.Generator().manual_seed(11)
+    src = oracle.OracleMoMLayer(Dg, Hg, NBg * BSg, BSg, Kg, Rg)
+    with torch.no_grad():
+        for p_ in src.parameters():
+            p_.copy_(torch.randn(p_.shape, generator=g) * 0.05)
+        src.mom_scale.fill_(0.7)
+    sd = {"model.M_blocks": torch.randn(NBg, BSg * Dg, generator=g) * 0.5}
+    for k, v in src.state_dict().items():
+        sd["model.layers.3.mom." + k] = v
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.safetensors")
+        save_file(_to_legacy(sd), path)
+        loaded = load_file(path)
+    bank, layers = ck.mom_layers_from_state_dict(loaded, Dg, Hg, device=dev, dtype=torch.bfloat16)
+    hip = layers[3].train()
+    hip.noise_scale = 0.0
+    assert fused_layer_supported(torch.empty(1, 1, Dg, device=dev, dtype=torch.bfloat16), bank,
+                                 hip.router_down.weight, hip.router_up.weight, hip.q_proj.weight, hip.k_proj.weight,
+                                 hip.v_proj.weight, hip.o_proj.weight, hip.mom_scale)
+    ref = oracle.OracleMoMLayer(Dg, Hg, NBg * BSg, BSg, Kg, Rg)
+    ref.load_state_dict({k: v.detach().float().cpu() for k, v in hip.state_dict().items()}, strict=True)
+    ref.noise_scale = 0.0
+    x = torch.randn(2, 200, Dg, generator=g).bfloat16()
+    dy = torch.randn(2, 200, Dg, generator=g)
+    xd = x.to(dev).requires_grad_(True)
+    bank = bank.detach().requires_grad_(True)
+    y = hip(xd, bank)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    xr = x.float().requires_grad_(True)
+    Mr = bank.detach().float().cpu().requires_grad_(True)
+    yr = ref(xr, Mr)
+    yr.backward(dy)
+    assert_close(y, yr, "y")
+    assert_close(xd.grad, xr.grad, "dx")
+    assert_close(bank.grad, Mr.grad, "dM_blocks")
+    # parameter gradients (sums over all tokens) by the reference's gradient metric, scaled_max =
+    # max|a - b| / max|b| (test_parity.py:64-67, bar 2e-2 at :488-490), at half that bar, and a
+    # relative Frobenius error of at most 1e-2
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "router_down", "router_up"):
+        got = getattr(hip, name).weight.grad.double().cpu()
+        exp = getattr(ref, name).weight.grad.double()
+        sm = scaled_max(got, exp)
+        fro = float((got - exp).norm() / exp.norm().clamp_min(1e-30))
+        assert sm <= 1e-2 and fro <= 1e-2, f"d{name}: scaled_max {sm:.3e}, relative Frobenius {fro:.3e}"
