@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 10
+#define NAYLIS_MOM_ABI_VERSION 11
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -95,6 +95,24 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
                         const void* dout, void* dq, void* dk, void* dv, float* dgates, void* workspace,
                         size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
                         int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
+
+/* The read backward with no workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight training or serving loops, harnesses that forbid
+ * hipMalloc); it allocates nothing.  Same arguments (less the workspace),
+ * results (bitwise) and errors as naylis_mom_read_bwd.  Its workspace is a
+ * scratch array of NAYLIS_READ_BWD_NOALLOC_MAX_BYTES that the library holds
+ * on each device it runs on until the process ends; a read whose
+ * naylis_mom_read_workspace_bytes() exceeds that returns
+ * NAYLIS_ERR_WORKSPACE.  All calls on one device share that array and its
+ * contents: calls that overlap on one GPU (on other streams or threads) race,
+ * and the caller must order them. */
+#define NAYLIS_READ_BWD_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int naylis_mom_read_bwd_noalloc(const void* q, const void* k, const void* v, const int32_t* top_idx,
+                                const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
+                                const void* dout, void* dq, void* dk, void* dv, float* dgates, int64_t B, int64_t S,
+                                int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
+                                void* stream);
 
 /* Token order for the read (no counterpart in the reference, which walks
  * tokens in sequence order with BLOCK_M = 128, triton_gpu.py:50,98): the

@@ -2,15 +2,19 @@
 // Every entry point validates its arguments the way the reference's Python
 // layer raises (mom_kernels/triton_gpu.py:420-429, mom_kernels/__init__.py:
 // 69-79) and returns a status code; no C++ exception crosses the boundary.
-// The library holds no tensors and no mutable global state; the last error
-// message is per calling thread (like errno).
+// The library holds no tensors; its only mutable global state is the
+// per-device scratch array of naylis_mom_read_bwd_noalloc (with the table of
+// its device addresses) and the last error message, which is per calling
+// thread (like errno).
 #include <stdarg.h>
 #include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
-#include <string>
+#include <atomic>
 #include <initializer_list>
+#include <mutex>
+#include <string>
 
 #include "../../include/naylis_mom.h"
 #include "launch.h"
@@ -208,6 +212,68 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   if (rc) return rc;
   return hip_status(launch_read_bwd_reduce(dkp, dvp, dlg, top_gates, dk, dv, dgates, w.n_chunks, d, st),
                     "mom_read_bwd reduce");
+}
+
+// ------------------------------------------- read backward, no allocation
+// The workspace of naylis_mom_read_bwd_noalloc: a file-scope device array
+// that each device the library runs on holds from the code object's load to
+// the end of the process.  In host code its name is not a device address:
+// every host use goes through the address hipGetSymbolAddress returns on the
+// device in question (one per device, looked up once).  Nothing in the read
+// backward's workspace has to start at zero (each word is written before it
+// is read within one call), so calls do not clear it.
+static __device__ __align__(256) unsigned char scratch[NAYLIS_READ_BWD_NOALLOC_MAX_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_addr[kScratchDevices];
+
+// The scratch array's address on the current device.
+int scratch_address(void** out) {
+  int dev = -1;
+  int rc = hip_status(hipGetDevice(&dev), "mom_read_bwd_noalloc: hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(NAYLIS_ERR_ARG, "mom_read_bwd_noalloc: device %d beyond the %d the library tracks", dev,
+                kScratchDevices);
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "mom_read_bwd_noalloc: hipGetSymbolAddress");
+      if (rc) return rc;
+      if (!p) return fail(NAYLIS_ERR_HIP, "mom_read_bwd_noalloc: no device address for the scratch array");
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return NAYLIS_OK;
+}
+
+}  // namespace
+
+int naylis_mom_read_bwd_noalloc(const void* q, const void* k, const void* v, const int32_t* top_idx,
+                                const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
+                                const void* dout, void* dq, void* dk, void* dv, float* dgates, int64_t B, int64_t S,
+                                int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
+                                void* stream) {
+  ReadDims d;
+  int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
+  if (rc) return rc;
+  const size_t need = plan_read_ws(d).total;
+  if (need > NAYLIS_READ_BWD_NOALLOC_MAX_BYTES)
+    return fail(NAYLIS_ERR_WORKSPACE,
+                "mom_read_bwd_noalloc: this read needs %zu bytes of workspace, more than the %zu of the library's "
+                "scratch array; call naylis_mom_read_bwd with a workspace",
+                need, (size_t)NAYLIS_READ_BWD_NOALLOC_MAX_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  return naylis_mom_read_bwd(q, k, v, top_idx, top_gates, token_order, out, lse, dout, dq, dk, dv, dgates, ws,
+                             NAYLIS_READ_BWD_NOALLOC_MAX_BYTES, B, S, H, head_dim, num_blocks, block_size, top_k,
+                             stream);
 }
 
 static int check_order_dims(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k) {

@@ -242,3 +242,15 @@ def test_add_rmsnorm_rejects_bad_arguments(lib):
     assert lib.naylis_mom_add_rmsnorm_fwd(p, p, 1, p, p, p, p, 0, 8, 1024, 1e-5, None) == _lib.NAYLIS_ERR_ARG
     assert lib.naylis_mom_add_rmsnorm_fwd(p, p, 0, p, p, p, p, 1, 8, 1000, 1e-5, None) == _lib.NAYLIS_ERR_ARG  # D
     assert lib.naylis_mom_add_rmsnorm_bwd(p, p, p, p, None, p, p, p, 0, 1, 8, 1024, None) == _lib.NAYLIS_ERR_WORKSPACE
+
+
+def test_read_bwd_noalloc_refuses_before_touching_a_device(lib):
+    """The no-allocation read backward checks shapes and its scratch limit
+    (NAYLIS_READ_BWD_NOALLOC_MAX_BYTES) before any device call."""
+    m = re.search(r"#define NAYLIS_READ_BWD_NOALLOC_MAX_BYTES \(\(size_t\)(\d+) << (\d+)\)", open(HEADER).read())
+    max_bytes = int(m.group(1)) << int(m.group(2))
+    dims = (1, 64, 16, 128, 128, 128, 2)              # 16384 slots of 16 x 128: 256 MiB of dK/dV partials
+    assert lib.naylis_mom_read_workspace_bytes(*dims) > max_bytes
+    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), *dims, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert b"scratch" in lib.naylis_mom_last_error()
+    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), 1, 64, 2, 96, 4, 16, 2, None) == _lib.NAYLIS_ERR_ARG
