@@ -284,14 +284,17 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
 
 // ---------------------------------------------------------------------------
 // Fast forward: head_dim 64, block sizes that are multiples of 32 (every
-// Naylis configuration).  One workgroup = (h, 256 consecutive positions of the
-// token order), 8 waves x 32 tokens (one MFMA column tile each).
+// Naylis configuration).  One workgroup = (h, 128 consecutive positions of the
+// token order), 4 waves x 32 tokens (one MFMA column tile each).
 //
 // The workgroup's active 32-slot chunks (every chunk of every block one of its
-// tokens selects, ascending) pass through LDS in stages of up to 8 chunks (K
-// and V of 256 slots: 72 KiB, two workgroups per CU), so a stage costs one
+// tokens selects, ascending) pass through LDS in stages of up to 4 chunks (K
+// and V of 128 slots: 36 KiB, four workgroups per CU), so a stage costs one
 // barrier pair instead of a barrier per slot group; inside a stage each wave
-// walks the chunks some token of its 32 selects with no barrier.
+// walks the chunks some token of its 32 selects with no barrier.  (Measured on
+// MI355X against 8 waves x 32 tokens with 8-chunk stages: equal at config 2,
+// 17 % faster at config 4, whose sequence-order tiles touch fewer blocks at
+// 128 tokens than at 256.)
 //
 // Softmax: a token's running max m is the exact max of the first chunk it
 // selects and afterwards moves only when a chunk would give it p > 2^64
@@ -327,14 +330,14 @@ __device__ __forceinline__ float add_bf16x8(const bf16x8& p, float acc) {
 }
 
 template <int TK>
-__global__ __launch_bounds__(512, 4) void read_fwd_fast_kernel(
+__global__ __launch_bounds__(256, 4) void read_fwd_fast_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
     float* __restrict__ lse, const int32_t* __restrict__ order, long N, int H, int L, int E, int block_size,
     int topk, float alpha, int n_tiles) {
   constexpr int HD = 64, KS = HD / 16, NO = HD / 32, PITCH = HD + 8;
-  constexpr int NW = 8, NT = 64 * NW, TM = 32 * NW;  // 8 waves x 32 tokens
-  constexpr int SCH = 8;                     // 32-slot chunks per LDS stage
+  constexpr int NW = 4, NT = 64 * NW, TM = 32 * NW;  // 4 waves x 32 tokens
+  constexpr int SCH = 4;                     // 32-slot chunks per LDS stage
   constexpr int TILE = SCH * 32 * PITCH;     // bf16 elements of one staged tensor
   constexpr int PER = SCH * 32 * HD / 8 / NT;  // 16-byte pieces per thread per tensor
   static_assert(PER * NT * 8 == SCH * 32 * HD, "stage copy must tile the workgroup");
@@ -523,10 +526,10 @@ template <int TK>
 static void fwd_fast_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, void* out,
                           float* lse, const ReadDims& d, hipStream_t st) {
   const long N = (long)d.B * d.S;
-  const int n_tiles = (int)((N + 255) / 256);
+  const int n_tiles = (int)((N + 127) / 128);
   const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL((read_fwd_fast_kernel<TK>), dim3(d.H * n_tiles), dim3(512), 0, st,
+               hipLaunchKernelGGL((read_fwd_fast_kernel<TK>), dim3(d.H * n_tiles), dim3(256), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (bf16_t*)out, lse,
                                   d.order, N, d.H, d.L, d.E, d.block_size, d.topk, alpha, n_tiles));
 }
