@@ -284,6 +284,233 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fast dQ: head_dim 64, block sizes that are multiples of 32 (every Naylis
+// configuration).  Same work and outputs as read_bwd_dq_kernel, organised as
+// the fast forward: the tile's active 32-slot chunks (ascending) pass through
+// LDS in stages of up to 4 chunks (K and V of 128 slots, 36 KiB), all of a
+// stage's loads in flight at once and one barrier pair per stage; inside a
+// stage each wave walks the chunks some token of its 32 selects with no
+// barrier.  A chunk never spans two blocks, so its gate bias is one value per
+// token.  At top-2 the kernel fits 168 VGPRs, so three workgroups share a CU
+// (measured on MI355X: 8 % faster than 64-slot groups with one group of
+// prefetch at config 2, 11 % at config 4; 8-chunk stages at two workgroups
+// per CU were no faster than those groups).
+template <int TK>
+__global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
+    const bf16_t* __restrict__ dout, const float* __restrict__ lse, bf16_t* __restrict__ dq,
+    float* __restrict__ delta, float* __restrict__ dlg_part, const int32_t* __restrict__ order, long N, int H,
+    int L, int E, int block_size, int topk, float alpha, float scale, int n_tiles) {
+  constexpr int HD = 64, KS = HD / 16, NO = HD / 32, PITCH = HD + 8;
+  constexpr int NT = 256;
+  constexpr int SCH = 4;                       // 32-slot chunks per LDS stage
+  constexpr int TILE = SCH * 32 * PITCH;       // bf16 elements of one staged tensor
+  constexpr int PER = SCH * 32 * HD / 8 / NT;  // 16-byte pieces per thread per tensor
+  static_assert(PER * NT * 8 == SCH * 32 * HD, "stage copy must tile the workgroup");
+
+  __shared__ __attribute__((aligned(16))) bf16_t k_lds[TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t v_lds[TILE];
+  __shared__ uint8_t flags[kMaxBlocks];
+  __shared__ uint32_t chunks[kMaxGroups];  // (block << 16) | chunk index (slot / 32)
+  __shared__ int n_chunks_s;
+
+  const int G = H * n_tiles;
+  const int wid = xcd_remap(blockIdx.x, G);
+  const int tile = wid % n_tiles;
+  const int h = wid / n_tiles;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const long pos = (long)tile * 128 + wave * 32 + col;  // position in the token order
+  const bool tok_ok = pos < N;
+  const int32_t* ord = order_table(order);
+  const long tok = tok_ok ? order_token(ord, pos, N) : 0;  // flattened b*S + s
+  const int D = H * HD;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(k, (uint32_t)L * (uint32_t)D * 2u);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v, (uint32_t)L * (uint32_t)D * 2u);
+  const int hoff = h * HD * 2;  // byte offset of head h in a row
+
+  TokenRoute<TK> rt;
+  load_route<TK>(rt, top_idx, top_gates, tok, tok_ok, topk);
+  bf16x8 qf[KS], df[KS], of[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (tok_ok) {
+      const long off = tok * D + (long)h * HD + 16 * ks + 8 * g;
+      qf[ks] = *reinterpret_cast<const bf16x8*>(q + off);
+      df[ks] = *reinterpret_cast<const bf16x8*>(dout + off);
+      of[ks] = *reinterpret_cast<const bf16x8*>(o + off);
+    } else {
+      qf[ks] = bf16x8{};
+      df[ks] = bf16x8{};
+      of[ks] = bf16x8{};
+    }
+  }
+  const float lse_t = tok_ok ? lse[(long)h * N + tok] : 0.f;
+
+  // ---- the tile's active chunks, ascending
+  for (int e = tid; e < E; e += NT) flags[e] = 0;
+  lds_barrier();
+  if (g == 0 && tok_ok) {
+#pragma unroll
+    for (int t = 0; t < TK; ++t)
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+  }
+  lds_barrier();
+  if (wave == 0) {
+    const int cpb = block_size >> 5;  // chunks per block
+    int total = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + lane;
+      const bool act = e < E && flags[e] != 0;
+      const unsigned long long m = __ballot(act);
+      if (act) {
+        const int p0 = (total + __popcll(m & ((1ull << lane) - 1ull))) * cpb;
+        for (int j = 0; j < cpb; ++j) chunks[p0 + j] = ((uint32_t)e << 16) | (uint32_t)(e * cpb + j);
+      }
+      total += __popcll(m);
+    }
+    if (lane == 0) n_chunks_s = total * cpb;
+  }
+
+  // delta0 = rowsum(o * do) from the rows loaded above
+  float dl = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dl = fmaf((float)of[ks][e], (float)df[ks][e], dl);
+  dl = wave_sum_pair(dl);
+
+  f32x16 acc_dq[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) acc_dq[j] = f32x16{};
+  // dlog_gates without the bf16 rounding of o inside delta: per selection t
+  // accumulate A_t = sum_{n in block t} P dP and M_t = sum_{n in block t} P,
+  // plus dx = sum_n P dP (= the exact delta); then dlog_t = A_t - dx * M_t.
+  float accA[TK], accM[TK];
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    accA[t] = 0.f;
+    accM[t] = 0.f;
+  }
+  float dx = 0.f;
+  lds_barrier();
+  const int n_ch = n_chunks_s;
+
+  for (int s0 = 0; s0 < n_ch; s0 += SCH) {
+    const int nst = min(SCH, n_ch - s0);
+    if (s0 > 0) lds_barrier();  // every wave is done with the previous stage
+    {
+      uint4 kr[PER], vr[PER];
+#pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        const int p = tid + NT * r;
+        const int row = p >> 3, c8 = p & 7, ch = row >> 5;
+        // rows of chunks beyond the stage read past the buffer's end, which
+        // a buffer load returns as zeros
+        const uint32_t slot = ch < nst ? (chunks[s0 + ch] & 0xffffu) * 32u + (uint32_t)(row & 31) : (uint32_t)L;
+        const uint32_t off = (slot * (uint32_t)D + 8u * (uint32_t)c8) * 2u;
+        kr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, hoff, 0));
+        vr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, hoff, 0));
+      }
+#pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        const int p = tid + NT * r;
+        const int row = p >> 3, c8 = p & 7;
+        *reinterpret_cast<uint4*>(&k_lds[row * PITCH + 8 * c8]) = kr[r];
+        *reinterpret_cast<uint4*>(&v_lds[row * PITCH + 8 * c8]) = vr[r];
+      }
+    }
+    // chunks of this stage that some token of the wave selects
+    unsigned mine = 0;
+    for (int c = 0; c < nst; ++c) {
+      const int e = (int)(chunks[s0 + c] >> 16);
+      bool sel = false;
+#pragma unroll
+      for (int t = 0; t < TK; ++t) sel |= t < topk && rt.idx[t] == e;
+      if (__any(sel)) mine |= 1u << c;
+    }
+    lds_barrier();
+
+    while (mine) {
+      const int c = __builtin_ctz(mine);
+      mine &= mine - 1;
+      // S^T = K Q^T and dP^T = V dO^T for the chunk's 32 slots x the wave's 32 tokens
+      f32x16 acc_s = f32x16{}, acc_p = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (32 * c + col) * PITCH + 16 * ks + 8 * g;
+        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(&k_lds[off]);
+        const bf16x8 av = *reinterpret_cast<const bf16x8*>(&v_lds[off]);
+        acc_s = mfma32(ak, qf[ks], acc_s);
+        acc_p = mfma32(av, df[ks], acc_p);
+      }
+      const int e = (int)(chunks[s0 + c] >> 16);
+      bool sel;
+      const float c2 = route_bias<TK>(rt, e, topk, sel);
+      const float add = sel ? c2 - lse_t : -INFINITY;
+      float rsA = 0.f, rsM = 0.f;
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, add));
+        const float dp = acc_p[vv];
+        acc_s[vv] = p * (dp - dl);
+        rsA = fmaf(p, dp, rsA);
+        rsM += p;
+      }
+      dx += rsA;
+#pragma unroll
+      for (int t = 0; t < TK; ++t)
+        if (t < topk && rt.idx[t] == e) {
+          accA[t] += rsA;
+          accM[t] += rsM;
+        }
+      // dQ^T += K^T . dS^T  (K^T read transposed from the natural K rows)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8 bs = pack8(acc_s, 8 * kk);
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+          const bf16x8 a = lds_frag_T<true, true>(k_lds, PITCH, 32 * c + 16 * kk, 32 * j);
+          acc_dq[j] = mfma32(a, bs, acc_dq[j]);
+        }
+      }
+    }
+  }
+
+  dx = wave_sum_pair(dx);
+  float dlg[TK];
+#pragma unroll
+  for (int t = 0; t < TK; ++t) dlg[t] = wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t]);
+
+  if (tok_ok) {
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int f0 = 32 * j + 16 * g;
+      bf16x8 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lo[e] = (__bf16)(acc_dq[j][e] * scale);
+        hi[e] = (__bf16)(acc_dq[j][8 + e] * scale);
+      }
+      bf16_t* dst = dq + tok * D + (long)h * HD + f0;
+      *reinterpret_cast<bf16x8*>(dst) = lo;
+      *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+    }
+    if (g == 0) {
+      delta[(long)h * N + tok] = dx;
+#pragma unroll
+      for (int t = 0; t < TK; ++t)
+        if (t < topk) dlg_part[((long)h * N + tok) * topk + t] = dlg[t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Active 64-token tiles per 128-slot group.
 constexpr int kDkdvTile = 64;
 
@@ -732,6 +959,19 @@ template <int HD, int TK>
 static void dq_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
                    const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
                    hipStream_t st) {
+  if constexpr (HD == 64) {
+    if (d.block_size % 32 == 0) {  // the staged kernel (every Naylis configuration)
+      const long N = (long)d.B * d.S;
+      const int n_tiles = (int)((N + 127) / 128);
+      const float scale = read_scale(HD);
+      NAYLIS_TIMED("read_bwd_dq", st,
+                   hipLaunchKernelGGL((read_bwd_dq_fast_kernel<TK>), dim3(d.H * n_tiles), dim3(256), 0, st,
+                                      (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
+                                      (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.order,
+                                      N, d.H, d.L, d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
+      return;
+    }
+  }
   constexpr int SGMAX = HD <= 64 ? 64 : 32;
   if (d.block_size % SGMAX == 0)
     dq_inst<HD, SGMAX, true, TK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
