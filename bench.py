@@ -404,7 +404,9 @@ def decoder_bench(args, cfg, dev):
     model = NaylisLlamaForCausalLM(mcfg)
     state_fp32 = None if args.no_cpu_baseline else {k: v.detach().clone() for k, v in model.state_dict().items()}
     model = cast_for_training(model).to(dev).train()
-    model.set_noise_scale(0.0)
+    # router noise on, as the reference trains until its noise cutoff (pretrain.py:515-535): each MoM
+    # layer draws its (B, T, E) uniform and the router kernel applies the Gumbel transform
+    model.set_noise_scale(1.0)
     ids = torch.randint(0, cfg["vocab"], (B, T), generator=torch.Generator().manual_seed(1)).to(dev)
 
     def step():
@@ -428,17 +430,14 @@ def decoder_bench(args, cfg, dev):
     kernels = _lib.KernelTimer.results()
     per = {k: (v[0] / v[1], v[1] / args.steps) for k, v in kernels.items() if v[1]}
 
-    # routing of every MoM layer for one forward: capture each layer's input
-    inputs = {}
-    hooks = [m.register_forward_hook(lambda mod, a, out, key=i: inputs.__setitem__(key, a[0].detach()))
-             for i, m in enumerate(x for x in model.modules() if isinstance(x, MoMLayer))]
+    # routing of every MoM layer for one forward (without labels the layers keep it)
     with torch.no_grad():
-        model(input_ids=ids, labels=ids)
-    for h in hooks:
-        h.remove()
+        model(input_ids=ids)
     A_total = 0
-    for i, m in enumerate(x for x in model.modules() if isinstance(x, MoMLayer)):
-        A_total += active_tiles(routing(m, model.model.M_blocks, inputs[i]), E)
+    for m in (x for x in model.modules() if isinstance(x, MoMLayer)):
+        # the routing this forward drew (with its Gumbel noise): the timed steps draw their own,
+        # of the same distribution
+        A_total += active_tiles(m.last_top_idx.view(B, T, -1), E)
     read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce_kv", "read_bwd_reduce_gates")
     read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
     read_flop = 14.0 * D * BS * 128 * A_total
@@ -475,11 +474,11 @@ def decoder_bench(args, cfg, dev):
         "data": "synthetic (random-init weights, token ids uniform over the vocabulary)",
         "config": {"workload": f"config3: Naylis decoder fwd+bwd, {cfg['layers']} layers d={D} heads={H}x{D // H} "
                                f"SwiGLU {cfg['ffn']} vocab {cfg['vocab']}, shared bank {E}x{BS} top-{cfg['K']} "
-                               f"rank {cfg['R']}, CE + 0.01 aux",
+                               f"rank {cfg['R']}, CE + 0.01 aux, router Gumbel noise scale 1.0",
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
         "roofline": roof,
         "model": {"flop_per_step": model_flop, "tflops": round(model_tf, 1),
-                  "mfma_frac": round(model_tf / PEAK_BF16_TFLOPS, 4), "loss": round(float(loss), 4)},
+                  "mfma_frac": round(model_tf / PEAK_BF16_TFLOPS, 4), "loss": round(float(loss.detach()), 4)},
         "read": {"active_tile_blocks_all_layers": A_total, "alg_flop": read_flop, "ms": round(read_ms, 4),
                  "tflops": round(read_tf, 2), "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},

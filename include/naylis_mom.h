@@ -254,9 +254,11 @@ int naylis_mom_swiglu_bwd(const void* gate, const void* up, const void* dh, void
  * The LM head loss of the decoder (model.py:536-545: F.cross_entropy of the
  * fp32 logits, reduction "sum", ignore_index) from bf16 logits (N, V) in one
  * pass: the forward writes each row's loss (log-sum-exp minus the label's
- * logit; 0 for rows labelled ignore_index) and its log-sum-exp; the backward
- * writes dlogits (N, V) bf16 = (softmax - one_hot(label)) * grad_rows[r *
- * grad_stride] (grad_stride 1: one gradient per row, 0: one for all rows).
+ * logit; 0 for rows labelled ignore_index; NaN for a label outside [0, V),
+ * where the reference raises) and its log-sum-exp; the backward writes
+ * dlogits (N, V) bf16 = (softmax - one_hot(label)) * grad_rows[r *
+ * grad_stride] (grad_stride 1: one gradient per row, 0: one for all rows;
+ * zero rows for ignore_index, NaN rows for out-of-range labels).
  * V a multiple of 2048; labels int64; logits / dlogits 16-byte aligned. */
 int naylis_mom_xent_fwd(const void* logits, const int64_t* labels, float* loss_rows, float* lse, int64_t N, int64_t V,
                         int64_t ignore_index, void* stream);

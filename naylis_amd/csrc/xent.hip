@@ -55,8 +55,10 @@ __global__ __launch_bounds__(256) void xent_fwd_kernel(const bf16_t* __restrict_
   s = wg_reduce(s, red, [](float a, float b) { return a + b; });
   if (threadIdx.x == 0) {
     const float lse = mx + logf(s);
-    const bool valid = lab != ignore_index && lab >= 0 && lab < V;
-    loss[row] = valid ? lse - bf16_to_f32(x[valid ? lab : 0]) : 0.f;
+    // a label that is neither ignore_index nor a class gives a NaN loss (the
+    // reference's F.cross_entropy raises on it): bad data cannot pass silently
+    const bool in_range = lab >= 0 && lab < V;
+    loss[row] = lab == ignore_index ? 0.f : in_range ? lse - bf16_to_f32(x[in_range ? lab : 0]) : __builtin_nanf("");
     lse_out[row] = lse;
   }
 }
@@ -71,8 +73,8 @@ __global__ __launch_bounds__(256) void xent_bwd_kernel(const bf16_t* __restrict_
   const bf16_t* x = logits + row * (long)V;
   bf16_t* dx = dlogits + row * (long)V;
   const long lab = labels[row];
-  const bool valid = lab != ignore_index && lab >= 0 && lab < V;
-  const float gr = valid ? g[row * g_stride] : 0.f;
+  // ignore_index rows get a zero gradient, out-of-range labels a NaN one
+  const float gr = lab == ignore_index ? 0.f : (lab >= 0 && lab < V) ? g[row * g_stride] : __builtin_nanf("");
   const float l = lse[row];
   for (int j = threadIdx.x * 8; j < V; j += 2048) {
     const uint4 u = *reinterpret_cast<const uint4*>(x + j);

@@ -6,6 +6,9 @@ log_softmax and the label pick, and the same passes backward.
 ``cross_entropy_rows`` reads the bf16 logits once forward and once backward
 and returns each row's loss (0 for ignore_index rows); summing and dividing
 by the number of valid labels stays with the caller, as in the reference.
+A label outside [0, V) that is not ignore_index, which F.cross_entropy
+rejects with an error, gives that row a NaN loss and NaN gradient, so the
+summed loss shows it instead of dropping the row silently.
 """
 from __future__ import annotations
 

@@ -34,6 +34,30 @@ def test_xent_matches_cross_entropy(N, V, dev):
     assert bool((lg.grad[labels == -100] == 0).all())
 
 
+def test_xent_out_of_range_label_is_nan(dev):
+    """A label outside [0, V) that is not ignore_index (F.cross_entropy
+    raises on it) makes that row's loss and gradient NaN; the other rows are
+    unaffected, so the summed loss is NaN rather than silently smaller."""
+    from naylis_amd.mom_kernels.hip_xent import cross_entropy_rows
+    g = torch.Generator().manual_seed(3)
+    N, V = 6, 2048
+    logits = (torch.randn(N, V, generator=g) * 4).bfloat16().to(dev)
+    labels = torch.randint(0, V, (N,), generator=g)
+    labels[1], labels[4] = V, -100                       # one out of range, one ignored
+    labels = labels.to(dev)
+    lg = logits.clone().requires_grad_(True)
+    rows = cross_entropy_rows(lg, labels)
+    rows.sum().backward()
+    torch.cuda.synchronize()
+    assert torch.isnan(rows[1]) and torch.isnan(rows.sum())
+    assert float(rows[4]) == 0.0
+    ok = torch.tensor([0, 2, 3, 5], device=dev)
+    want = F.cross_entropy(logits[ok].float(), labels[ok], reduction="none")
+    assert torch.allclose(rows[ok], want, rtol=1e-5, atol=1e-5)
+    assert bool(torch.isnan(lg.grad[1]).all()) and bool((lg.grad[4] == 0).all())
+    assert bool(torch.isfinite(lg.grad[ok]).all())
+
+
 def test_xent_rejects_unsupported(dev):
     from naylis_amd.mom_kernels.hip_xent import cross_entropy_rows
     with pytest.raises(RuntimeError, match="multiple of"):
