@@ -22,6 +22,9 @@ def build(dev):
     layer = layer.to(dev)
     for lin in (layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
         lin.to(torch.bfloat16)
+    # no router noise: each forward (and each replay) would otherwise draw its own uniform sample
+    # and route differently from the eager reference
+    layer.noise_scale = 0.0
     g = torch.Generator().manual_seed(4)
     M = (torch.randn(E, BS * D, generator=g) * 0.3).bfloat16().to(dev).requires_grad_(True)
     x = torch.randn(B, T, D, generator=g).bfloat16().to(dev).requires_grad_(True)
