@@ -438,7 +438,7 @@ def decoder_bench(args, cfg, dev):
         # the routing this forward drew (with its Gumbel noise): the timed steps draw their own,
         # of the same distribution
         A_total += active_tiles(m.last_top_idx.view(B, T, -1), E)
-    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce_kv", "read_bwd_reduce_gates")
+    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce")
     read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
     read_flop = 14.0 * D * BS * 128 * A_total
     read_tf = read_flop / (read_ms * 1e-3) / 1e12
@@ -560,7 +560,7 @@ def main(argv=None):
     # the roofline is the read itself (the north-star path): its kernels, one launch each per step,
     # priced on the 14-unit basis (forward 2 products, backward 5, 2 flop per multiply-add) over
     # their summed durations
-    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce_kv", "read_bwd_reduce_gates")
+    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce")
     read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
     read_flop = 14.0 * D * BS * 128 * A
     read_tf = read_flop / (read_ms * 1e-3) / 1e12

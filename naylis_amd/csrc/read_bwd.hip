@@ -18,9 +18,9 @@
 //     stay in registers;
 //     S, dP, dS per tile, dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
 //     read transposed from the natural-layout tiles; fp32 partials per share.
-//  4. read_bwd_reduce kernels — partials summed over shares in a fixed order
-//     (dk scaled), per-head dlog partials summed over heads and mapped to
-//     d(top_gates) through log(max(g, 1e-9)).
+//  4. read_bwd_reduce_kernel — one launch: partials summed over shares in a
+//     fixed order (dk scaled), per-head dlog partials summed over heads and
+//     mapped to d(top_gates) through log(max(g, 1e-9)).
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
@@ -905,11 +905,15 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
   }
 }
 
+// One launch for both reductions of the backward: workgroups [0, kv_blocks)
+// sum the dK/dV partials, the rest the per-head dlog partials.
+//
 // dk/dv = sum over shares (fixed order) of the fp32 partials; dk scaled.
-__global__ void read_bwd_reduce_kv_kernel(const float* __restrict__ dk_part, const float* __restrict__ dv_part,
-                                          bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long n, long stride,
-                                          int n_chunks, float scale) {
-  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n / 4; i += (long)gridDim.x * blockDim.x) {
+__device__ __forceinline__ void read_bwd_reduce_kv(const float* __restrict__ dk_part,
+                                                   const float* __restrict__ dv_part, bf16_t* __restrict__ dk,
+                                                   bf16_t* __restrict__ dv, long n, long stride, int n_chunks,
+                                                   float scale, long blk, long nblk) {
+  for (long i = blk * (long)blockDim.x + threadIdx.x; i < n / 4; i += nblk * blockDim.x) {
     f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c < n_chunks; ++c) {
       sk += *reinterpret_cast<const f32x4*>(dk_part + c * stride + 4 * i);
@@ -928,14 +932,26 @@ __global__ void read_bwd_reduce_kv_kernel(const float* __restrict__ dk_part, con
 
 // d(top_gates) = (sum_h dlog partial) / g  where g >= 1e-9, else 0
 // (the gradient of log(clamp_min(g, 1e-9)), triton_gpu.py:435).
-__global__ void read_bwd_reduce_gates_kernel(const float* __restrict__ dlg_part, const float* __restrict__ top_gates,
-                                             float* __restrict__ dgates, long n, int H) {
-  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+__device__ __forceinline__ void read_bwd_reduce_gates(const float* __restrict__ dlg_part,
+                                                      const float* __restrict__ top_gates,
+                                                      float* __restrict__ dgates, long n, int H, long blk, long nblk) {
+  for (long i = blk * (long)blockDim.x + threadIdx.x; i < n; i += nblk * blockDim.x) {
     float s = 0.f;
     for (int h = 0; h < H; ++h) s += dlg_part[(long)h * n + i];
     const float gt = top_gates[i];
     dgates[i] = gt >= 1e-9f ? s / gt : 0.f;
   }
+}
+
+__global__ __launch_bounds__(256) void read_bwd_reduce_kernel(
+    const float* __restrict__ dk_part, const float* __restrict__ dv_part, bf16_t* __restrict__ dk,
+    bf16_t* __restrict__ dv, long n, long stride, int n_chunks, float scale, int kv_blocks,
+    const float* __restrict__ dlg_part, const float* __restrict__ top_gates, float* __restrict__ dgates, long ng,
+    int H) {
+  if ((int)blockIdx.x < kv_blocks)
+    read_bwd_reduce_kv(dk_part, dv_part, dk, dv, n, stride, n_chunks, scale, blockIdx.x, kv_blocks);
+  else
+    read_bwd_reduce_gates(dlg_part, top_gates, dgates, ng, H, blockIdx.x - kv_blocks, gridDim.x - kv_blocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -1086,17 +1102,13 @@ hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, co
   const long stride = (long)read_lq(d.L) * D;
   long blocks = (n / 4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  NAYLIS_TIMED("read_bwd_reduce_kv", st,
-               hipLaunchKernelGGL(read_bwd_reduce_kv_kernel, dim3((int)blocks), dim3(256), 0, st, dk_part, dv_part,
-                                  (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD)));
   const long ng = (long)d.B * d.S * d.topk;
-  if (ng > 0) {
-    long gb = (ng + 255) / 256;
-    if (gb > 8192) gb = 8192;
-    NAYLIS_TIMED("read_bwd_reduce_gates", st,
-                 hipLaunchKernelGGL(read_bwd_reduce_gates_kernel, dim3((int)gb), dim3(256), 0, st, dlg_part, top_gates,
-                                    dgates, ng, d.H));
-  }
+  long gb = (ng + 255) / 256;
+  if (gb > 8192) gb = 8192;
+  NAYLIS_TIMED("read_bwd_reduce", st,
+               hipLaunchKernelGGL(read_bwd_reduce_kernel, dim3((int)(blocks + gb)), dim3(256), 0, st, dk_part, dv_part,
+                                  (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD), (int)blocks,
+                                  dlg_part, top_gates, dgates, ng, d.H));
   return hipGetLastError();
 }
 

@@ -699,15 +699,23 @@ __global__ __launch_bounds__(256) void router_bwd_dx_kernel(const XT* __restrict
   }
 }
 
-// Fixed-order reduction of per-chunk partials: out[i] = sum_c part[c][i].
-// Block = 64 outputs x 4 interleaved partial groups; group g sums partials
-// c = g, g+4, g+8, ... in ascending order (loads batched 8 at a time), then
-// the 4 group sums are added in a fixed order.
-__global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                            long n, int n_parts) {
+// The router backward's weight gradients from their fp32 partials, both in one
+// launch: workgroups [0, blocks_a) reduce job a (dW_down), the rest job b
+// (dW_up).  out[i] = sum over parts of part[p][i]: four lane groups take every
+// fourth part in order, then their sums are added in group order, so the
+// result does not depend on scheduling.
+__global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restrict__ part_a, float* __restrict__ out_a,
+                                                             long n_a, int parts_a, int blocks_a,
+                                                             const float* __restrict__ part_b, float* __restrict__ out_b,
+                                                             long n_b, int parts_b) {
   __shared__ float grp_sum[4][64];
+  const bool a = (int)blockIdx.x < blocks_a;
+  const float* part = a ? part_a : part_b;
+  float* out = a ? out_a : out_b;
+  const long n = a ? n_a : n_b;
+  const int n_parts = a ? parts_a : parts_b;
   const int o = threadIdx.x & 63, gq = threadIdx.x >> 6;
-  const long i = (long)blockIdx.x * 64 + o;
+  const long i = (long)(a ? blockIdx.x : blockIdx.x - blocks_a) * 64 + o;
   float s = 0.f;
   if (i < n) {
     int c = gq;
@@ -723,6 +731,14 @@ __global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restr
   grp_sum[gq][o] = s;
   __syncthreads();
   if (gq == 0 && i < n) out[i] = ((grp_sum[0][o] + grp_sum[1][o]) + grp_sum[2][o]) + grp_sum[3][o];
+}
+
+static void launch_router_reduce2(const float* dwd_part, float* dw_down, long nwd, int parts_d, const float* dwup_part,
+                                  float* dw_up, long nwu, int parts_u, hipStream_t st) {
+  const int bd = (int)((nwd + 63) / 64), bu = (int)((nwu + 63) / 64);
+  NAYLIS_TIMED("router_reduce", st,
+               hipLaunchKernelGGL(router_reduce_kernel, dim3(bd + bu), dim3(256), 0, st, dwd_part, dw_down, nwd,
+                                  parts_d, bd, dwup_part, dw_up, nwu, parts_u));
 }
 
 // ---------------------------------------------------------------------------
@@ -861,10 +877,7 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
   const long nwd = (long)d.R * d.D;
   const long nwu = (long)d.E * d.R;
   if (ntok == 0) {  // no tokens: the weight gradients are zero
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)),
-                       dim3(256), 0, st, dwd_part, dw_down, nwd, 0));
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,
-                       0));
+    launch_router_reduce2(dwd_part, dw_down, nwd, 0, dwup_part, dw_up, nwu, 0, st);
     return hipGetLastError();
   }
   const bool fast = router_fast_bwd_ok(x, x_bf16, dx, d);
@@ -872,11 +885,8 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
     const int n_up = launch_router_fast_scan(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf,
                                              (double*)(base + w.scan_csum), wt, dwup_part, d, st);
     launch_router_fast_dx(x, wt, w_down, dx_accumulate ? dx : nullptr, dx, dwd_part, d, st);
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)),
-                                                         dim3(256), 0, st, dwd_part, dw_down, nwd,
-                                                         (int)((ntok + kDxRange - 1) / kDxRange)));
-    NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)),
-                                                         dim3(256), 0, st, dwup_part, dw_up, nwu, n_up));
+    launch_router_reduce2(dwd_part, dw_down, nwd, (int)((ntok + kDxRange - 1) / kDxRange), dwup_part, dw_up, nwu,
+                          n_up, st);
     return hipGetLastError();
   }
   if (d.E <= 8 && d.topk <= 2)
@@ -901,10 +911,7 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
   else
     bwd_dx<float>(x, wt, w_down, dx, dwd_part, d, st);
   const int n_dx_chunks = (int)((ntok + kDxRange - 1) / kDxRange);  // both paths: 256-token ranges
-  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwd + 63) / 64)), dim3(256),
-                     0, st, dwd_part, dw_down, nwd, n_dx_chunks));
-  NAYLIS_TIMED("router_reduce", st, hipLaunchKernelGGL(router_reduce_kernel, dim3((int)((nwu + 63) / 64)), dim3(256), 0, st, dwup_part, dw_up, nwu,
-                     n_tok_blocks));
+  launch_router_reduce2(dwd_part, dw_down, nwd, n_dx_chunks, dwup_part, dw_up, nwu, n_tok_blocks, st);
   return hipGetLastError();
 }
 
