@@ -59,11 +59,14 @@ using CfgTiny = GemmCfg<2, 2, 1, 1>;
 
 // LDS pitches: a [row][k] tile row is 64 + 8 elements (36 dwords: eight
 // consecutive rows' 16-byte reads hit distinct banks); a [k][row] tile row
-// is ROWS + 16 elements (== 8 dwords mod 64: the 4 rows of a transposing
-// read hit distinct banks).
+// is ROWS + 32 elements (16 dwords mod 32).  Measured on MI355X for the
+// transposed fragment reads below (two ds_read_b64_tr_b16 each, 16 waves per
+// CU): 128-row tiles 173 B/clk/CU at pitch 160 against 111 at 144 and
+// 113 - 117 at 152, 176, 192; 64-row tiles 182 at 96 against 118 - 121 at
+// 72, 80, 88, 104, 112.
 template <bool KC, int ROWS>
 struct TileShape {
-  static constexpr int PITCH = KC ? kGK + 8 : ROWS + 16;
+  static constexpr int PITCH = KC ? kGK + 8 : ROWS + 32;
   static constexpr int ELEMS = KC ? ROWS * PITCH : kGK * PITCH;
 };
 
