@@ -109,14 +109,17 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
   for (int j = 0; j < NO; ++j) acc_dq[j] = f32x16{};
   // dlog_gates without the bf16 rounding of o inside delta: per selection t
   // accumulate A_t = sum_{n in block t} P dP and M_t = sum_{n in block t} P,
-  // plus dx = sum_n P dP (= the exact delta); then dlog_t = A_t - dx * M_t.
+  // plus dx = sum_n P dP and S = sum_n P over every selected slot.  P is
+  // recomputed from the forward's lse, so S = 1 only up to the rounding of
+  // the forward's row sum; dividing by S makes the weights exactly
+  // normalised: delta = dx / S and dlog_t = A_t / S - delta M_t / S.
   float accA[TK], accM[TK];
 #pragma unroll
   for (int t = 0; t < TK; ++t) {
     accA[t] = 0.f;
     accM[t] = 0.f;
   }
-  float dx = 0.f;
+  float dx = 0.f, sp = 0.f;
 
   lds_barrier();
   const int n_act = n_active;
@@ -210,6 +213,7 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
           rsM += p;
         }
       dx += rsA;
+      sp += rsM;
 #pragma unroll
       for (int t = 0; t < TK; ++t)
         if (t < topk && rt.idx[t] == e) {
@@ -231,6 +235,7 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
           acc_s[i][vv] = p * (dp - dl);
           const float pdp = p * dp;
           dx += pdp;
+          sp += p;
 #pragma unroll
           for (int t = 0; t < TK; ++t)
             if (t < topk && rt.idx[t] == e) {
@@ -252,10 +257,12 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dq_kernel(
     }
   }
 
-  dx = wave_sum_pair(dx);
+  sp = wave_sum_pair(sp);
+  const float inv_sp = sp > 0.f ? 1.f / sp : 0.f;
+  dx = wave_sum_pair(dx) * inv_sp;  // delta of the normalised weights
   float dlg[TK];
 #pragma unroll
-  for (int t = 0; t < TK; ++t) dlg[t] = wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t]);
+  for (int t = 0; t < TK; ++t) dlg[t] = (wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t])) * inv_sp;
 
   if (tok_ok) {
 #pragma unroll
@@ -390,14 +397,17 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
   for (int j = 0; j < NO; ++j) acc_dq[j] = f32x16{};
   // dlog_gates without the bf16 rounding of o inside delta: per selection t
   // accumulate A_t = sum_{n in block t} P dP and M_t = sum_{n in block t} P,
-  // plus dx = sum_n P dP (= the exact delta); then dlog_t = A_t - dx * M_t.
+  // plus dx = sum_n P dP and S = sum_n P over every selected slot.  P is
+  // recomputed from the forward's lse, so S = 1 only up to the rounding of
+  // the forward's row sum; dividing by S makes the weights exactly
+  // normalised: delta = dx / S and dlog_t = A_t / S - delta M_t / S.
   float accA[TK], accM[TK];
 #pragma unroll
   for (int t = 0; t < TK; ++t) {
     accA[t] = 0.f;
     accM[t] = 0.f;
   }
-  float dx = 0.f;
+  float dx = 0.f, sp = 0.f;
   lds_barrier();
   const int n_ch = n_chunks_s;
 
@@ -463,6 +473,7 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
         rsM += p;
       }
       dx += rsA;
+      sp += rsM;
 #pragma unroll
       for (int t = 0; t < TK; ++t)
         if (t < topk && rt.idx[t] == e) {
@@ -482,10 +493,12 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
     }
   }
 
-  dx = wave_sum_pair(dx);
+  sp = wave_sum_pair(sp);
+  const float inv_sp = sp > 0.f ? 1.f / sp : 0.f;
+  dx = wave_sum_pair(dx) * inv_sp;  // delta of the normalised weights
   float dlg[TK];
 #pragma unroll
-  for (int t = 0; t < TK; ++t) dlg[t] = wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t]);
+  for (int t = 0; t < TK; ++t) dlg[t] = (wave_sum_pair(accA[t]) - dx * wave_sum_pair(accM[t])) * inv_sp;
 
   if (tok_ok) {
 #pragma unroll

@@ -296,10 +296,10 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
 // 17 % faster at config 4, whose sequence-order tiles touch fewer blocks at
 // 128 tokens than at 256.)
 //
-// Softmax: a token's running max m is the exact max of the first chunk it
-// selects and afterwards moves only when a chunk would give it p > 2^64
-// (p <= 2^64 is exact in fp32 and in range for bf16; O and l carry the same
-// scale), so the common chunk needs one fma and one exp2 per score and no
+// Softmax: a token's reference m is one score of the first chunk it selects
+// and afterwards moves only when a chunk gives it some p > 2^64 (p <= 2^64 is
+// exact in fp32 and in range for bf16; O and l carry the same scale), so the
+// common chunk needs one fma and one exp2 per score, no maximum and no
 // rescale of O.  The row sum l adds the bf16 weights that multiply V
 // (v_dot2c_f32_bf16), so O / l is a convex combination of V rows exactly as
 // the MFMA sees them.
@@ -413,16 +413,35 @@ __global__ __launch_bounds__(256, 4) void read_fwd_fast_kernel(
         x = mfma32(a, qf[ks], x);
       }
     };
-    // VALU phase: softmax of the scores in x into bf16 weights pk
+    // VALU phase: softmax of the scores in x into bf16 weights pk.  The
+    // reference m_run of a token is set on its first selected chunk from one
+    // of the chunk's scores (the larger of the lane pair's first), not from
+    // the chunk maximum, which would cost 13 VALU instructions a chunk; it
+    // moves only when a chunk gives some p > 2^64, which the chunk's sum of
+    // p shows (inf included).  Then the chunk's scores are recomputed from
+    // the stage, the reference moves to their maximum (every p <= 1) and o
+    // and l_run are rescaled.  Any reference gives the same o and lse up to
+    // the bf16 rounding of p.
     auto softmax = [&](int s0, int c, f32x16& x, bf16x8 (&pk)[2]) {
       const int e = (int)(chunks[s0 + c] >> 16);
       bool sl;
       const float cb = route_bias<TK>(rt, e, topk, sl);
-      const float cand = fmaf(pair_max(max16(x)), alpha, cb);
-      // the running max moves on the token's first selected chunk, or when
-      // this chunk would give p > 2^64
-      if (__any(sl && (m_run == kNegBig || cand > m_run + 64.f))) {
-        if (sl && (m_run == kNegBig || cand > m_run + 64.f)) {
+      if (__any(sl && m_run == kNegBig)) {
+        const float ref = fmaf(pair_max(x[0]), alpha, cb);
+        if (sl && m_run == kNegBig) m_run = ref;
+      }
+      float add = sl ? cb - m_run : -INFINITY;
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
+      pk[0] = pack8(x, 0);
+      pk[1] = pack8(x, 8);
+      float part = add_bf16x8(pk[1], add_bf16x8(pk[0], 0.f));
+      // the lane pair holds one token: both move together
+      const bool big = !(pair_max(part) <= 0x1p64f);
+      if (__any(sl && big)) {
+        qk(c, x);
+        const float cand = fmaf(pair_max(max16(x)), alpha, cb);
+        if (sl && big) {
           const float cr = __builtin_amdgcn_exp2f(m_run - cand);
 #pragma unroll
           for (int j = 0; j < NO; ++j)
@@ -431,13 +450,14 @@ __global__ __launch_bounds__(256, 4) void read_fwd_fast_kernel(
           l_run *= cr;
           m_run = cand;
         }
-      }
-      const float add = sl ? cb - m_run : -INFINITY;
+        add = sl ? cb - m_run : -INFINITY;
 #pragma unroll
-      for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
-      pk[0] = pack8(x, 0);
-      pk[1] = pack8(x, 8);
-      l_run = add_bf16x8(pk[1], add_bf16x8(pk[0], l_run));
+        for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
+        pk[0] = pack8(x, 0);
+        pk[1] = pack8(x, 8);
+        part = add_bf16x8(pk[1], add_bf16x8(pk[0], 0.f));
+      }
+      l_run += part;
     };
     // MFMA phase part: O^T += V^T P^T with V^T read transposed from the stage
     auto pv = [&](int c, const bf16x8 (&pk)[2]) {

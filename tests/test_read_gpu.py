@@ -89,6 +89,47 @@ def test_read_fwd_bwd_matches_oracle(case, dev):
     assert worst < 2e-2, worst
 
 
+@pytest.mark.parametrize("big_block", [1, 0])
+def test_read_score_jump_moves_the_reference(big_block, dev):
+    """Every token selects blocks 0 and 1; the scores of one block sit about
+    2^138 above the other's in p.  With the large block second, the forward's
+    reference (set from a score of the token's first selected chunk) is far
+    below it: without moving the reference p would be inf.  With the large
+    block first, the second block's p underflow towards zero.  Forward and
+    backward against the fp32 oracle.  All the weight lands on one block, so
+    the gates' true gradient is ~0: the backward must normalise its recomputed
+    weights by their sum (the forward's lse carries the rounding of its bf16
+    row sum) for the gate gradient to come out ~0 too."""
+    from naylis_amd import mom_kernels
+    B, S, H, HD, NB, BS = 1, 128, 2, 64, 4, 64
+    g = torch.Generator().manual_seed(21)
+    L, D = NB * BS, H * HD
+    q = (1.0 + 0.1 * torch.randn(B, S, H, HD, generator=g)).bfloat16()
+    k = 0.3 * torch.randn(L, D, generator=g)
+    k[big_block * BS:(big_block + 1) * BS] += 12.0   # scores ~ 64 * 12 / 8 = 96 (log2: 138)
+    k = k.bfloat16()
+    v = (torch.randn(L, D, generator=g) * 0.4).bfloat16()
+    gates = F.softmax(torch.randn(B, S, 2, generator=g), -1)
+    top = torch.tensor([0, 1]).expand(B, S, 2).clone()
+    top[:, ::3] = torch.tensor([1, 0])                # both selection orders
+    dout = torch.randn(B, S, H, HD, generator=g).bfloat16()
+    ref = oracle_read(q, k, v, top, gates, dout, NB, BS)
+    qd, kd, vd, gd = (t.to(dev).requires_grad_(True) for t in (q, k, v, gates))
+    out = mom_kernels.mom_read(qd, kd, vd, top.to(dev), gd, num_blocks=NB, block_size=BS, mode="hip")
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    assert_close(out, ref[0], "out")
+    # every k of the large block carries the same offset (12 in each feature),
+    # so an error in sum_n dS_n (the bf16 rounding of dS; the delta taken from
+    # the forward's bf16 output) reaches dq as one shift of all its features,
+    # 12/8 times larger: compare dq with its feature mean removed
+    dq = qd.grad.float().cpu()
+    assert_close(dq - dq.mean(-1, keepdim=True), ref[1] - ref[1].mean(-1, keepdim=True), "dq")
+    for got, want, name in zip((kd.grad, vd.grad, gd.grad), ref[2:], ("dk", "dv", "d_gates")):
+        assert_close(got, want, name)
+
+
 def test_read_deterministic(dev):
     from naylis_amd import mom_kernels
     case = (2, 256, 4, 64, 8, 128, 2, "smooth")
