@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 11
+#define NAYLIS_MOM_ABI_VERSION 12
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -285,6 +285,31 @@ int naylis_mom_bank_kv_fwd(const void* slots, const void* w_k, const void* w_v, 
 int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, const void* dk, const void* dv,
                            void* d_slots, int slots_grad_dtype, void* dw_k, void* dw_v, int w_grad_dtype, int64_t L,
                            int64_t D_in, int64_t D_out, void* stream);
+
+/* Grouped: the projections of n layers that read one bank (the decoder's 20
+ * MoM layers share model.M_blocks, model.py:409-416, and each projects it,
+ * model.py:253-256), one launch per product instead of n.  Arrays hold one
+ * pointer per layer (host memory); shapes and dtypes as above, the same for
+ * every layer.
+ *   forward   k_out[i] = slots w_k[i]^T, v_out[i] = slots w_v[i]^T, each
+ *             bitwise equal to naylis_mom_bank_kv_fwd of layer i;
+ *   backward  d_slots = sum_i dk[i] w_k[i] + dv[i] w_v[i], accumulated in
+ *             fp32 over every layer in layer order and rounded once (the
+ *             reference sums the per-layer bank gradients in autograd);
+ *             dw_k[i], dw_v[i] bitwise equal to naylis_mom_bank_kv_bwd's.
+ * 1 <= n <= NAYLIS_BANK_GROUP_MAX_LAYERS; D_in a multiple of 8, D_out of 64;
+ * pointers 16-byte aligned.  The backward keeps n fp32 (L, D_in) partials in
+ * the caller's workspace (naylis_mom_bank_kv_bwd_grouped_workspace_bytes). */
+#define NAYLIS_BANK_GROUP_MAX_LAYERS 24
+int naylis_mom_bank_kv_fwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                   void* const* k_out, void* const* v_out, int64_t n_layers, int64_t L, int64_t D_in,
+                                   int64_t D_out, void* stream);
+size_t naylis_mom_bank_kv_bwd_grouped_workspace_bytes(int64_t n_layers, int64_t L, int64_t D_in, int64_t D_out);
+int naylis_mom_bank_kv_bwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                   const void* const* dk, const void* const* dv, void* d_slots, int slots_grad_dtype,
+                                   void* const* dw_k, void* const* dw_v, int w_grad_dtype, void* workspace,
+                                   size_t workspace_bytes, int64_t n_layers, int64_t L, int64_t D_in, int64_t D_out,
+                                   void* stream);
 
 /* ------------------------------------------------- projection weight grad ---
  * Weight gradient of the layer's bias-free query / output projections

@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -24,6 +24,7 @@ NAYLIS_ERR_HIP = 3
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _size_t = ctypes.c_size_t
+_pp = ctypes.POINTER(ctypes.c_void_p)  # host array of device pointers
 _int = ctypes.c_int
 _float = ctypes.c_float
 
@@ -64,6 +65,10 @@ SIGNATURES = {
     "naylis_mom_linear_wgrad": (_int, [_c_void_p] * 3 + [_int, _c_void_p, _size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
+    "naylis_mom_bank_kv_fwd_grouped": (_int, [_c_void_p] + [_pp] * 4 + [_i64] * 4 + [_c_void_p]),
+    "naylis_mom_bank_kv_bwd_grouped_workspace_bytes": (_size_t, [_i64] * 4),
+    "naylis_mom_bank_kv_bwd_grouped": (_int, [_c_void_p] + [_pp] * 4 + [_c_void_p, _int] + [_pp] * 2
+                                       + [_int, _c_void_p, _size_t] + [_i64] * 4 + [_c_void_p]),
     "naylis_mom_bank_quant_fp8": (_int, [_c_void_p] * 6 + [_i64] * 2 + [_c_void_p]),
     "naylis_mom_decode_step": (_int, [_c_void_p] * 4 + [_int] + [_c_void_p] * 10 + [_i64] * 7 + [_c_void_p]),
     "naylis_mom_timing_enable": (None, [_int]),

@@ -211,4 +211,76 @@ hipError_t launch_bank_kv_bwd(const void* slots, const void* w_k, const void* w_
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// The projections of n layers that read one bank, one grouped launch each:
+//   forward   K_i = slots W_k,i^T, V_i = slots W_v,i^T        (2n jobs)
+//   backward  d_slots = sum_i dK_i W_k,i + dV_i W_v,i          (n jobs, summed in layer order)
+//             dW_k,i = dK_i^T slots, dW_v,i = dV_i^T slots     (2n jobs)
+// Each K_i, V_i, dW_k,i, dW_v,i is bitwise what the per-layer launch gives;
+// d_slots is accumulated in fp32 over all layers and rounded once.
+bool bank_grouped_ok(int n, int L, int D_in, int D_out) {
+  // the backward's K splits at D_out between dK and dV: a whole number of 64-wide K steps
+  return n >= 1 && 2 * n <= kGemmMaxGroupJobs && L > 0 && D_in % 8 == 0 && D_out % 64 == 0;
+}
+
+size_t bank_kv_bwd_grouped_ws_bytes(int n, int L, int D_in) { return gemm_grouped_ws_bytes(n, L, D_in, true); }
+
+hipError_t launch_bank_kv_fwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                      void* const* k_out, void* const* v_out, int n, int L, int D_in, int D_out,
+                                      hipStream_t st) {
+  GemmGroupedLaunch g{};
+  g.njobs = 2 * n;
+  g.M = L;
+  g.N = D_out;
+  g.K = g.K1 = D_in;
+  g.out = kGemmOutBF16;
+  for (int z = 0; z < 2 * n; ++z) {
+    const int i = z / 2;
+    g.job[z].a = GemmOp{slots, nullptr, D_in, true};
+    g.job[z].b = GemmOp{z % 2 ? w_v[i] : w_k[i], nullptr, D_in, true};
+    g.job[z].c = z % 2 ? v_out[i] : k_out[i];
+    g.job[z].ldc = D_out;
+  }
+  if (!gemm_grouped_supported(g)) return hipErrorInvalidValue;
+  return launch_gemm_grouped(g, "bank_kv_fwd", st);
+}
+
+hipError_t launch_bank_kv_bwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                      const void* const* dk, const void* const* dv, void* d_slots, bool slots_f32,
+                                      void* const* dw_k, void* const* dw_v, bool w_f32, void* ws, int n, int L,
+                                      int D_in, int D_out, hipStream_t st) {
+  GemmGroupedLaunch g1{};  // d_slots (L x D_in) = sum_i [dK_i | dV_i] . [W_k,i ; W_v,i]
+  g1.njobs = n;
+  g1.M = L;
+  g1.N = D_in;
+  g1.K = 2 * D_out;
+  g1.K1 = D_out;
+  g1.out = slots_f32 ? kGemmOutF32 : kGemmOutBF16;
+  g1.sum_jobs = true;
+  g1.ws = ws;
+  for (int i = 0; i < n; ++i) {
+    g1.job[i].a = GemmOp{dk[i], dv[i], D_out, true};
+    g1.job[i].b = GemmOp{w_k[i], w_v[i], D_in, false};
+    g1.job[i].c = d_slots;
+    g1.job[i].ldc = D_in;
+  }
+  GemmGroupedLaunch g2{};  // dW_k,i, dW_v,i (D_out x D_in) = dK_i^T . slots
+  g2.njobs = 2 * n;
+  g2.M = D_out;
+  g2.N = D_in;
+  g2.K = g2.K1 = L;
+  g2.out = w_f32 ? kGemmOutF32 : kGemmOutBF16;
+  for (int z = 0; z < 2 * n; ++z) {
+    const int i = z / 2;
+    g2.job[z].a = GemmOp{z % 2 ? dv[i] : dk[i], nullptr, D_out, false};
+    g2.job[z].b = GemmOp{slots, nullptr, D_in, false};
+    g2.job[z].c = z % 2 ? dw_v[i] : dw_k[i];
+    g2.job[z].ldc = D_in;
+  }
+  if (!gemm_grouped_supported(g1) || !gemm_grouped_supported(g2)) return hipErrorInvalidValue;
+  hipError_t e = launch_gemm_grouped(g1, "bank_kv_bwd_dslots", st);
+  if (e != hipSuccess) return e;
+  return launch_gemm_grouped(g2, "bank_kv_bwd_dw", st);
+}
+
 }  // namespace naylis

@@ -609,6 +609,71 @@ int naylis_mom_bank_kv_bwd(const void* slots, const void* w_k, const void* w_v, 
                     "mom_bank_kv_bwd");
 }
 
+static int check_bank_grouped(int64_t n, int64_t L, int64_t D_in, int64_t D_out, const char* what) {
+  if (n < 1 || n > NAYLIS_BANK_GROUP_MAX_LAYERS)
+    return fail(NAYLIS_ERR_ARG, "%s: n_layers (%lld) outside [1, %d]", what, (long long)n,
+                NAYLIS_BANK_GROUP_MAX_LAYERS);
+  if (L <= 0 || D_in <= 0 || D_out <= 0 || L > NAYLIS_MAX_SLOTS || D_in > 65536 || D_out > 65536)
+    return fail(NAYLIS_ERR_ARG, "%s: bad shape L=%lld D_in=%lld D_out=%lld", what, (long long)L, (long long)D_in,
+                (long long)D_out);
+  if (!bank_grouped_ok((int)n, (int)L, (int)D_in, (int)D_out))
+    return fail(NAYLIS_ERR_ARG, "%s: D_in (%lld) must be a multiple of 8 and D_out (%lld) of 64", what,
+                (long long)D_in, (long long)D_out);
+  return NAYLIS_OK;
+}
+
+static bool all_set(const void* const* p, int64_t n) {
+  if (!p) return false;
+  for (int64_t i = 0; i < n; ++i)
+    if (!p[i]) return false;
+  return true;
+}
+
+int naylis_mom_bank_kv_fwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                   void* const* k_out, void* const* v_out, int64_t n_layers, int64_t L, int64_t D_in,
+                                   int64_t D_out, void* stream) {
+  int rc = check_bank_grouped(n_layers, L, D_in, D_out, "mom_bank_kv_fwd_grouped");
+  if (rc) return rc;
+  if (!slots || !all_set(w_k, n_layers) || !all_set(w_v, n_layers) || !all_set((const void* const*)k_out, n_layers) ||
+      !all_set((const void* const*)v_out, n_layers))
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_fwd_grouped: null pointer argument");
+  const hipError_t e = launch_bank_kv_fwd_grouped(slots, w_k, w_v, k_out, v_out, (int)n_layers, (int)L, (int)D_in,
+                                                  (int)D_out, (hipStream_t)stream);
+  if (e == hipErrorInvalidValue)
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_fwd_grouped: pointers must be 16-byte aligned");
+  return hip_status(e, "mom_bank_kv_fwd_grouped");
+}
+
+size_t naylis_mom_bank_kv_bwd_grouped_workspace_bytes(int64_t n_layers, int64_t L, int64_t D_in, int64_t D_out) {
+  if (check_bank_grouped(n_layers, L, D_in, D_out, "mom_bank_kv_bwd_grouped_workspace_bytes") != NAYLIS_OK) return 0;
+  return bank_kv_bwd_grouped_ws_bytes((int)n_layers, (int)L, (int)D_in);
+}
+
+int naylis_mom_bank_kv_bwd_grouped(const void* slots, const void* const* w_k, const void* const* w_v,
+                                   const void* const* dk, const void* const* dv, void* d_slots, int slots_grad_dtype,
+                                   void* const* dw_k, void* const* dw_v, int w_grad_dtype, void* workspace,
+                                   size_t workspace_bytes, int64_t n_layers, int64_t L, int64_t D_in, int64_t D_out,
+                                   void* stream) {
+  int rc = check_bank_grouped(n_layers, L, D_in, D_out, "mom_bank_kv_bwd_grouped");
+  if (rc) return rc;
+  if ((rc = check_dtype(slots_grad_dtype, "mom_bank_kv_bwd_grouped"))) return rc;
+  if ((rc = check_dtype(w_grad_dtype, "mom_bank_kv_bwd_grouped"))) return rc;
+  if (!slots || !d_slots || !all_set(w_k, n_layers) || !all_set(w_v, n_layers) || !all_set(dk, n_layers) ||
+      !all_set(dv, n_layers) || !all_set((const void* const*)dw_k, n_layers) ||
+      !all_set((const void* const*)dw_v, n_layers))
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_bwd_grouped: null pointer argument");
+  const size_t need = bank_kv_bwd_grouped_ws_bytes((int)n_layers, (int)L, (int)D_in);
+  if (!workspace || workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "mom_bank_kv_bwd_grouped: workspace of %zu bytes, %zu needed", workspace_bytes,
+                need);
+  const hipError_t e = launch_bank_kv_bwd_grouped(
+      slots, w_k, w_v, dk, dv, d_slots, slots_grad_dtype == NAYLIS_DTYPE_F32, dw_k, dw_v,
+      w_grad_dtype == NAYLIS_DTYPE_F32, workspace, (int)n_layers, (int)L, (int)D_in, (int)D_out, (hipStream_t)stream);
+  if (e == hipErrorInvalidValue)
+    return fail(NAYLIS_ERR_ARG, "mom_bank_kv_bwd_grouped: pointers must be 16-byte aligned");
+  return hip_status(e, "mom_bank_kv_bwd_grouped");
+}
+
 // ---------------------------------------------------- projection weight grad
 static int wgrad_splits(int64_t N, int64_t D_in, int64_t D_out) {
   // enough workgroups for two per CU, each reducing at least 1024 tokens, as a power of two: the

@@ -34,6 +34,10 @@ struct DevJob {
 struct DevJobs {
   DevJob j[2];
 };
+// the job table of a grouped launch (every job of one shape and layout)
+struct DevJobsGrouped {
+  DevJob j[kGemmMaxGroupJobs];
+};
 
 // Tile configuration: WAVES_M x WAVES_N waves, each owning TM x TN MFMA tiles
 // of 32 x 32 (a (32 TM) x (32 TN) block of C).
@@ -136,8 +140,8 @@ __device__ __forceinline__ bf16x8 gemm_frag(const bf16_t* tile, int row0, int ks
 }
 
 // OUT: 0 = fp32 C, 1 = bf16 C, 2 = fp32 partial into ws[job][split][M][N]
-template <class C, bool AKC, bool BKC, int OUT>
-__global__ __launch_bounds__(C::NT) void gemm_kernel(DevJobs jobs, int M, int N, int K1, int kper, int tiles_m,
+template <class C, bool AKC, bool BKC, int OUT, class JOBS = DevJobs>
+__global__ __launch_bounds__(C::NT) void gemm_kernel(JOBS jobs, int M, int N, int K1, int kper, int tiles_m,
                                                      int tiles_n, int splits, int njobs, int K,
                                                      float* __restrict__ ws) {
   using SA = Stage<AKC, C::BM, C::NT>;
@@ -317,6 +321,38 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(DevJobs jobs, const fl
   }
 }
 
+// C = sum over jobs (ascending) of the fp32 partials ws[job][M][N] (a grouped
+// launch whose jobs add into one output); 4 consecutive elements per thread.
+template <int OUT>
+__global__ __launch_bounds__(256) void gemm_sum_jobs_kernel(const float* __restrict__ ws, void* __restrict__ c,
+                                                            long ldc, int M, int N, int njobs) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  const long mn = (long)M * N;
+  if (i >= mn) return;
+  f32x4 s = *reinterpret_cast<const f32x4*>(ws + i);
+  for (int j = 1; j < njobs; ++j) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(ws + j * mn + i);
+    s[0] += v[0];
+    s[1] += v[1];
+    s[2] += v[2];
+    s[3] += v[3];
+  }
+  const long m = i / N, n = i % N;
+  if constexpr (OUT == 0) {
+    float* o = reinterpret_cast<float*>(c) + m * ldc + n;
+    o[0] = s[0];
+    o[1] = s[1];
+    o[2] = s[2];
+    o[3] = s[3];
+  } else {
+    bf16_t* o = reinterpret_cast<bf16_t*>(c) + m * ldc + n;
+    o[0] = f32_to_bf16(s[0]);
+    o[1] = f32_to_bf16(s[1]);
+    o[2] = f32_to_bf16(s[2]);
+    o[3] = f32_to_bf16(s[3]);
+  }
+}
+
 // Zero-fill through a kernel (a memset node is not safe inside captured HIP graphs).
 __global__ __launch_bounds__(256) void zero_fill_kernel(uint8_t* __restrict__ p, size_t bytes) {
   const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 16;
@@ -426,6 +462,106 @@ hipError_t launch_gemm(const GemmLaunch& g, const char* name, hipStream_t st) {
     gemm_layouts<CfgMid>(dj, gl, kper, splits, name, st);
   else
     gemm_layouts<CfgTiny>(dj, gl, kper, splits, name, st);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped launch: njobs GEMMs of one shape and layout in one grid (no K split),
+// on the tile launch_gemm would pick for the whole grid.  Every output element
+// accumulates over K in the same order as a single launch_gemm of its job, so
+// each job's C is bitwise what launch_gemm gives.  With sum_jobs the jobs' fp32
+// products go to ws[job][M][N] and one more launch adds them in job order into
+// job[0].c.
+size_t gemm_grouped_ws_bytes(int njobs, int M, int N, bool sum_jobs) {
+  return sum_jobs ? (size_t)njobs * M * N * sizeof(float) : 0;
+}
+
+bool gemm_grouped_supported(const GemmGroupedLaunch& g) {
+  if (g.njobs < 1 || g.njobs > kGemmMaxGroupJobs) return false;
+  if (g.sum_jobs && ((long)g.M * g.N) % 4) return false;
+  for (int j = 0; j < g.njobs; ++j) {
+    GemmLaunch one{};
+    one.job[0] = g.job[j];
+    one.njobs = 1;
+    one.M = g.M;
+    one.N = g.N;
+    one.K = g.K;
+    one.K1 = g.K1;
+    one.out = g.out;
+    one.splits = 1;
+    if (!gemm_supported(one)) return false;
+    if (g.job[j].a.kcontig != g.job[0].a.kcontig || g.job[j].b.kcontig != g.job[0].b.kcontig) return false;
+  }
+  return true;
+}
+
+template <class C, bool AKC, bool BKC>
+static void grouped_dispatch(const DevJobsGrouped& dj, const GemmGroupedLaunch& g, int kper, const char* name,
+                             hipStream_t st) {
+  const int tiles_m = (g.M + C::BM - 1) / C::BM, tiles_n = (g.N + C::BN - 1) / C::BN;
+  const dim3 grid(tiles_m * tiles_n * g.njobs);
+  const int K1 = g.K1 < g.K ? g.K1 : g.K;
+  if (g.sum_jobs)
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 2, DevJobsGrouped>), grid, dim3(C::NT), 0, st, dj, g.M,
+                                    g.N, K1, kper, tiles_m, tiles_n, 1, g.njobs, g.K, (float*)g.ws));
+  else if (g.out == kGemmOutF32)
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 0, DevJobsGrouped>), grid, dim3(C::NT), 0, st, dj, g.M,
+                                    g.N, K1, kper, tiles_m, tiles_n, 1, g.njobs, g.K, (float*)nullptr));
+  else
+    NAYLIS_TIMED(name, st,
+                 hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 1, DevJobsGrouped>), grid, dim3(C::NT), 0, st, dj, g.M,
+                                    g.N, K1, kper, tiles_m, tiles_n, 1, g.njobs, g.K, (float*)nullptr));
+}
+
+template <class C>
+static void grouped_layouts(const DevJobsGrouped& dj, const GemmGroupedLaunch& g, int kper, const char* name,
+                            hipStream_t st) {
+  const bool ak = g.job[0].a.kcontig, bk = g.job[0].b.kcontig;
+  if (ak && bk)
+    grouped_dispatch<C, true, true>(dj, g, kper, name, st);
+  else if (ak)
+    grouped_dispatch<C, true, false>(dj, g, kper, name, st);
+  else if (bk)
+    grouped_dispatch<C, false, true>(dj, g, kper, name, st);
+  else
+    grouped_dispatch<C, false, false>(dj, g, kper, name, st);
+}
+
+hipError_t launch_gemm_grouped(const GemmGroupedLaunch& g, const char* name, hipStream_t st) {
+  DevJobsGrouped dj{};
+  for (int j = 0; j < g.njobs; ++j) {
+    const GemmJob& s = g.job[j];
+    dj.j[j].a = DevOp{(const bf16_t*)s.a.p1, (const bf16_t*)(s.a.p2 ? s.a.p2 : s.a.p1), s.a.ld};
+    dj.j[j].b = DevOp{(const bf16_t*)s.b.p1, (const bf16_t*)(s.b.p2 ? s.b.p2 : s.b.p1), s.b.ld};
+    dj.j[j].c = s.c;
+    dj.j[j].ldc = s.ldc;
+  }
+  const int kper = (g.K + kGK - 1) / kGK * kGK;
+  auto wgs = [&](int bm, int bn) { return (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.njobs; };
+  const long cus = 256;
+  const long wide = wgs(CfgWide::BM, CfgWide::BN);
+  if (wide >= cus && wide % cus == 0)
+    grouped_layouts<CfgWide>(dj, g, kper, name, st);
+  else if (wgs(CfgSmall::BM, CfgSmall::BN) >= cus)
+    grouped_layouts<CfgSmall>(dj, g, kper, name, st);
+  else if (wgs(CfgMid::BM, CfgMid::BN) >= cus)
+    grouped_layouts<CfgMid>(dj, g, kper, name, st);
+  else
+    grouped_layouts<CfgTiny>(dj, g, kper, name, st);
+  if (g.sum_jobs) {
+    const long mn = (long)g.M * g.N;
+    const dim3 rg((unsigned)((mn / 4 + 255) / 256));
+    if (g.out == kGemmOutF32)
+      NAYLIS_TIMED("gemm_sum_jobs", st,
+                   hipLaunchKernelGGL((gemm_sum_jobs_kernel<0>), rg, dim3(256), 0, st, (const float*)g.ws,
+                                      g.job[0].c, g.job[0].ldc, g.M, g.N, g.njobs));
+    else
+      NAYLIS_TIMED("gemm_sum_jobs", st,
+                   hipLaunchKernelGGL((gemm_sum_jobs_kernel<1>), rg, dim3(256), 0, st, (const float*)g.ws,
+                                      g.job[0].c, g.job[0].ldc, g.M, g.N, g.njobs));
+  }
   return hipGetLastError();
 }
 

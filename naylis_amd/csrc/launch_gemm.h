@@ -43,6 +43,23 @@ bool gemm_supported(const GemmLaunch& g);
 size_t gemm_ws_bytes(int njobs, int M, int N, int splits);
 hipError_t launch_gemm(const GemmLaunch& g, const char* timer_name, hipStream_t st);
 
+// Up to kGemmMaxGroupJobs GEMMs of one shape and layout in one launch (no K
+// split; each job's C bitwise equal to launch_gemm of that job).  With
+// sum_jobs, C = sum over jobs of A_j B_j, written to job[0].c through fp32
+// partials in ws (gemm_grouped_ws_bytes) added in job order.
+constexpr int kGemmMaxGroupJobs = 48;
+struct GemmGroupedLaunch {
+  GemmJob job[kGemmMaxGroupJobs];
+  int njobs;
+  int M, N, K, K1;
+  GemmOut out;
+  bool sum_jobs;
+  void* ws;
+};
+bool gemm_grouped_supported(const GemmGroupedLaunch& g);
+size_t gemm_grouped_ws_bytes(int njobs, int M, int N, bool sum_jobs);
+hipError_t launch_gemm_grouped(const GemmGroupedLaunch& g, const char* timer_name, hipStream_t st);
+
 // Zero `bytes` bytes at p with a kernel (safe inside captured HIP graphs).
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t st);
 

@@ -10,9 +10,13 @@ reference's (``model.layers.<i>.mom.*``, ``model.layers.<i>.mom_norm.*``,
 ``naylis_amd.checkpoint``).
 
 What differs from the reference is where the MoM work runs: ``self.mom`` is
-``naylis_amd.layer.MoMLayer`` (router, bank K/V, read, ReZero on the library's
-kernels, one autograd node per layer) and the load-balance aux loss consumes
-the router probabilities that kernel emits (``naylis_amd.layer.mom_aux_loss``).
+``naylis_amd.layer.MoMLayer`` (router, read, ReZero on the library's kernels,
+one autograd node per layer), the bank's K and V for every layer come from one
+grouped projection per forward (``mom_kernels.mom_bank_kv_grouped``: one
+launch for all layers' K/V, and in the backward one fp32 accumulation of all
+layers' bank gradients where the reference sums 20 per-layer gradients in
+autograd), and the load-balance aux loss consumes the router probabilities
+the layer kernel emits (``naylis_amd.layer.mom_aux_loss``).
 There is no eager MoM path: off ROCm the MoM layers raise.  The norms
 (``mom_norm``, the block's two norms, the final norm) are the library's fused
 RMSNorm (``NaylisRMSNorm``, the role of the reference's ``use_liger`` norm)
@@ -34,6 +38,7 @@ from transformers.modeling_outputs import BaseModelOutputWithPast, CausalLMOutpu
 from transformers.models.llama.modeling_llama import (LlamaDecoderLayer, LlamaForCausalLM, LlamaModel,
                                                       LlamaRMSNorm)
 
+from . import mom_kernels
 from .layer import MoMLayer, cast_mom_layer, mom_aux_loss
 from .mom_kernels.hip_norm import NaylisRMSNorm, add_rms_norm
 from .mom_kernels.hip_linear import use_library_wgrad
@@ -112,7 +117,8 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
             return torch.utils.checkpoint.checkpoint(fn, *tensors, use_reentrant=False, preserve_rng_state=False)
         return fn(*tensors)
 
-    def forward(self, hidden_states, M_blocks=None, position_embeddings=None, pending=None, **kwargs):
+    def forward(self, hidden_states, M_blocks=None, position_embeddings=None, pending=None, bank_kv=None,
+                **kwargs):
         if M_blocks is None:
             raise ValueError("M_blocks is required: the MoM layer cannot run without the shared memory bank")
         h = hidden_states
@@ -125,7 +131,7 @@ class NaylisDecoderLayer(LlamaDecoderLayer):
         h, x = add_rms_norm(h, a, self.mom_norm)
         # the ReZero product promotes to the fp32 scale's dtype; the add rounds
         # it to the residual stream's (bf16 in bf16 training, fp32 under autocast)
-        h, x = add_rms_norm(h, self.mom(x, M_blocks), self.post_attention_layernorm)
+        h, x = add_rms_norm(h, self.mom(x, M_blocks, bank_kv), self.post_attention_layernorm)
         return h, self._maybe_ckpt(self.mlp, x)
 
 
@@ -151,10 +157,15 @@ class NaylisLlamaModel(LlamaModel):
         if position_ids is None:
             position_ids = torch.arange(S, device=h.device).unsqueeze(0).expand(B, -1)
         pos = self.rotary_emb(h, position_ids)
+        # every layer projects the one bank (model.py:409-416, 253-256): one grouped launch for all
+        # layers' K and V, and one accumulation of their bank gradients in the backward
+        moms = [layer.mom for layer in self.layers]
+        kv = mom_kernels.mom_bank_kv_grouped(self.M_blocks, [m.k_proj.weight for m in moms],
+                                             [m.v_proj.weight for m in moms], mem_slots=moms[0].mem_slots)
         pending = None
-        for layer in self.layers:
+        for layer, bank_kv in zip(self.layers, kv):
             h, pending = layer(h, M_blocks=self.M_blocks, position_embeddings=pos, pending=pending,
-                               attention_mask=attention_mask, **kwargs)
+                               bank_kv=bank_kv, attention_mask=attention_mask, **kwargs)
         out = self.norm(h) if pending is None else add_rms_norm(h, pending, self.norm)[1]
         return BaseModelOutputWithPast(last_hidden_state=out)
 

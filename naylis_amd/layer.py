@@ -95,7 +95,11 @@ class MoMLayer(nn.Module):
         return mom_kernels.mom_route(x, self.router_down.weight, self.router_up.weight, self.top_blocks,
                                      noise=noise, noise_scale=self.noise_scale, noise_is_uniform=noise_is_uniform)
 
-    def forward(self, x, M_blocks):
+    def forward(self, x, M_blocks, bank_kv=None):
+        """``bank_kv``: this layer's (K, V) of the bank, when the caller
+        projected the bank for several layers at once
+        (``mom_kernels.mom_bank_kv_grouped``); else the layer projects
+        M_blocks itself."""
         B, S, D = x.shape
         if self._kernel_mode is None:
             self._kernel_mode = self._resolve_kernel(x)
@@ -108,13 +112,14 @@ class MoMLayer(nn.Module):
         ckpt = self.mom_grad_ckpt and self.training and torch.is_grad_enabled()
         if not ckpt and fused_layer_supported(x, M_blocks, self.router_down.weight, self.router_up.weight,
                                               self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
-                                              self.o_proj.weight, self.mom_scale):
+                                              self.o_proj.weight, self.mom_scale, bank_kv):
             # one autograd node for router + bank + q + read + o + ReZero
             y, router_probs, top_idx = mom_layer(
                 x, M_blocks, self.router_down.weight, self.router_up.weight, self.q_proj.weight,
                 self.k_proj.weight, self.v_proj.weight, self.o_proj.weight, self.mom_scale,
                 n_heads=self.n_heads, num_blocks=self.num_blocks, block_size=self.block_size,
-                top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale, noise_is_uniform=True)
+                top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale, noise_is_uniform=True,
+                bank_kv=bank_kv)
             if self.training:
                 self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
                 self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
@@ -123,18 +128,20 @@ class MoMLayer(nn.Module):
         if self.training:
             self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
             self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
+        k, v = bank_kv if bank_kv is not None else (None, None)
         if ckpt:
             out = torch.utils.checkpoint.checkpoint(
-                self._read, x, top_idx, top_gates, M_blocks, use_reentrant=False, preserve_rng_state=False)
+                self._read, x, top_idx, top_gates, M_blocks, k, v, use_reentrant=False, preserve_rng_state=False)
         else:
-            out = self._read(x, top_idx, top_gates, M_blocks)
+            out = self._read(x, top_idx, top_gates, M_blocks, k, v)
         return mom_kernels.mom_rezero(out, self.mom_scale)
 
-    def _read(self, x, top_idx, top_gates, M_blocks):
-        """q projection, bank K/V, gated flash read, o projection (model.py:241-276)."""
+    def _read(self, x, top_idx, top_gates, M_blocks, k=None, v=None):
+        """q projection, bank K/V (unless given), gated flash read, o projection (model.py:241-276)."""
         B, S, D = x.shape
         q_sh = mom_kernels.mom_linear(x, self.q_proj.weight).view(B, S, self.n_heads, self.head_dim)
-        k, v = mom_kernels.mom_bank_kv(M_blocks, self.k_proj.weight, self.v_proj.weight, mem_slots=self.mem_slots)
+        if k is None:
+            k, v = mom_kernels.mom_bank_kv(M_blocks, self.k_proj.weight, self.v_proj.weight, mem_slots=self.mem_slots)
         out = mom_kernels.mom_read(q_sh, k, v, top_idx, top_gates, num_blocks=self.num_blocks,
                                    block_size=self.block_size, mode=self._kernel_mode)
         return mom_kernels.mom_linear(out.reshape(B, S, D), self.o_proj.weight)

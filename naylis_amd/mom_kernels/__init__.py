@@ -22,7 +22,7 @@ from .. import _lib
 from .hip_read import mom_read as _hip_mom_read
 
 __all__ = ["HAS_HIP", "preflight", "resolve_mode", "mom_read", "announce", "mom_route",
-           "mom_bank_kv", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step",
+           "mom_bank_kv", "mom_bank_kv_grouped", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step",
            "mom_router_stats"]
 
 _ANNOUNCED = {"backend": None}
@@ -111,6 +111,11 @@ def mom_router_stats(*args, **kwargs):
 def mom_bank_kv(*args, **kwargs):
     from .hip_bank import mom_bank_kv as _bank
     return _bank(*args, **kwargs)
+
+
+def mom_bank_kv_grouped(*args, **kwargs):
+    from .hip_bank import mom_bank_kv_grouped as _grouped
+    return _grouped(*args, **kwargs)
 
 
 def mom_linear(*args, **kwargs):

@@ -28,10 +28,11 @@ def _ws(nbytes, dev):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
 
 
-def fused_layer_supported(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale):
+def fused_layer_supported(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, bank_kv=None):
     """True when the fused node applies: bf16 activations and projection
     weights, fp32 router weights and gate, D a multiple of 128 (the router's
-    accumulating backward), all on one ROCm device."""
+    accumulating backward), all on one ROCm device.  With ``bank_kv`` the
+    bank's K and V come from the caller (bf16, contiguous)."""
     if torch.version.hip is None or not x.is_cuda:
         return False
     if x.dim() != 3 or x.dtype != torch.bfloat16 or x.shape[-1] % 128 != 0:
@@ -46,6 +47,9 @@ def fused_layer_supported(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale):
         return False
     if scale.dtype != torch.float32 or scale.numel() != 1 or scale.device != dev:
         return False
+    if bank_kv is not None:
+        return all(t.dtype == torch.bfloat16 and t.device == dev and t.is_contiguous() and t.dim() == 2
+                   and t.shape[1] == x.shape[-1] for t in bank_kv)
     return M_blocks.device == dev and M_blocks.dtype in (torch.bfloat16, torch.float32)
 
 
@@ -54,7 +58,8 @@ class MomLayerFunction(torch.autograd.Function):
     probs the router softmax (for the load-balance aux loss), top_idx int32."""
 
     @staticmethod
-    def forward(ctx, x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, noise, noise_scale, geom):
+    def forward(ctx, x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, noise, noise_scale, geom, k_ext=None,
+                v_ext=None):
         n_heads, num_blocks, block_size, top_k, noise_kind = geom
         lib = _lib.load()
         B, T, D = x.shape
@@ -79,15 +84,18 @@ class MomLayerFunction(torch.autograd.Function):
                 probs.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), act.data_ptr(), None, rws.data_ptr(),
                 rws.numel(), B, T, D, R, E, top_k, st))
             del rws
-            # ---- bank K/V (model.py:253-256)
-            slots = M_blocks.reshape(-1, D)
-            m_dtype = slots.dtype
-            slots = slots.to(torch.bfloat16).contiguous()
-            L = slots.shape[0]
-            k = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
-            v = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
-            _lib.check(lib.naylis_mom_bank_kv_fwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), k.data_ptr(),
-                                                  v.data_ptr(), L, D, D, st))
+            # ---- bank K/V (model.py:253-256), unless the caller projected the bank (grouped over layers)
+            if k_ext is None:
+                slots = M_blocks.reshape(-1, D)
+                m_dtype = slots.dtype
+                slots = slots.to(torch.bfloat16).contiguous()
+                L = slots.shape[0]
+                k = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
+                v = torch.empty((L, D), device=dev, dtype=torch.bfloat16)
+                _lib.check(lib.naylis_mom_bank_kv_fwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+                                                      k.data_ptr(), v.data_ptr(), L, D, D, st))
+            else:
+                slots, m_dtype, k, v = None, None, k_ext, v_ext
             # ---- q projection, gated read, o projection (model.py:251, 258-276)
             q = F.linear(x, w_q)
             order = read_order(top_idx, num_blocks)
@@ -104,7 +112,8 @@ class MomLayerFunction(torch.autograd.Function):
         ctx.save_for_backward(x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v,
                               q, order, out, lse, z)
         ctx.geom = geom
-        ctx.m_shape = (tuple(M_blocks.shape), m_dtype)
+        ctx.external_bank = k_ext is not None
+        ctx.m_shape = None if k_ext is not None else (tuple(M_blocks.shape), m_dtype)
         ctx.mark_non_differentiable(top_idx)
         ctx.set_materialize_grads(False)
         return y, probs, top_idx
@@ -118,7 +127,7 @@ class MomLayerFunction(torch.autograd.Function):
         B, T, D = x.shape
         R, E = w_down.shape[0], w_up.shape[0]
         H, HD = n_heads, D // n_heads
-        L = slots.shape[0]
+        L = k.shape[0]
         dev = x.device
         st = _lib.stream_of(dev)
         f32 = dict(device=dev, dtype=torch.float32)
@@ -155,15 +164,19 @@ class MomLayerFunction(torch.autograd.Function):
                 out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                 dgates.data_ptr(), rws.data_ptr(), rws.numel(), B, T, H, HD, num_blocks, block_size, top_k, st))
             del rws, dout
-            # ---- bank K/V
-            m_shape, m_dtype = ctx.m_shape
-            sdt = _BF16 if m_dtype == torch.bfloat16 else _F32
-            d_slots = torch.empty((L, D), device=dev, dtype=m_dtype)
-            dw_k = torch.empty_like(w_k)
-            dw_v = torch.empty_like(w_v)
-            _lib.check(lib.naylis_mom_bank_kv_bwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(), dk.data_ptr(),
-                                                  dv.data_ptr(), d_slots.data_ptr(), sdt, dw_k.data_ptr(),
-                                                  dw_v.data_ptr(), _BF16, L, D, D, st))
+            # ---- bank K/V (the caller's grouped node takes dK, dV when it projected the bank)
+            if ctx.external_bank:
+                d_m, dw_k, dw_v, dk_ext, dv_ext = None, None, None, dk, dv
+            else:
+                m_shape, m_dtype = ctx.m_shape
+                sdt = _BF16 if m_dtype == torch.bfloat16 else _F32
+                d_slots = torch.empty((L, D), device=dev, dtype=m_dtype)
+                dw_k = torch.empty_like(w_k)
+                dw_v = torch.empty_like(w_v)
+                _lib.check(lib.naylis_mom_bank_kv_bwd(slots.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+                                                      dk.data_ptr(), dv.data_ptr(), d_slots.data_ptr(), sdt,
+                                                      dw_k.data_ptr(), dw_v.data_ptr(), _BF16, L, D, D, st))
+                d_m, dk_ext, dv_ext = d_slots.view(m_shape), None, None
             # ---- q projection: dx = dq W_q (the router adds its part below), dW_q = dq^T x
             dq2 = dq.view(N, D)
             dx = torch.mm(dq2, w_q).view(B, T, D)
@@ -178,8 +191,8 @@ class MomLayerFunction(torch.autograd.Function):
                 top_idx.data_ptr(), gates.data_ptr(), dgates.data_ptr(),
                 dp_ptr, dp_stride, None, dx.data_ptr(), 1, dw_down.data_ptr(),
                 dw_up.data_ptr(), rws.data_ptr(), rws.numel(), B, T, D, R, E, top_k, st))
-        return (dx, d_slots.view(m_shape), dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None,
-                None)
+        return (dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None, None, dk_ext,
+                dv_ext)
 
 
 def _wgrad(lib, xin, dy, dtype, dev, st):
@@ -199,13 +212,16 @@ def _wgrad(lib, xin, dy, dtype, dev, st):
 
 
 def mom_layer(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, *, n_heads, num_blocks, block_size, top_k,
-              noise=None, noise_scale=1.0, noise_is_uniform=False):
+              noise=None, noise_scale=1.0, noise_is_uniform=False, bank_kv=None):
     """The fused layer node; callers check fused_layer_supported() first.
     ``noise_is_uniform``: noise is the uniform draw and the router kernel
-    applies the Gumbel transform.  Returns (y fp32, router probs, top_idx int32)."""
+    applies the Gumbel transform.  ``bank_kv``: the bank's (K, V) projected by
+    the caller (M_blocks, w_k and w_v then get no gradient here; K and V do).
+    Returns (y fp32, router probs, top_idx int32)."""
     if noise is not None:
         noise = noise.detach().float().contiguous()
-    return MomLayerFunction.apply(x, M_blocks, w_down.float().contiguous(), w_up.float().contiguous(), w_q, w_k,
-                                  w_v, w_o, scale, noise, float(noise_scale),
+    k_ext, v_ext = bank_kv if bank_kv is not None else (None, None)
+    return MomLayerFunction.apply(x, M_blocks if bank_kv is None else None, w_down.float().contiguous(),
+                                  w_up.float().contiguous(), w_q, w_k, w_v, w_o, scale, noise, float(noise_scale),
                                   (int(n_heads), int(num_blocks), int(block_size), int(top_k),
-                                   1 if noise_is_uniform else 0))
+                                   1 if noise_is_uniform else 0), k_ext, v_ext)

@@ -254,3 +254,26 @@ def test_read_bwd_noalloc_refuses_before_touching_a_device(lib):
     assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), *dims, None) == _lib.NAYLIS_ERR_WORKSPACE
     assert b"scratch" in lib.naylis_mom_last_error()
     assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), 1, 64, 2, 96, 4, 16, 2, None) == _lib.NAYLIS_ERR_ARG
+
+
+def test_bank_grouped_rejects_bad_arguments(lib):
+    """The grouped bank projection refuses, before touching a device, layer
+    counts outside [1, NAYLIS_BANK_GROUP_MAX_LAYERS], D_out not a multiple of
+    64, null pointer arrays or entries, and a short workspace."""
+    P = ctypes.c_void_p
+    one = (P * 2)(1, 1)
+    fwd = lib.naylis_mom_bank_kv_fwd_grouped
+    assert fwd(1, one, one, one, one, 0, 64, 64, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert fwd(1, one, one, one, one, 25, 64, 64, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert fwd(1, one, one, one, one, 2, 64, 64, 96, None) == _lib.NAYLIS_ERR_ARG
+    assert "D_out" in lib.naylis_mom_last_error().decode()
+    assert fwd(1, None, one, one, one, 2, 64, 64, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert fwd(1, (P * 2)(1, None), one, one, one, 2, 64, 64, 64, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_bank_kv_bwd_grouped_workspace_bytes(2, 64, 32, 64) == 2 * 64 * 32 * 4
+    assert lib.naylis_mom_bank_kv_bwd_grouped_workspace_bytes(0, 64, 32, 64) == 0
+    bwd = lib.naylis_mom_bank_kv_bwd_grouped
+    f32, bf16 = 0, 1  # NAYLIS_DTYPE_F32, NAYLIS_DTYPE_BF16
+    args = [1, one, one, one, one, 1, f32, one, one, bf16]
+    assert bwd(*args, None, 0, 2, 64, 32, 64, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert bwd(*args, 1, 2 * 64 * 32 * 4 - 1, 2, 64, 32, 64, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert bwd(*args, 1, 1 << 20, 25, 64, 32, 64, None) == _lib.NAYLIS_ERR_ARG

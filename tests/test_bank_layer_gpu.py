@@ -177,3 +177,76 @@ def test_layer_fused_node_matches_modular(dev, monkeypatch):
     err = (x0.float() - x1.float()).abs()
     scale = float(x1.float().abs().max())
     assert float(err.max()) <= 2.0 ** -7 * scale, (float(err.max()), scale)
+
+
+@pytest.mark.parametrize("n,L,D", [(3, 1024, 1024), (20, 1024, 1024), (25, 512, 256)])
+def test_bank_kv_grouped_matches_per_layer(n, L, D, dev):
+    """The grouped projection of n layers that read one bank (the decoder's
+    layers share model.M_blocks, model.py:409-416): every K_i, V_i, dW_k,i and
+    dW_v,i bitwise equal to the per-layer call, and the bank gradient equal to
+    the per-layer fp32 bank gradients added in layer order (25 layers run as
+    two groups of at most 24, whose two sums autograd adds)."""
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(n)
+    M = torch.randn(L, D, generator=g) * 0.5  # fp32 bank: its gradient stays fp32
+    wk = [(torch.randn(D, D, generator=g) * 0.03).bfloat16() for _ in range(n)]
+    wv = [(torch.randn(D, D, generator=g) * 0.03).bfloat16() for _ in range(n)]
+    dk = [torch.randn(L, D, generator=g).bfloat16() for _ in range(n)]
+    dv = [torch.randn(L, D, generator=g).bfloat16() for _ in range(n)]
+    Md = M.to(dev).requires_grad_(True)
+    wkd = [w.to(dev).requires_grad_(True) for w in wk]
+    wvd = [w.to(dev).requires_grad_(True) for w in wv]
+    kv = mom_kernels.mom_bank_kv_grouped(Md, wkd, wvd, mem_slots=L)
+    assert len(kv) == n
+    torch.autograd.backward([t for pair in kv for t in pair],
+                            [t.to(dev) for i in range(n) for t in (dk[i], dv[i])])
+    ref_dm = None
+    for i in range(n):
+        Mi = M.to(dev).requires_grad_(True)
+        wki, wvi = wk[i].to(dev).requires_grad_(True), wv[i].to(dev).requires_grad_(True)
+        k, v = mom_kernels.mom_bank_kv(Mi, wki, wvi, mem_slots=L)
+        torch.autograd.backward([k, v], [dk[i].to(dev), dv[i].to(dev)])
+        assert torch.equal(kv[i][0], k) and torch.equal(kv[i][1], v), i
+        assert torch.equal(wkd[i].grad, wki.grad) and torch.equal(wvd[i].grad, wvi.grad), i
+        ref_dm = Mi.grad if ref_dm is None else ref_dm + Mi.grad
+    assert Md.grad.dtype == torch.float32
+    assert torch.equal(Md.grad, ref_dm)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_external_bank_matches_own_projection(fused, dev, monkeypatch):
+    """MoMLayer given its bank K/V from the grouped projection (as the decoder
+    does) against the layer projecting M_blocks itself: output and every
+    gradient (bank, projections, router, x) bitwise equal, on the fused node
+    and on the modular path."""
+    import naylis_amd.layer as layer_mod
+    from naylis_amd import mom_kernels
+    if not fused:
+        monkeypatch.setattr(layer_mod, "fused_layer_supported", lambda *a, **k: False)
+    B, S, D, H, NB, BS, K, R = 2, 256, 256, 4, 8, 128, 2, 32
+    res = []
+    for external in (False, True):
+        layer, _, M = build_pair(D, H, NB, BS, K, R, seed=21)
+        ld = layer.to(dev)
+        for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+            lin.to(torch.bfloat16)
+        ld.train()
+        ld.noise_scale = 0.0
+        g = torch.Generator().manual_seed(5)
+        x = torch.randn(B, S, D, generator=g).bfloat16().to(dev).requires_grad_(True)
+        dy = torch.randn(B, S, D, generator=g).to(dev)
+        Md = M.to(dev).requires_grad_(True)
+        if external:
+            kv = mom_kernels.mom_bank_kv_grouped(Md, [ld.k_proj.weight], [ld.v_proj.weight], mem_slots=NB * BS)[0]
+            y = ld(x, Md, kv)
+        else:
+            y = ld(x, Md)
+        (y * dy).sum().backward()
+        res.append((y.detach(), x.grad.clone(), Md.grad.clone(),
+                    {n: p.grad.clone() for n, p in ld.named_parameters()}))
+    (y0, x0, m0, g0), (y1, x1, m1, g1) = res
+    assert torch.equal(y0, y1)
+    assert torch.equal(x0, x1)
+    assert torch.equal(m0, m1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
