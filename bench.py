@@ -171,40 +171,74 @@ def executed_tiles(idx, E, tile=128):
     return int(oh.view(n_tiles, tile, E).any(1).sum()), ("grouped" if int(order[0]) == 1 else "sequence")
 
 
+def cpu_model():
+    """The host CPU's model name (what `lscpu` reports), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, sample_b):
-    """Eager fp32 oracle layer fwd+bwd on the host cores, on `sample_b` of the
-    B sequences at the full T (1 warmup + median of 3)."""
+    """Eager fp32 oracle layer on the host cores, as planned for the CPU
+    baseline: config 2 fwd+bwd on `sample_b` of the B sequences at the full T
+    (all of them by default) and config 1 forward (B=2, T=512), each 2 warmup
+    runs then the median of 5."""
     import torch
 
     import oracle
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
+
+    def make(B, T, D, H, E, BS, K, R):
+        torch.manual_seed(0)
+        layer = oracle.OracleMoMLayer(D, H, E * BS, BS, K, R)
+        with torch.no_grad():
+            for lin in (layer.router_down, layer.router_up, layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
+                lin.weight.normal_(0, 0.02)
+            layer.mom_scale.fill_(1.0)
+        layer.noise_scale = 0.0
+        M = (torch.randn(E, BS * D) * 0.02).requires_grad_(True)
+        x = torch.randn(B, T, D)
+        x = (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)).requires_grad_(True)
+        return layer, M, x, torch.randn(B, T, D)
+
+    def median_time(fn):
+        times = []
+        for _ in range(2 + 5):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times[2:])
+
     B, T, D, H, E, BS, K, R = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS", "K", "R"))
     b = min(sample_b, B)
-    torch.manual_seed(0)
-    layer = oracle.OracleMoMLayer(D, H, E * BS, BS, K, R)
-    with torch.no_grad():
-        for lin in (layer.router_down, layer.router_up, layer.q_proj, layer.k_proj, layer.v_proj, layer.o_proj):
-            lin.weight.normal_(0, 0.02)
-        layer.mom_scale.fill_(1.0)
-    layer.noise_scale = 0.0
-    M = (torch.randn(E, BS * D) * 0.02).requires_grad_(True)
-    x = torch.randn(b, T, D)
-    x = (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)).requires_grad_(True)
-    dy = torch.randn(b, T, D)
-    times = []
-    for i in range(4):
-        t0 = time.perf_counter()
+    layer, M, x, dy = make(b, T, D, H, E, BS, K, R)
+
+    def fwd_bwd():
         y = layer(x, M)
         y.backward(dy)
-        times.append(time.perf_counter() - t0)
         layer.zero_grad(set_to_none=True)
         M.grad = None
         x.grad = None
-    med = statistics.median(times[1:])
+
+    med = median_time(fwd_bwd)
+    del layer, M, x, dy
+    c1 = WORKLOADS["config1"]
+    l1, M1, x1, _ = make(*(c1[k] for k in ("B", "T", "D", "H", "E", "BS", "K", "R")))
+    with torch.no_grad():
+        med1 = median_time(lambda: l1(x1, M1))
     return {"value": round(b * T / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"oracle.OracleMoMLayer fp32 fwd+bwd, {b} of {B} sequences x T={T} "
-                      f"(1 warmup, median of 3 runs: {med:.3f} s), torch {torch.__version__}"}
+                      f"(2 warmup, median of 5 runs: {med:.3f} s), torch {torch.__version__}",
+            "cpu_model": cpu_model(),
+            "config1_forward": {"value": round(c1["B"] * c1["T"] / med1, 1), "unit": "tokens/s",
+                                "ms": round(med1 * 1e3, 2),
+                                "sample": f"oracle.OracleMoMLayer fp32 forward, B={c1['B']} T={c1['T']} "
+                                          f"d={c1['D']} (2 warmup, median of 5)"}}
 
 
 def build_decode(cfg, device):
@@ -499,7 +533,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=2)
+    ap.add_argument("--cpu-sample-batch", type=int, default=8)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the timed region, run 3 plain device copies of this many MiB (a known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
