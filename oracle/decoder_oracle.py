@@ -121,7 +121,7 @@ class OracleDecoder(nn.Module):
         v = a.v_proj(x).view(B, S, H, hd).transpose(1, 2)
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         s = (q @ k.transpose(-1, -2)) * hd ** -0.5
-        mask = torch.ones(S, S, dtype=torch.bool).triu(1)
+        mask = torch.ones(S, S, dtype=torch.bool, device=x.device).triu(1)
         p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1)
         o = (p @ v).transpose(1, 2).reshape(B, S, D)
         return a.o_proj(o)
@@ -136,7 +136,8 @@ class OracleDecoder(nn.Module):
         m = self.model
         h = m.embed_tokens(input_ids)
         B, S, D = h.shape
-        cos, sin = rope_cos_sin(S, D // self.n_heads, self.theta, h.dtype)
+        cos, sin = rope_cos_sin(S, D // self.n_heads, self.theta, h.dtype)  # tables computed on the host
+        cos, sin = cos.to(h.device), sin.to(h.device)
         aux_terms = []
         for i, layer in enumerate(m.layers):
             h = h + self._attention(layer.self_attn, rms_norm(h, layer.input_layernorm.weight, self.eps), cos, sin)

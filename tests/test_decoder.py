@@ -5,7 +5,8 @@ every ReZero scale at 0 the MoM reads add nothing), the product's module tree
 has the reference's parameter names and loads into the oracle strictly, and
 the config-3 decoder has the stated size.  GPU: loss and gradients of the
 product decoder (bf16, fused MoM nodes) against the fp32 CPU oracle on the
-same weights, and gradient-checkpoint exactness.
+same weights, the full-size config-3 decoder's MoM layers and loss against
+the fp32 oracle run on the GPU, and gradient-checkpoint exactness.
 """
 import copy
 
@@ -223,6 +224,63 @@ def test_decoder_loss_and_grads_match_oracle(d_model, dev):
         checked += 1
     assert not bad, bad
     assert checked == len(g32) and "model.M_blocks" in g32
+
+
+@pytest.mark.gpu
+def test_decoder_config3_size_matches_oracle(dev):
+    """The config-3 decoder at full size (20 layers, d=1024, 16 heads, SwiGLU
+    2816, vocabulary 32768, bank 8 x 128 top-2, T=2048; batch 2 of the
+    bench's 8) against the fp32 oracle run on the GPU as the checker
+    (forward only: the backward of a bf16 eager reference is what the small
+    cases above cover).  ReZero scales 0.5 and a bank of Frobenius norm 63 so
+    the reads matter.  Every MoM layer on the input the decoder gave it:
+    routing equal to the fp64 oracle router outside near-ties and output
+    within 1e-2 relative Frobenius of the fp32 oracle layer; the training loss
+    (CE + 0.01 aux) within 1e-2 of the fp32 oracle decoder's with the routing
+    forced to the decoder's."""
+    from naylis_amd.layer import MoMLayer
+    torch.manual_seed(0)
+    cfg = naylis_config()
+    model = NaylisLlamaForCausalLM(cfg)
+    with torch.no_grad():
+        for layer in model.model.layers:
+            layer.mom.mom_scale.fill_(0.5)
+        M = model.model.M_blocks
+        M.mul_(63.0 / float(M.norm()))
+    model = cast_for_training(model).to(dev).train()
+    model.set_noise_scale(0.0)
+    ids = torch.randint(0, cfg.vocab_size, (2, cfg.max_position_embeddings),
+                        generator=torch.Generator().manual_seed(6)).to(dev)
+    moms = [m for m in model.modules() if isinstance(m, MoMLayer)]
+    assert len(moms) == 20
+    caps = {}
+    hooks = [m.register_forward_hook(lambda mod, a, out, key=i: caps.__setitem__(key, (a[0].detach(), out.detach())))
+             for i, m in enumerate(moms)]
+    with torch.no_grad():
+        model(input_ids=ids)
+        for h in hooks:
+            h.remove()
+        routing = [m.last_top_idx.view(2, -1, cfg.mom_top_blocks).long() for m in moms]
+        loss = float(model(input_ids=ids, labels=ids).loss)
+        ref = _oracle_for(cfg).to(dev)
+        ref.load_state_dict({k: v.detach().float() for k, v in model.state_dict().items()}, strict=True)
+        ref.train()
+        for i, m in enumerate(moms):
+            x, y = caps[i][0].float(), caps[i][1].float()
+            rm = ref.model.layers[i].mom
+            logits64, _, idx64, _, _ = oracle.router(x.double(), rm.router_down.weight.double(),
+                                                     rm.router_up.weight.double(), cfg.mom_top_blocks)
+            got = routing[i]
+            srt = logits64.sort(-1, descending=True).values
+            margin = (srt[..., cfg.mom_top_blocks - 1] - srt[..., cfg.mom_top_blocks]).abs()
+            tie = margin <= 1e-5 * logits64.abs().amax(-1)
+            differ = (got.sort(-1).values != idx64.sort(-1).values).any(-1)
+            assert not (differ & ~tie).any(), f"layer {i}: {int((differ & ~tie).sum())} routing differences"
+            want, _, _, _ = oracle.layer_forward(x, rm, ref.model.M_blocks, force_idx=got)
+            assert _rel(y, want) <= 1e-2, f"layer {i}: {_rel(y, want):.3e}"
+            del want
+        loss32, _, _ = ref(ids, labels=ids, routing=routing)
+    assert abs(loss - float(loss32)) <= 1e-2 * abs(float(loss32)), (loss, float(loss32))
 
 
 @pytest.mark.gpu
