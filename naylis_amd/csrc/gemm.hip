@@ -5,14 +5,18 @@
 // whose reduction runs over all tokens.
 //
 // Workgroup tile 128 x 128, K step 64; 4 waves in 2 x 2, each wave 64 x 64 =
-// 2 x 2 MFMA tiles.  Each operand is staged into LDS in its global layout by
-// plain 16-byte copies: a K-contiguous operand as [row][k] (an MFMA fragment
-// is one 16-byte LDS read), an M- or N-contiguous one as [k][row] (a fragment
-// is two gfx950 transposing reads, ds_read_b64_tr_b16).  LDS is double
-// buffered with one barrier per K step; the next step's global loads are in
-// flight during the current step's MFMAs.  With splits > 1 the K range is
-// divided over workgroups, fp32 partials go to a workspace and a fixed-order
-// reduction writes C (deterministic, independent of scheduling).
+// 2 x 2 MFMA tiles (256 x 128 with 8 waves, or 64 x 128 / 64 x 64 for small
+// grids: see the GemmCfg list).  Each operand is staged into LDS in its global
+// layout by plain 16-byte copies: a K-contiguous operand as [row][k] (an MFMA
+// fragment is one 16-byte LDS read), an M- or N-contiguous one as [k][row] (a
+// fragment is two gfx950 transposing reads, ds_read_b64_tr_b16).  LDS is
+// double buffered with one barrier per K step; the next steps' global loads
+// are in flight during the current step's MFMAs.  With splits > 1 the K range
+// is divided over workgroups, fp32 partials go to a workspace and a
+// fixed-order reduction writes C (deterministic, independent of scheduling).
+// A grouped launch runs up to 48 GEMMs of one shape in one grid (the bank
+// projection of all decoder layers), optionally adding their products into
+// one output in job order.
 #include "common.h"
 #include "launch_gemm.h"
 #include "timing.h"
