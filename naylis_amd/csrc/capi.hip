@@ -200,7 +200,7 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   float* dkp = (float*)(ws + w.part);
   float* dvp = (float*)(ws + w.part + part_bytes);
   if (B * S > 0) {
-    rc = hip_status(launch_read_bwd_dq(q, k, v, top_idx, top_gates, out, dout, lse, dq, delta, dlg, d, st),
+    rc = hip_status(launch_read_bwd_dq(q, k, v, top_idx, top_gates, out, dout, lse, dq, delta, dlg, tflags, d, st),
                     "mom_read_bwd dq");
     if (rc) return rc;
   }

@@ -26,7 +26,8 @@ hipError_t launch_read_fwd(const void* q, const void* k, const void* v, const in
 
 hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const int32_t* top_idx,
                               const float* top_gates, const void* o, const void* dout, const float* lse, void* dq,
-                              float* delta, float* dlg_part, const ReadDims& d, hipStream_t st);
+                              float* delta, float* dlg_part, uint8_t* tile_flags, const ReadDims& d,
+                              hipStream_t st);
 
 hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, int32_t* list, int32_t* count,
                                   const ReadDims& d, hipStream_t st);
@@ -92,5 +93,7 @@ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }
 int read_bwd_chunks(const ReadDims& d);
 int read_bwd_n_ttiles(const ReadDims& d);
+// true when launch_read_bwd_dq also writes the dK/dV tile flags (launch_read_tile_lists then skips them)
+bool read_dq_writes_tile_flags(const ReadDims& d);
 
 }  // namespace naylis

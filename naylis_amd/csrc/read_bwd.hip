@@ -307,8 +307,9 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
     const bf16_t* __restrict__ dout, const float* __restrict__ lse, bf16_t* __restrict__ dq,
-    float* __restrict__ delta, float* __restrict__ dlg_part, const int32_t* __restrict__ order, long N, int H,
-    int L, int E, int block_size, int topk, float alpha, float scale, int n_tiles) {
+    float* __restrict__ delta, float* __restrict__ dlg_part, uint8_t* __restrict__ tile_flags,
+    const int32_t* __restrict__ order, long N, int H, int L, int E, int block_size, int topk, float alpha,
+    float scale, int n_tiles) {
   constexpr int HD = 64, KS = HD / 16, NO = HD / 32, PITCH = HD + 8;
   constexpr int NT = 256;
   constexpr int SCH = 4;                       // 32-slot chunks per LDS stage
@@ -319,6 +320,7 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t k_lds[TILE];
   __shared__ __attribute__((aligned(16))) bf16_t v_lds[TILE];
   __shared__ uint8_t flags[kMaxBlocks];
+  __shared__ uint8_t tflags[2][kMaxBlocks];  // per 64-position half (the dK/dV kernel's tiles)
   __shared__ uint32_t chunks[kMaxGroups];  // (block << 16) | chunk index (slot / 32)
   __shared__ int n_chunks_s;
 
@@ -360,14 +362,29 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
   const float lse_t = tok_ok ? lse[(long)h * N + tok] : 0.f;
 
   // ---- the tile's active chunks, ascending
-  for (int e = tid; e < E; e += NT) flags[e] = 0;
+  for (int e = tid; e < E; e += NT) {
+    flags[e] = 0;
+    tflags[0][e] = 0;
+    tflags[1][e] = 0;
+  }
   lds_barrier();
   if (g == 0 && tok_ok) {
 #pragma unroll
     for (int t = 0; t < TK; ++t)
-      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) flags[rt.idx[t]] = 1;
+      if (t < topk && rt.idx[t] >= 0 && rt.idx[t] < E) {
+        flags[rt.idx[t]] = 1;
+        tflags[wave >> 1][rt.idx[t]] = 1;
+      }
   }
   lds_barrier();
+  if (tile_flags != nullptr && h == 0) {
+    // the dK/dV kernel's 64-position tiles 2 tile and 2 tile + 1: which blocks their tokens select
+    const long n_tt = (N + kDkdvTile - 1) / kDkdvTile;
+    for (int i = tid; i < 2 * E; i += NT) {
+      const long t64 = 2L * tile + i / E;
+      if (t64 < n_tt) tile_flags[t64 * E + i % E] = tflags[i / E][i % E];
+    }
+  }
   if (wave == 0) {
     const int cpb = block_size >> 5;  // chunks per block
     int total = 0;
@@ -524,8 +541,7 @@ __global__ __launch_bounds__(256, TK <= 2 ? 3 : 2) void read_bwd_dq_fast_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Active 64-token tiles per 128-slot group.
-constexpr int kDkdvTile = 64;
+// Active 64-token tiles per 128-slot group (kDkdvTile positions of the token order each).
 
 // tile_flags[tile][e] = 1 when a token of the tile (64 positions of the token
 // order) selects block e
@@ -986,18 +1002,19 @@ static void dq_inst(const void* q, const void* k, const void* v, const int32_t* 
 
 template <int HD, int TK>
 static void dq_hdk(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
-                   const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
-                   hipStream_t st) {
+                   const void* dout, const float* lse, void* dq, float* delta, float* dlg, uint8_t* tflags,
+                   const ReadDims& d, hipStream_t st) {
   if constexpr (HD == 64) {
-    if (d.block_size % 32 == 0) {  // the staged kernel (every Naylis configuration)
+    if (read_dq_writes_tile_flags(d)) {  // the staged kernel (every Naylis configuration)
       const long N = (long)d.B * d.S;
       const int n_tiles = (int)((N + 127) / 128);
       const float scale = read_scale(HD);
       NAYLIS_TIMED("read_bwd_dq", st,
                    hipLaunchKernelGGL((read_bwd_dq_fast_kernel<TK>), dim3(d.H * n_tiles), dim3(256), 0, st,
                                       (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
-                                      (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, d.order,
-                                      N, d.H, d.L, d.E, d.block_size, d.topk, scale * kLog2e, scale, n_tiles));
+                                      (const bf16_t*)o, (const bf16_t*)dout, lse, (bf16_t*)dq, delta, dlg, tflags,
+                                      d.order, N, d.H, d.L, d.E, d.block_size, d.topk, scale * kLog2e, scale,
+                                      n_tiles));
       return;
     }
   }
@@ -1012,22 +1029,25 @@ static void dq_hdk(const void* q, const void* k, const void* v, const int32_t* t
 
 template <int HD>
 static void dq_hd(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg, const void* o,
-                  const void* dout, const float* lse, void* dq, float* delta, float* dlg, const ReadDims& d,
-                  hipStream_t st) {
+                  const void* dout, const float* lse, void* dq, float* delta, float* dlg, uint8_t* tflags,
+                  const ReadDims& d, hipStream_t st) {
   if (d.topk <= 2)
-    dq_hdk<HD, 2>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_hdk<HD, 2>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, tflags, d, st);
   else
-    dq_hdk<HD, kMaxTopK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, d, st);
+    dq_hdk<HD, kMaxTopK>(q, k, v, ti, tg, o, dout, lse, dq, delta, dlg, tflags, d, st);
 }
+
+bool read_dq_writes_tile_flags(const ReadDims& d) { return d.HD == 64 && d.block_size % 32 == 0; }
 
 hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const int32_t* top_idx,
                               const float* top_gates, const void* o, const void* dout, const float* lse, void* dq,
-                              float* delta, float* dlg_part, const ReadDims& d, hipStream_t st) {
+                              float* delta, float* dlg_part, uint8_t* tile_flags, const ReadDims& d,
+                              hipStream_t st) {
   switch (d.HD) {
-    case 16: dq_hd<16>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 32: dq_hd<32>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 64: dq_hd<64>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
-    case 128: dq_hd<128>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, d, st); break;
+    case 16: dq_hd<16>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, tile_flags, d, st); break;
+    case 32: dq_hd<32>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, tile_flags, d, st); break;
+    case 64: dq_hd<64>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, tile_flags, d, st); break;
+    case 128: dq_hd<128>(q, k, v, top_idx, top_gates, o, dout, lse, dq, delta, dlg_part, tile_flags, d, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1049,7 +1069,8 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
                                   const ReadDims& d, hipStream_t st) {
   const long ntok = (long)d.B * d.S;
   const int n_tt = read_bwd_n_ttiles(d);
-  if (n_tt > 0)
+  // the staged dQ kernel already wrote the flags (launch_read_bwd_dq runs first)
+  if (n_tt > 0 && !read_dq_writes_tile_flags(d))
     NAYLIS_TIMED("read_tile_lists", st,
                  hipLaunchKernelGGL(read_tile_flags_kernel, dim3(n_tt), dim3(64), 0, st, top_idx, d.order, tile_flags,
                                     ntok, d.E, d.topk));
