@@ -85,7 +85,7 @@ int check_read_dims(int64_t B, int64_t S, int64_t H, int64_t hd, int64_t num_blo
 struct ReadWs {
   size_t delta, dlg, tile_flags, list, count, part;  // byte offsets
   size_t total;
-  int n_chunks;
+  int n_parts;
 };
 
 // The forward needs no workspace; the backward's layout is below.
@@ -94,7 +94,7 @@ ReadWs plan_read_ws(const ReadDims& d) {
   const size_t ntok = (size_t)d.B * d.S;
   const size_t n_tt = (size_t)read_bwd_n_ttiles(d);
   const size_t n_sg = (size_t)read_lq(d.L) / 128;
-  w.n_chunks = read_bwd_chunks(d);
+  w.n_parts = read_bwd_parts(d);
   size_t off = 0;
   w.delta = off;
   off += align256(ntok * d.H * 4);
@@ -107,7 +107,7 @@ ReadWs plan_read_ws(const ReadDims& d) {
   w.count = off;
   off += align256(n_sg * 4);
   w.part = off;
-  off += 2 * align256((size_t)w.n_chunks * read_lq(d.L) * d.H * d.HD * 4);
+  off += 2 * align256((size_t)w.n_parts * 128 * d.H * d.HD * 4);
   w.total = off;
   return w;
 }
@@ -196,7 +196,7 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   uint8_t* tflags = (uint8_t*)(ws + w.tile_flags);
   int32_t* list = (int32_t*)(ws + w.list);
   int32_t* count = (int32_t*)(ws + w.count);
-  const size_t part_bytes = align256((size_t)w.n_chunks * read_lq(d.L) * d.H * d.HD * 4);
+  const size_t part_bytes = align256((size_t)w.n_parts * 128 * d.H * d.HD * 4);
   float* dkp = (float*)(ws + w.part);
   float* dvp = (float*)(ws + w.part + part_bytes);
   if (B * S > 0) {
@@ -206,11 +206,11 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   }
   rc = hip_status(launch_read_tile_lists(top_idx, tflags, list, count, d, st), "mom_read_bwd tile lists");
   if (rc) return rc;
-  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dkp, dvp,
-                                       w.n_chunks, d, st),
+  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dkp, dvp, d,
+                                       st),
                   "mom_read_bwd dkdv");
   if (rc) return rc;
-  return hip_status(launch_read_bwd_reduce(dkp, dvp, dlg, top_gates, dk, dv, dgates, w.n_chunks, d, st),
+  return hip_status(launch_read_bwd_reduce(dkp, dvp, count, dlg, top_gates, dk, dv, dgates, d, st),
                     "mom_read_bwd reduce");
 }
 

@@ -35,10 +35,10 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const void* dout, const float* lse, const float* delta,
                                 const int32_t* list, const int32_t* count, float* dk_part, float* dv_part,
-                                int n_chunks, const ReadDims& d, hipStream_t st);
+                                const ReadDims& d, hipStream_t st);
 
-hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const float* dlg_part,
-                                  const float* top_gates, void* dk, void* dv, float* dgates, int n_chunks,
+hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const int32_t* count,
+                                  const float* dlg_part, const float* top_gates, void* dk, void* dv, float* dgates,
                                   const ReadDims& d, hipStream_t st);
 
 // Decode step (decode.hip): B sequences, D = H * HD features, router rank R,
@@ -91,7 +91,9 @@ hipError_t launch_xent(const void* logits, const int64_t* labels, float* loss, f
 // helpers shared by the workspace planner and the launchers
 inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
 inline int read_lq(int L) { return round_up(L, 128); }
-int read_bwd_chunks(const ReadDims& d);
+// the dK/dV pass's ranges per head and fp32 partials (128 slot rows each)
+int read_bwd_ranges(const ReadDims& d);
+int read_bwd_parts(const ReadDims& d);
 int read_bwd_n_ttiles(const ReadDims& d);
 // true when launch_read_bwd_dq also writes the dK/dV tile flags (launch_read_tile_lists then skips them)
 bool read_dq_writes_tile_flags(const ReadDims& d);

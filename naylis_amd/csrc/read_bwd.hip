@@ -13,13 +13,14 @@
 //     dlog_gates (sum of dS over each selected block).
 //  2. read_tile_flags / read_tile_lists — which 64-token tiles select any
 //     block of each 128-slot group, as compact ascending lists.
-//  3. read_bwd_dkdv_kernel — one workgroup per (h, 128-slot group, share of
-//     that group's active tiles), 4 waves of 32 slots; K/V rows of its slots
-//     stay in registers;
+//  3. read_bwd_dkdv_kernel — one workgroup per (h, equal range of the
+//     (128-slot group, active tile) items), 4 waves of 32 slots; K/V rows of
+//     the current group's slots stay in registers;
 //     S, dP, dS per tile, dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
-//     read transposed from the natural-layout tiles; fp32 partials per share.
-//  4. read_bwd_reduce_kernel — one launch: partials summed over shares in a
-//     fixed order (dk scaled), per-head dlog partials summed over heads and
+//     read transposed from the natural-layout tiles; an fp32 partial per
+//     (range, group) segment.
+//  4. read_bwd_reduce_kernel — one launch: each group's partials summed in
+//     range order (dk scaled), per-head dlog partials summed over heads and
 //     mapped to d(top_gates) through log(max(g, 1e-9)).
 #include "launch.h"
 #include "read_common.h"
@@ -594,29 +595,58 @@ __global__ __launch_bounds__(256) void read_tile_lists_kernel(const uint8_t* __r
   if (threadIdx.x == 0) count[sg] = total;
 }
 
-// dK / dV over the shared bank.  Wave w owns slots 128 sg + 32 (w & 3) +
-// lane%32.  NH = 2: 8 waves, the token half (w >> 2) of each 64-token tile,
-// one workgroup per CU at head_dim 64.  NH = 1: 4 waves, each walking both
-// token halves, so two workgroups share a CU and the two waves on a SIMD
-// belong to different workgroups: they drift apart and one's MFMA work
-// overlaps the other's exp2 work instead of both waiting on the same phase.
+// Work split of the dK / dV pass.  Its items are the (128-slot group, active
+// 64-token tile) pairs, group-major: group sg owns items [pre[sg], pre[sg+1])
+// with pre the exclusive prefix of the per-group tile counts.  Per head the
+// items are cut into R equal contiguous ranges (the last ones may be short or
+// empty), one workgroup each, so every workgroup does the same number of
+// tiles however unevenly the groups are selected.  A range that crosses into
+// another group writes the partial of the group it leaves and starts afresh:
+// the segment (range r, group sg) writes partial r + sg, which is unique
+// (a later group in the same or a later range has a larger sum), and group
+// sg's partials are r + sg for r in [pre[sg] / per, (pre[sg+1] - 1) / per].
+//
+// Exclusive prefix of count[0 .. n_sg) into pre[0 .. n_sg], pre[n_sg] the
+// total, by one wave (n_sg <= kMaxSlotGroups = 128: two groups per lane).
+__device__ __forceinline__ void tile_count_prefix(const int32_t* __restrict__ count, int n_sg, int* pre) {
+  const int lane = threadIdx.x & 63;
+  const int c0 = 2 * lane < n_sg ? count[2 * lane] : 0;
+  const int c1 = 2 * lane + 1 < n_sg ? count[2 * lane + 1] : 0;
+  int incl = c0 + c1;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  const int excl = incl - c0 - c1;
+  if (2 * lane < n_sg) pre[2 * lane] = excl;
+  if (2 * lane + 1 < n_sg) pre[2 * lane + 1] = excl + c0;
+  if (lane == 63) pre[n_sg] = incl;
+}
+
+// dK / dV over the shared bank.  One workgroup per (head, range of items);
+// four waves, wave w owning slots 128 sg + 32 w + lane%32 of the current
+// group, whose K / V rows it holds in registers.  Two workgroups share a CU,
+// so the two waves on a SIMD belong to different workgroups: they drift apart
+// and one's MFMA work overlaps the other's exp2 work (one 8-wave workgroup
+// per CU, waves splitting each tile's tokens, measured 4-6 % slower).
 // Lanes own slots (S = Q K^T orientation), so P and dS come out of the
 // accumulators already in the B-operand layout of dV^T = dO^T P and
 // dK^T = Q^T dS, whose A operands are read transposed from the tiles.
-template <int HD, bool ALIGNED, int TK, bool SPLIT_V, int NH>
-__global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
+template <int HD, bool ALIGNED, int TK, bool SPLIT_V>
+__global__ __launch_bounds__(256, 2) void read_bwd_dkdv_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, const int32_t* __restrict__ tile_list,
     const int32_t* __restrict__ tile_count, float* __restrict__ dk_part, float* __restrict__ dv_part,
     const int32_t* __restrict__ order, long ntok, int H, int L, int Lq, int E, int block_size, int topk, float alpha,
-    int n_chunks, int n_ttiles) {
+    int R, int n_ttiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NO = HDP / 32;
   constexpr int TT = kDkdvTile;
   constexpr int PITCH = HDP + 8;
-  constexpr int NT = 256 * NH;
+  constexpr int NT = 256;
   constexpr int VEC = TT * HD / 8;        // 16-byte vectors per staged tensor tile
   constexpr int PER = (VEC + NT - 1) / NT;
 
@@ -628,44 +658,55 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
   __shared__ int32_t idx_lds2[2][TT * TK];
   __shared__ float lg_lds2[2][TT * TK];
   __shared__ float lse_lds2[2][TT];
-  __shared__ __attribute__((aligned(16))) float red[NH == 2 ? 4 * NO * 16 * 64 : 1];  // half-1 partials (NH = 2)
+  __shared__ int pre[kMaxSlotGroups + 1];
 
   const int n_sg = Lq / 128;
-  const int G = H * n_sg * n_chunks;
-  const int wid = xcd_remap(blockIdx.x, G);
-  const int chunk = wid % n_chunks;
-  const int sg = (wid / n_chunks) % n_sg;
-  const int h = wid / (n_chunks * n_sg);
+  const int wid = xcd_remap(blockIdx.x, H * R);
+  const int r = wid % R;
+  const int h = wid / R;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int quarter = wave & 3, half = NH == 2 ? wave >> 2 : 0;
   const int g = lane >> 5;
   const int col = lane & 31;
-  const int slot = sg * 128 + quarter * 32 + col;
-  const bool slot_ok = slot < L;
   const int D = H * HD;
-  const int lane_blk = slot / block_size;
 
-  // this workgroup's share of the group's active tiles
-  const int cnt = tile_count[sg];
-  const int per = (cnt + n_chunks - 1) / n_chunks;
-  const int i_begin = min(cnt, chunk * per), i_end = min(cnt, i_begin + per);
-  const int32_t* tiles = tile_list + (long)sg * n_ttiles;
+  if (wave == 0) tile_count_prefix(tile_count, n_sg, pre);
+  lds_barrier();
+  const int total = pre[n_sg];
+  const int per = (total + R - 1) / R;
+  const int i_begin = min(total, r * per), i_end = min(total, i_begin + per);
+  if (i_begin >= i_end) return;  // uniform over the workgroup
+  // first group at or after `s` whose items reach past item j
+  auto group_of = [&](int j, int s) {
+    while (j >= pre[s + 1]) ++s;
+    return s;
+  };
+  auto item_tile = [&](int j, int s) { return tile_list[(long)s * n_ttiles + (j - pre[s])]; };
 
+  // the current group's slots and K / V rows
+  int sgc = group_of(i_begin, 0);
+  int slot = 0, lane_blk = 0;
+  bool slot_ok = false;
   bf16x8 kf[KS], vf[KS];
+  auto load_kv = [&]() {
+    slot = sgc * 128 + wave * 32 + col;
+    slot_ok = slot < L;
+    lane_blk = slot / block_size;
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (slot_ok) {
-      const long off = (long)slot * D + (long)h * HD + 16 * ks + 8 * g;
-      kf[ks] = *reinterpret_cast<const bf16x8*>(k + off);
-      vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
-    } else {
-      kf[ks] = bf16x8{};
-      vf[ks] = bf16x8{};
+    for (int ks = 0; ks < KS; ++ks) {
+      if (slot_ok) {
+        const long off = (long)slot * D + (long)h * HD + 16 * ks + 8 * g;
+        kf[ks] = *reinterpret_cast<const bf16x8*>(k + off);
+        vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
+      } else {
+        kf[ks] = bf16x8{};
+        vf[ks] = bf16x8{};
+      }
     }
-  }
+  };
+  load_kv();
   f32x16 acc_dk[NO], acc_dv[NO];
 #pragma unroll
   for (int j = 0; j < NO; ++j) {
@@ -686,10 +727,10 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
   // per-thread constant part of the tile copy: row (token in tile) and column
   int cp_row[PER], cp_col[PER];
 #pragma unroll
-  for (int r = 0; r < PER; ++r) {
-    const int vi = tid + NT * r;
-    cp_row[r] = vi < VEC ? vi / (HD / 8) : TT;
-    cp_col[r] = h * HD + 8 * (vi % (HD / 8));
+  for (int rr = 0; rr < PER; ++rr) {
+    const int vi = tid + NT * rr;
+    cp_row[rr] = vi < VEC ? vi / (HD / 8) : TT;
+    cp_col[rr] = h * HD + 8 * (vi % (HD / 8));
   }
   // Tokens of a tile (rows of this thread's copies, and row tid < TT for the
   // routing / statistics), fetched from the token order one tile ahead of the
@@ -704,9 +745,9 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
     const long pos0 = (long)tt * TT;
     const int rows = (int)min((long)TT, ntok - pos0);
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      rpos[r] = cp_row[r] < rows ? pos0 + cp_row[r] : -1;
-      if (ord != nullptr && rpos[r] >= 0) rraw[r] = ord[rpos[r]];
+    for (int rr = 0; rr < PER; ++rr) {
+      rpos[rr] = cp_row[rr] < rows ? pos0 + cp_row[rr] : -1;
+      if (ord != nullptr && rpos[rr] >= 0) rraw[rr] = ord[rpos[rr]];
     }
     tpos = (tid < TT && tid < rows) ? pos0 + tid : -1;
     if (ord != nullptr && tpos >= 0) traw = ord[tpos];
@@ -718,18 +759,18 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
   auto load_tile = [&]() {
     long rtok[PER];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) rtok[r] = token_at(rpos[r], rraw[r]);
+    for (int rr = 0; rr < PER; ++rr) rtok[rr] = token_at(rpos[rr], rraw[rr]);
     const long ttok = token_at(tpos, traw);
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
+    for (int rr = 0; rr < PER; ++rr) {
       uint4 qv = make_uint4(0, 0, 0, 0), dv4 = make_uint4(0, 0, 0, 0);
-      if (rtok[r] >= 0) {
-        const long off = rtok[r] * D + cp_col[r];
+      if (rtok[rr] >= 0) {
+        const long off = rtok[rr] * D + cp_col[rr];
         qv = *reinterpret_cast<const uint4*>(q + off);
         dv4 = *reinterpret_cast<const uint4*>(dout + off);
       }
-      qreg[r] = qv;
-      dreg[r] = dv4;
+      qreg[rr] = qv;
+      dreg[rr] = dv4;
     }
     if (tid < TT) {
       const bool ok = ttok >= 0;
@@ -743,7 +784,8 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
       pdl = ok ? delta[(long)h * ntok + tk] : 0.f;
     }
   };
-  auto store_tile = [&](int buf) {
+  // stores the prefetched tile; sg: the group the tile is read against
+  auto store_tile = [&](int buf, int sg) {
     bf16_t* q_lds = q_lds2[buf];
     bf16_t* do_lds = do_lds2[buf];
     float(*add_lds)[TT] = add_lds2[buf];
@@ -752,12 +794,12 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
     float* lg_lds = lg_lds2[buf];
     float* lse_lds = lse_lds2[buf];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int vi = tid + NT * r;
+    for (int rr = 0; rr < PER; ++rr) {
+      const int vi = tid + NT * rr;
       if (vi < VEC) {
         const int row = vi / (HD / 8), c8 = vi % (HD / 8);
-        *reinterpret_cast<uint4*>(&q_lds[row * PITCH + 8 * c8]) = qreg[r];
-        *reinterpret_cast<uint4*>(&do_lds[row * PITCH + 8 * c8]) = dreg[r];
+        *reinterpret_cast<uint4*>(&q_lds[row * PITCH + 8 * c8]) = qreg[rr];
+        *reinterpret_cast<uint4*>(&do_lds[row * PITCH + 8 * c8]) = dreg[rr];
       }
     }
     if (tid < TT) {
@@ -787,22 +829,49 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
       }
     }
   };
+  // this segment's sums into partial r + sgc (rows of the group's slots)
+  auto flush = [&]() {
+    if (!slot_ok) return;
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int f0 = 32 * j + 16 * g;
+      if (f0 < HD) {
+        const long base = ((long)(r + sgc) * 128 + wave * 32 + col) * D + (long)h * HD + f0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          *reinterpret_cast<f32x4*>(dk_part + base + 4 * u) =
+              f32x4{acc_dk[j][4 * u], acc_dk[j][4 * u + 1], acc_dk[j][4 * u + 2], acc_dk[j][4 * u + 3]};
+          *reinterpret_cast<f32x4*>(dv_part + base + 4 * u) =
+              f32x4{acc_dv[j][4 * u], acc_dv[j][4 * u + 1], acc_dv[j][4 * u + 2], acc_dv[j][4 * u + 3]};
+        }
+      }
+    }
+  };
 
-  if (i_begin < i_end) {
-    fetch_tokens(tiles[i_begin]);
-    load_tile();
+  // groups of items it + 1 .. it + 3 (the pipeline's stages), walked forward
+  int sg1 = sgc, sg2 = sgc, sg3 = sgc;
+  fetch_tokens(item_tile(i_begin, sgc));
+  load_tile();
+  if (i_begin + 1 < i_end) {
+    sg1 = group_of(i_begin + 1, sgc);
+    fetch_tokens(item_tile(i_begin + 1, sg1));
   }
-  if (i_begin + 1 < i_end) fetch_tokens(tiles[i_begin + 1]);
-  if (i_begin < i_end) store_tile(0);
+  store_tile(0, sgc);
   if (i_begin + 1 < i_end) load_tile();                  // tile i_begin + 1 in flight
-  if (i_begin + 2 < i_end) fetch_tokens(tiles[i_begin + 2]);
+  if (i_begin + 2 < i_end) {
+    sg2 = group_of(i_begin + 2, sg1);
+    fetch_tokens(item_tile(i_begin + 2, sg2));
+  }
   lds_barrier();
   for (int it = i_begin; it < i_end; ++it) {
     const int buf = (it - i_begin) & 1;
     // tile it + 1 into the other buffer (last read before the previous barrier)
-    if (it + 1 < i_end) store_tile(buf ^ 1);
+    if (it + 1 < i_end) store_tile(buf ^ 1, sg1);
     if (it + 2 < i_end) load_tile();                       // in flight during the math below
-    if (it + 3 < i_end) fetch_tokens(tiles[it + 3]);       // the tokens of the tile after
+    if (it + 3 < i_end) {                                  // the tokens of the tile after
+      sg3 = group_of(it + 3, sg2);
+      fetch_tokens(item_tile(it + 3, sg3));
+    }
     const bf16_t* q_lds = q_lds2[buf];
     const bf16_t* do_lds = do_lds2[buf];
     const float(*add_lds)[TT] = add_lds2[buf];
@@ -811,19 +880,18 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
     const float* lg_lds = lg_lds2[buf];
     const float* lse_lds = lse_lds2[buf];
 
-    // NH = 2: this wave's token half; NH = 1: both halves in turn
 #pragma unroll
-    for (int hh = (NH == 2 ? half : 0); hh < (NH == 2 ? half + 1 : 2); ++hh) {
+    for (int hh = 0; hh < 2; ++hh) {  // the tile's two 32-token halves
       // ---- S = Q K^T and dP - delta = dO V^T - delta for this wave's 32 tokens x
       // 32 slots (the dP accumulator starts at -delta of each register's token)
       f32x16 acc_s = f32x16{}, acc_p;
-  #pragma unroll
+#pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
         const f32x4 nd4 = *reinterpret_cast<const f32x4*>(&dl_lds[32 * hh + 8 * j4 + 4 * g]);
-  #pragma unroll
+#pragma unroll
         for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd4[u];
       }
-  #pragma unroll
+#pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int off = (32 * hh + col) * PITCH + 16 * ks + 8 * g;
         const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[off]);
@@ -832,18 +900,18 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
         acc_p = mfma32(ad, vf[ks], acc_p);
       }
       // ---- P and dS, registers indexed by token
-  #pragma unroll
+#pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
         const int r0 = 32 * hh + 8 * j4 + 4 * g;  // tokens r0 .. r0+3 in registers 4*j4 .. 4*j4+3
         f32x4 ad4;
         if constexpr (ALIGNED) {
-          ad4 = *reinterpret_cast<const f32x4*>(&add_lds[quarter][r0]);
+          ad4 = *reinterpret_cast<const f32x4*>(&add_lds[wave][r0]);
         } else {
-  #pragma unroll
+#pragma unroll
           for (int u = 0; u < 4; ++u) {
             float c = 0.f;
             bool sel = false;
-  #pragma unroll
+#pragma unroll
             for (int t = 0; t < TK; ++t)
               if (t < topk && idx_lds[(r0 + u) * TK + t] == lane_blk) {
                 c += lg_lds[(r0 + u) * TK + t];
@@ -852,7 +920,7 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
             ad4[u] = (sel && slot_ok) ? c - lse_lds[r0 + u] : -INFINITY;
           }
         }
-  #pragma unroll
+#pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int vv = 4 * j4 + u;
           const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, ad4[u]));
@@ -864,7 +932,7 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
       // dV sums P over thousands of tokens, so P enters as hi + lo bf16 parts
       // (hi = bf16(P), lo = bf16(P - hi)); bf16 rounding of P would otherwise
       // dominate the error of small dV entries.
-  #pragma unroll
+#pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         bf16x8 bp, bp_lo;
         if constexpr (SPLIT_V)
@@ -872,7 +940,7 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
         else
           bp = pack8(acc_s, 8 * kk);
         const bf16x8 bd = pack8(acc_p, 8 * kk);
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < NO; ++j) {
           const bf16x8 a_do = lds_frag_T<true, true>(do_lds, PITCH, 32 * hh + 16 * kk, 32 * j);
           const bf16x8 a_q = lds_frag_T<true, true>(q_lds, PITCH, 32 * hh + 16 * kk, 32 * j);
@@ -883,79 +951,59 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void read_bwd_dkdv_kernel(
       }
     }
     lds_barrier();  // every wave is done with buffer buf before it is refilled
-  }
-
-  // ---- sum the two token halves (fixed order, NH = 2), write this share's partials
-  if constexpr (NH == 2) {
-  lds_barrier();
-  if (half == 1) {
+    if (it + 1 == i_end || sg1 != sgc) {  // the segment of group sgc ends with this tile
+      flush();
+      if (it + 1 < i_end) {
+        sgc = sg1;
+        load_kv();
 #pragma unroll
-    for (int j = 0; j < NO; ++j)
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dk[j][vv];
-  }
-  lds_barrier();
-  if (half == 0) {
-#pragma unroll
-    for (int j = 0; j < NO; ++j)
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) acc_dk[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
-  }
-  lds_barrier();
-  if (half == 1) {
-#pragma unroll
-    for (int j = 0; j < NO; ++j)
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) red[((quarter * NO + j) * 16 + vv) * 64 + lane] = acc_dv[j][vv];
-  }
-  lds_barrier();
-  if (half == 0) {
-#pragma unroll
-    for (int j = 0; j < NO; ++j)
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) acc_dv[j][vv] += red[((quarter * NO + j) * 16 + vv) * 64 + lane];
-  }
-  }
-  if (half == 0 && slot_ok) {
-#pragma unroll
-    for (int j = 0; j < NO; ++j) {
-      const int f0 = 32 * j + 16 * g;
-      if (f0 < HD) {
-        const long base = ((long)chunk * Lq + slot) * D + (long)h * HD + f0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          *reinterpret_cast<f32x4*>(dk_part + base + 4 * u) =
-              f32x4{acc_dk[j][4 * u], acc_dk[j][4 * u + 1], acc_dk[j][4 * u + 2], acc_dk[j][4 * u + 3]};
-          *reinterpret_cast<f32x4*>(dv_part + base + 4 * u) =
-              f32x4{acc_dv[j][4 * u], acc_dv[j][4 * u + 1], acc_dv[j][4 * u + 2], acc_dv[j][4 * u + 3]};
+        for (int j = 0; j < NO; ++j) {
+          acc_dk[j] = f32x16{};
+          acc_dv[j] = f32x16{};
         }
       }
     }
+    sg1 = sg2;
+    sg2 = sg3;
   }
 }
 
 // One launch for both reductions of the backward: workgroups [0, kv_blocks)
 // sum the dK/dV partials, the rest the per-head dlog partials.
 //
-// dk/dv = sum over shares (fixed order) of the fp32 partials; dk scaled.
+// dk / dv of a slot = the sum of its group's partials in ascending range order
+// (a fixed order; the work split above), dk scaled.  A workgroup takes whole
+// slot rows; pre: LDS for the group prefix.
 __device__ __forceinline__ void read_bwd_reduce_kv(const float* __restrict__ dk_part,
-                                                   const float* __restrict__ dv_part, bf16_t* __restrict__ dk,
-                                                   bf16_t* __restrict__ dv, long n, long stride, int n_chunks,
-                                                   float scale, long blk, long nblk) {
-  for (long i = blk * (long)blockDim.x + threadIdx.x; i < n / 4; i += nblk * blockDim.x) {
-    f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < n_chunks; ++c) {
-      sk += *reinterpret_cast<const f32x4*>(dk_part + c * stride + 4 * i);
-      sv += *reinterpret_cast<const f32x4*>(dv_part + c * stride + 4 * i);
-    }
-    bf16x4 ok, ov;
+                                                   const float* __restrict__ dv_part,
+                                                   const int32_t* __restrict__ tile_count, bf16_t* __restrict__ dk,
+                                                   bf16_t* __restrict__ dv, int L, int n_sg, int D, int R,
+                                                   float scale, long blk, long nblk, int* pre) {
+  if (threadIdx.x < 64) tile_count_prefix(tile_count, n_sg, pre);
+  __syncthreads();
+  const int total = pre[n_sg];
+  const int per = max(1, (total + R - 1) / R);
+  const long stride = 128L * D;  // one partial
+  for (long slot = blk; slot < L; slot += nblk) {
+    const int sg = (int)(slot >> 7);
+    const int lo = pre[sg], hi = pre[sg + 1];
+    const int r0 = lo / per, n = hi > lo ? (hi - 1) / per - r0 + 1 : 0;
+    const long base = ((long)(r0 + sg) * 128 + (slot & 127)) * D;
+    for (int c4 = threadIdx.x; c4 < D / 4; c4 += blockDim.x) {
+      f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < n; ++i) {
+        sk += *reinterpret_cast<const f32x4*>(dk_part + base + i * stride + 4 * c4);
+        sv += *reinterpret_cast<const f32x4*>(dv_part + base + i * stride + 4 * c4);
+      }
+      bf16x4 ok, ov;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ok[u] = (__bf16)(sk[u] * scale);
-      ov[u] = (__bf16)sv[u];
+      for (int u = 0; u < 4; ++u) {
+        ok[u] = (__bf16)(sk[u] * scale);
+        ov[u] = (__bf16)sv[u];
+      }
+      *reinterpret_cast<bf16x4*>(dk + slot * D + 4 * c4) = ok;
+      *reinterpret_cast<bf16x4*>(dv + slot * D + 4 * c4) = ov;
     }
-    *reinterpret_cast<bf16x4*>(dk + 4 * i) = ok;
-    *reinterpret_cast<bf16x4*>(dv + 4 * i) = ov;
   }
 }
 
@@ -973,12 +1021,13 @@ __device__ __forceinline__ void read_bwd_reduce_gates(const float* __restrict__ 
 }
 
 __global__ __launch_bounds__(256) void read_bwd_reduce_kernel(
-    const float* __restrict__ dk_part, const float* __restrict__ dv_part, bf16_t* __restrict__ dk,
-    bf16_t* __restrict__ dv, long n, long stride, int n_chunks, float scale, int kv_blocks,
+    const float* __restrict__ dk_part, const float* __restrict__ dv_part, const int32_t* __restrict__ tile_count,
+    bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int L, int n_sg, int D, int R, float scale, int kv_blocks,
     const float* __restrict__ dlg_part, const float* __restrict__ top_gates, float* __restrict__ dgates, long ng,
     int H) {
+  __shared__ int pre[kMaxSlotGroups + 1];
   if ((int)blockIdx.x < kv_blocks)
-    read_bwd_reduce_kv(dk_part, dv_part, dk, dv, n, stride, n_chunks, scale, blockIdx.x, kv_blocks);
+    read_bwd_reduce_kv(dk_part, dv_part, tile_count, dk, dv, L, n_sg, D, R, scale, blockIdx.x, kv_blocks, pre);
   else
     read_bwd_reduce_gates(dlg_part, top_gates, dgates, ng, H, blockIdx.x - kv_blocks, gridDim.x - kv_blocks);
 }
@@ -1055,15 +1104,10 @@ hipError_t launch_read_bwd_dq(const void* q, const void* k, const void* v, const
 
 int read_bwd_n_ttiles(const ReadDims& d) { return (int)(((long)d.B * d.S + kDkdvTile - 1) / kDkdvTile); }
 
-int read_bwd_chunks(const ReadDims& d) {
-  // shares per 128-slot group: enough workgroups to cover the chip twice
-  const int n_tt = read_bwd_n_ttiles(d);
-  const int per_chunk_wgs = d.H * (read_lq(d.L) / 128);
-  int nc = (512 + per_chunk_wgs - 1) / per_chunk_wgs;
-  if (nc > n_tt) nc = n_tt;
-  if (nc < 1) nc = 1;
-  return nc;
-}
+// ranges of the dK/dV work split per head: the heads' ranges together fill
+// the chip's 256 CUs with two workgroups each
+int read_bwd_ranges(const ReadDims& d) { return d.H >= 512 ? 1 : 512 / d.H; }
+int read_bwd_parts(const ReadDims& d) { return read_bwd_ranges(d) + read_lq(d.L) / 128 - 1; }
 
 hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, int32_t* list, int32_t* count,
                                   const ReadDims& d, hipStream_t st) {
@@ -1080,36 +1124,32 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
   return hipGetLastError();
 }
 
-// four waves per workgroup, two workgroups per CU (NH = 1): measured 4 % faster
-// than one 8-wave workgroup per CU at config 2 and 6 % at config 4
-constexpr int kDkdvNH = 1;
 template <int HD, bool AL, int TK>
 static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg,
                       const void* dout, const float* lse, const float* delta, const int32_t* list,
-                      const int32_t* count, float* dkp, float* dvp, int nc, const ReadDims& d, hipStream_t st) {
+                      const int32_t* count, float* dkp, float* dvp, const ReadDims& d, hipStream_t st) {
   const int Lq = read_lq(d.L);
+  const int R = read_bwd_ranges(d);
   const float alpha = read_scale(HD) * kLog2e;
   NAYLIS_TIMED("read_bwd_dkdv", st,
-               hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true, kDkdvNH>), dim3(d.H * (Lq / 128) * nc),
-                                  dim3(256 * kDkdvNH), 0,
-                                  st, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg,
-                                  (const bf16_t*)dout, lse, delta, list, count, dkp, dvp, d.order,
-                                  (long)d.B * d.S, d.H, d.L, Lq, d.E, d.block_size, d.topk, alpha, nc,
-                                  read_bwd_n_ttiles(d)));
+               hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * R), dim3(256), 0, st,
+                                  (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)dout,
+                                  lse, delta, list, count, dkp, dvp, d.order, (long)d.B * d.S, d.H, d.L, Lq, d.E,
+                                  d.block_size, d.topk, alpha, R, read_bwd_n_ttiles(d)));
 }
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const void* dout, const float* lse, const float* delta,
                                 const int32_t* list, const int32_t* count, float* dk_part, float* dv_part,
-                                int n_chunks, const ReadDims& d, hipStream_t st) {
+                                const ReadDims& d, hipStream_t st) {
   const bool al = d.block_size % 32 == 0;
 #define NAYLIS_DKDV2(HDV, TKV)                                                                                 \
   if (al)                                                                                                      \
-    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part,    \
-                              n_chunks, d, st);                                                                \
+    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part, d, \
+                              st);                                                                             \
   else                                                                                                         \
     dkdv_inst<HDV, false, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part,   \
-                               n_chunks, d, st);
+                               d, st);
 #define NAYLIS_DKDV(HDV)        \
   if (d.topk <= 2) {            \
     NAYLIS_DKDV2(HDV, 2)        \
@@ -1128,21 +1168,18 @@ hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, con
   return hipGetLastError();
 }
 
-hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const float* dlg_part,
-                                  const float* top_gates, void* dk, void* dv, float* dgates, int n_chunks,
+hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const int32_t* count,
+                                  const float* dlg_part, const float* top_gates, void* dk, void* dv, float* dgates,
                                   const ReadDims& d, hipStream_t st) {
-  const long D = (long)d.H * d.HD;
-  const long n = (long)d.L * D;
-  const long stride = (long)read_lq(d.L) * D;
-  long blocks = (n / 4 + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
+  const int D = d.H * d.HD;
+  const int blocks = d.L < 8192 ? d.L : 8192;  // slot rows
   const long ng = (long)d.B * d.S * d.topk;
   long gb = (ng + 255) / 256;
   if (gb > 8192) gb = 8192;
   NAYLIS_TIMED("read_bwd_reduce", st,
                hipLaunchKernelGGL(read_bwd_reduce_kernel, dim3((int)(blocks + gb)), dim3(256), 0, st, dk_part, dv_part,
-                                  (bf16_t*)dk, (bf16_t*)dv, n, stride, n_chunks, read_scale(d.HD), (int)blocks,
-                                  dlg_part, top_gates, dgates, ng, d.H));
+                                  count, (bf16_t*)dk, (bf16_t*)dv, d.L, read_lq(d.L) / 128, D, read_bwd_ranges(d),
+                                  read_scale(d.HD), blocks, dlg_part, top_gates, dgates, ng, d.H));
   return hipGetLastError();
 }
 

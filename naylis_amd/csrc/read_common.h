@@ -8,6 +8,7 @@ namespace naylis {
 constexpr int kMaxTopK = 8;       // selections per token supported in registers
 constexpr int kMaxBlocks = 1024;  // bank blocks (flags live in LDS)
 constexpr int kMaxGroups = 512;   // slot groups of 32 over the whole bank (L <= 16384)
+constexpr int kMaxSlotGroups = kMaxGroups / 4;  // 128-slot groups (dK/dV work split)
 constexpr int kDkdvTile = 64;     // token-order positions per dK/dV tile (tile flags and lists)
 constexpr int kReadWaves = 8;     // waves (x 32 tokens) per forward / dQ workgroup
 
