@@ -63,9 +63,10 @@ static OrderWs plan_order_ws(long N, int E) {
 }
 
 // (1) per chunk of 1024 tokens: key = sorted block pair, rank among the
-// chunk's earlier tokens of the same key (a 64-lane comparison loop inside a
-// wave, per-wave key counts across waves), the chunk's key histogram, and
-// the distinct-block count of each 128-token tile in sequence order.
+// chunk's earlier tokens of the same key (inside a wave one ballot per
+// distinct key of the wave, per-wave key counts across waves), the chunk's
+// key histogram, and the distinct-block count of each 128-token tile in
+// sequence order.
 __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* __restrict__ top_idx,
                                                                 uint16_t* __restrict__ keys, int32_t* __restrict__ rank,
                                                                 int32_t* __restrict__ hist,
@@ -86,12 +87,20 @@ __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* _
     if (b0 >= 0 && b0 < E) mask |= 1u << b0;
   }
   for (int i = tid; i < kOrdWaves * nkeys; i += kOrdChunk) wcnt[i / nkeys][i % nkeys] = 0;
+  // lanes of this wave with the same key, below and above this lane: one
+  // round per distinct key, led by the lowest lane not yet matched
   int before = 0, after = 0;
-#pragma unroll 8
-  for (int j = 0; j < 64; ++j) {
-    const int kj = __shfl(key, j, 64);
-    before += (j < lane && kj == key);
-    after += (j > lane && kj == key);
+  const uint64_t below = (1ull << lane) - 1;
+  uint64_t rem = __ballot(real);
+  while (rem) {
+    const int lead = __builtin_ctzll(rem);
+    const int k = __builtin_amdgcn_readlane(key, lead);
+    const uint64_t m = __ballot(real && key == k);
+    if (real && key == k) {
+      before = __popcll(m & below);
+      after = __popcll(m & ~below) - 1;
+    }
+    rem &= ~m;
   }
   for (int o = 32; o > 0; o >>= 1) mask |= __shfl_xor(mask, o, 64);
   if (lane == 0) wmask[wave] = mask;
@@ -133,6 +142,9 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
                                                                   int nchunks) {
   __shared__ int32_t off[kOrdMaxE * kOrdMaxE];
   __shared__ int32_t ends[kOrdMaxE * kOrdMaxE];  // inclusive scan of the key totals
+  __shared__ int32_t nzs[kOrdMaxE * kOrdMaxE];   // inclusive scan of "key has tokens"
+  __shared__ int32_t cend[kOrdMaxE * kOrdMaxE];  // the keys with tokens, ascending: segment end
+  __shared__ uint32_t cmask[kOrdMaxE * kOrdMaxE];  // and block pair mask
   __shared__ long red[2][kOrdWaves];
   const int nkeys = E * E;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -150,33 +162,46 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
       }
     }
     ends[tid] = all;
+    nzs[tid] = all > 0;
   }
   __syncthreads();
-  for (int st = 1; st < nkeys; st <<= 1) {  // inclusive scan over keys
-    int add = 0;
-    if (tid < nkeys && tid >= st) add = ends[tid - st];
+  for (int st = 1; st < nkeys; st <<= 1) {  // inclusive scans over keys
+    int add = 0, addn = 0;
+    if (tid < nkeys && tid >= st) {
+      add = ends[tid - st];
+      addn = nzs[tid - st];
+    }
     __syncthreads();
-    if (tid < nkeys) ends[tid] += add;
+    if (tid < nkeys) {
+      ends[tid] += add;
+      nzs[tid] += addn;
+    }
     __syncthreads();
   }
-  if (tid < nkeys) off[tid] = ends[tid] - all + before;
+  if (tid < nkeys) {
+    off[tid] = ends[tid] - all + before;
+    if (all > 0) {
+      cend[nzs[tid] - 1] = ends[tid];
+      cmask[nzs[tid] - 1] = (1u << (tid / E)) | (1u << (tid % E));
+    }
+  }
+  __syncthreads();
+  const int nnz = nzs[nkeys - 1];
   // (tile, block) pairs of both orders
   const long ntiles = (N + kOrdTile - 1) / kOrdTile;
   long seq = 0, grp = 0;
   for (long t = tid; t < ntiles; t += kOrdChunk) {
     seq += seqcnt[t];
     const long p0 = t * kOrdTile, p1 = min(N, p0 + kOrdTile);
-    int lo = 0, hi = nkeys - 1;  // first key whose segment ends after p0
+    // the keys with tokens tile [0, N) in order: from the first whose
+    // segment ends after p0, those that start before p1
+    int lo = 0, hi = nnz - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (ends[mid] > p0) hi = mid; else lo = mid + 1;
+      if (cend[mid] > p0) hi = mid; else lo = mid + 1;
     }
     uint32_t mask = 0;
-    for (int key = lo; key < nkeys; ++key) {
-      const int start = key > 0 ? ends[key - 1] : 0;
-      if (start >= p1) break;
-      if (ends[key] > start) mask |= (1u << (key / E)) | (1u << (key % E));
-    }
+    for (int i = lo; i < nnz && (i == 0 ? 0 : cend[i - 1]) < p1; ++i) mask |= cmask[i];
     grp += __popc(mask);
   }
   for (int o = 32; o > 0; o >>= 1) {

@@ -49,6 +49,7 @@ def gpu_order(top_idx, E, dev):
 @pytest.mark.parametrize("B,S,E,k,coherent", [
     (8, 2048, 8, 2, False),    # config 2 geometry, incoherent routing: grouping pays
     (4, 4096, 32, 2, True),    # config 4 style: one block set per 128-token tile, sequence order kept
+    (4, 4096, 32, 2, False),   # 32 blocks, incoherent: hundreds of keys, many of them empty
     (2, 300, 8, 2, False),     # ragged token count
     (2, 300, 8, 3, False),     # top-3: sequence order
     (1, 1000, 64, 2, False),   # more than 32 blocks: sequence order
@@ -74,3 +75,16 @@ def test_read_order_matches_cpu_rule(B, S, E, k, coherent, dev):
         assert np.array_equal(got, np.arange(B * S))
     elif E <= 32 and k == 2 and B * S > 1024:
         assert not np.array_equal(got, np.arange(B * S)), "grouping should pay for incoherent routing"
+
+
+@pytest.mark.parametrize("pairs", [[(3, 3)], [(3, 3), (5, 1), (1, 5), (0, 7)]])
+def test_read_order_repeated_pairs(pairs, dev):
+    """Few keys with long segments (one key covering every tile), and a
+    duplicated id (both selections naming one block)."""
+    g = torch.Generator().manual_seed(len(pairs))
+    B, S, E = 2, 3000, 8
+    pick = torch.randint(0, len(pairs), (B, S), generator=g)
+    idx = torch.tensor(pairs, dtype=torch.int64)[pick]
+    want, _ = cpu_order(idx, E)
+    got = gpu_order(idx, E, dev)
+    assert np.array_equal(got, want)
