@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 12
+#define NAYLIS_MOM_ABI_VERSION 13
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -339,6 +339,12 @@ size_t naylis_mom_rezero_workspace_bytes(int64_t n);
 int naylis_mom_rezero_fwd(const void* z, int z_dtype, const float* s, float* y, int64_t n, void* stream);
 int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dtype, const float* s, void* dz, float* ds,
                           void* workspace, size_t workspace_bytes, int64_t n, void* stream);
+/* y = s * x with y in y_dtype (bf16 or fp32): the gate folded into the o
+ * projection's weight, W' = s * W_o, so that the layer's fp32 output is one
+ * GEMM, o W'^T = s * (o W_o^T) (model.py:239, 251).  The gradients of W_o and
+ * s then follow from dW' (the gradient of W') by naylis_mom_rezero_bwd over
+ * the weight's elements: dW_o = s * dW', ds = sum(dW' * W_o). */
+int naylis_mom_rezero_scale(const void* x, int x_dtype, const float* s, void* y, int y_dtype, int64_t n, void* stream);
 
 /* --------------------------------------------------------- decode step ---
  * One new token per sequence: the O(1) running-sum form of the prefix-mean

@@ -750,6 +750,18 @@ int naylis_mom_rezero_fwd(const void* z, int z_dtype, const float* s, float* y, 
                     "rezero_fwd");
 }
 
+int naylis_mom_rezero_scale(const void* x, int x_dtype, const float* s, void* y, int y_dtype, int64_t n, void* stream) {
+  int rc;
+  if (n < 0) return fail(NAYLIS_ERR_ARG, "rezero_scale: negative size %lld", (long long)n);
+  if ((rc = check_dtype(x_dtype, "rezero_scale"))) return rc;
+  if ((rc = check_dtype(y_dtype, "rezero_scale"))) return rc;
+  if (n == 0) return NAYLIS_OK;
+  if (!x || !s || !y) return fail(NAYLIS_ERR_ARG, "rezero_scale: null pointer argument");
+  return hip_status(launch_rezero_scale(x, x_dtype == NAYLIS_DTYPE_BF16, s, y, y_dtype == NAYLIS_DTYPE_BF16, (long)n,
+                                        (hipStream_t)stream),
+                    "rezero_scale");
+}
+
 int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dtype, const float* s, void* dz, float* ds,
                           void* workspace, size_t workspace_bytes, int64_t n, void* stream) {
   int rc;

@@ -6,6 +6,12 @@
 //     dz = s * dy  (in z's dtype)        ds = sum_i dy_i * z_i  (fp32)
 // The backward is one pass over dy and z; ds is reduced through per-workgroup
 // partials summed in a fixed order (deterministic).
+//
+// The same scale with a bf16 (or fp32) result, y = s * x in y's dtype, folds
+// the gate into the o projection's weight (s * (o W^T) = o (s W)^T): the
+// layer then gets y straight from one GEMM with an fp32 result, and the
+// backward's dW = s * dW' and ds = sum(W * dW'), dW' the gradient of the
+// scaled weight, are this file's backward run over the weight's elements.
 #include "common.h"
 #include "launch_rezero.h"
 #include "timing.h"
@@ -71,9 +77,9 @@ __device__ __forceinline__ void st1(T* p, float x) {
     *p = x;
 }
 
-template <typename ZT>
+template <typename ZT, typename YT>
 __global__ __launch_bounds__(kRzThreads) void rezero_fwd_kernel(const ZT* __restrict__ z, const float* __restrict__ s,
-                                                                float* __restrict__ y, long n, int vec) {
+                                                                YT* __restrict__ y, long n, int vec) {
   const float sc = *s;
   const long base = (long)blockIdx.x * kRzChunk;
   if (vec && base + kRzChunk <= n) {  // whole chunk: every load issued before the first store
@@ -84,14 +90,14 @@ __global__ __launch_bounds__(kRzThreads) void rezero_fwd_kernel(const ZT* __rest
     for (int st = 0; st < kRzSteps; ++st) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[st][e] *= sc;
-      st8<float>(y + base + ((long)st * kRzThreads + threadIdx.x) * kRzVec, v[st]);
+      st8<YT>(y + base + ((long)st * kRzThreads + threadIdx.x) * kRzVec, v[st]);
     }
     return;
   }
   for (int st = 0; st < kRzSteps; ++st) {
     const long i = base + ((long)st * kRzThreads + threadIdx.x) * kRzVec;
     for (int e = 0; e < kRzVec; ++e)
-      if (i + e < n) y[i + e] = sc * ld1<ZT>(z + i + e);
+      if (i + e < n) st1<YT>(y + i + e, sc * ld1<ZT>(z + i + e));
   }
 }
 
@@ -160,19 +166,30 @@ static int n_chunks(long n) { return (int)((n + kRzChunk - 1) / kRzChunk); }
 
 size_t rezero_ws_bytes(long n) { return (size_t)(n_chunks(n) > 0 ? n_chunks(n) : 1) * sizeof(float); }
 
-hipError_t launch_rezero_fwd(const void* z, bool z_bf16, const float* s, float* y, long n, hipStream_t st) {
+template <typename ZT, typename YT>
+static void fwd_launch(const void* z, const float* s, void* y, long n, int vec, hipStream_t st) {
+  NAYLIS_TIMED("rezero_fwd", st,
+               hipLaunchKernelGGL((rezero_fwd_kernel<ZT, YT>), dim3(n_chunks(n)), dim3(kRzThreads), 0, st,
+                                  (const ZT*)z, s, (YT*)y, n, vec));
+}
+
+hipError_t launch_rezero_scale(const void* z, bool z_bf16, const float* s, void* y, bool y_bf16, long n,
+                               hipStream_t st) {
   if (n == 0) return hipSuccess;
   const int vec = ((uintptr_t)z & 15) == 0 && ((uintptr_t)y & 15) == 0;
-  const dim3 grid(n_chunks(n));
-  if (z_bf16)
-    NAYLIS_TIMED("rezero_fwd", st,
-                 hipLaunchKernelGGL((rezero_fwd_kernel<bf16_t>), grid, dim3(kRzThreads), 0, st, (const bf16_t*)z, s,
-                                    y, n, vec));
+  if (z_bf16 && y_bf16)
+    fwd_launch<bf16_t, bf16_t>(z, s, y, n, vec, st);
+  else if (z_bf16)
+    fwd_launch<bf16_t, float>(z, s, y, n, vec, st);
+  else if (y_bf16)
+    fwd_launch<float, bf16_t>(z, s, y, n, vec, st);
   else
-    NAYLIS_TIMED("rezero_fwd", st,
-                 hipLaunchKernelGGL((rezero_fwd_kernel<float>), grid, dim3(kRzThreads), 0, st, (const float*)z, s, y,
-                                    n, vec));
+    fwd_launch<float, float>(z, s, y, n, vec, st);
   return hipGetLastError();
+}
+
+hipError_t launch_rezero_fwd(const void* z, bool z_bf16, const float* s, float* y, long n, hipStream_t st) {
+  return launch_rezero_scale(z, z_bf16, s, y, false, n, st);
 }
 
 template <typename ZT, typename DT>

@@ -134,17 +134,18 @@ class MoMLayer(nn.Module):
                 self._read, x, top_idx, top_gates, M_blocks, k, v, use_reentrant=False, preserve_rng_state=False)
         else:
             out = self._read(x, top_idx, top_gates, M_blocks, k, v)
-        return mom_kernels.mom_rezero(out, self.mom_scale)
+        # o projection and ReZero gate (model.py:251, 239): one GEMM, the gate folded into the weight
+        return mom_kernels.mom_gated_linear(out, self.o_proj.weight, self.mom_scale)
 
     def _read(self, x, top_idx, top_gates, M_blocks, k=None, v=None):
-        """q projection, bank K/V (unless given), gated flash read, o projection (model.py:241-276)."""
+        """q projection, bank K/V (unless given), gated flash read (model.py:241-274)."""
         B, S, D = x.shape
         q_sh = mom_kernels.mom_linear(x, self.q_proj.weight).view(B, S, self.n_heads, self.head_dim)
         if k is None:
             k, v = mom_kernels.mom_bank_kv(M_blocks, self.k_proj.weight, self.v_proj.weight, mem_slots=self.mem_slots)
         out = mom_kernels.mom_read(q_sh, k, v, top_idx, top_gates, num_blocks=self.num_blocks,
                                    block_size=self.block_size, mode=self._kernel_mode)
-        return mom_kernels.mom_linear(out.reshape(B, S, D), self.o_proj.weight)
+        return out.reshape(B, S, D)
 
 
 def mom_aux_loss(layers):

@@ -22,7 +22,7 @@ from .. import _lib
 from .hip_read import mom_read as _hip_mom_read
 
 __all__ = ["HAS_HIP", "preflight", "resolve_mode", "mom_read", "announce", "mom_route",
-           "mom_bank_kv", "mom_bank_kv_grouped", "mom_linear", "mom_rezero", "has_hip", "quantize_bank_fp8", "decode_step",
+           "mom_bank_kv", "mom_bank_kv_grouped", "mom_linear", "mom_rezero", "mom_gated_linear", "has_hip", "quantize_bank_fp8", "decode_step",
            "mom_router_stats"]
 
 _ANNOUNCED = {"backend": None}
@@ -126,6 +126,11 @@ def mom_linear(*args, **kwargs):
 def mom_rezero(*args, **kwargs):
     from .hip_rezero import mom_rezero as _rezero
     return _rezero(*args, **kwargs)
+
+
+def mom_gated_linear(*args, **kwargs):
+    from .hip_rezero import mom_gated_linear as _gated
+    return _gated(*args, **kwargs)
 
 
 def quantize_bank_fp8(*args, **kwargs):

@@ -8,8 +8,13 @@ elementwise kernel, and materialises zero gradients for router outputs the
 loss does not use.  Here the backward runs the library calls in a fixed
 order instead: the q projection's input gradient is written first and the
 router's backward accumulates into it (C ABI dx_accumulate, one bf16 rounding
-of the fp32 sum), and absent output gradients are passed as NULL.  Results
-equal the modular path's to bf16 rounding; the modular Functions stay the
+of the fp32 sum), and absent output gradients are passed as NULL.  The
+ReZero gate is folded into the o projection's weight, s * (out W_o^T) =
+out (s W_o)^T, so the layer's fp32 output is one GEMM with an fp32 result
+(no bf16 z to scale, store and read back); its backward takes dW' = dy^T out
+in fp32 and gets dW_o = s dW' and ds = sum(dW' W_o) from one pass over the
+weight.  Results equal the modular path's to bf16 rounding (W' is rounded
+where the modular path rounds o W_o^T); the modular Functions stay the
 public drop-in API (mom_read etc.) and serve gradient checkpointing.
 """
 from __future__ import annotations
@@ -18,7 +23,9 @@ import torch
 import torch.nn.functional as F
 
 from .. import _lib
+from .hip_linear import library_wgrad as _wgrad
 from .hip_read import read_order
+from .hip_rezero import gated_linear_backward, gated_linear_forward
 from .hip_router import d_probs_arg
 
 _F32, _BF16 = 0, 1
@@ -104,13 +111,12 @@ class MomLayerFunction(torch.autograd.Function):
             _lib.check(lib.naylis_mom_read_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), order.data_ptr(),
                 out.data_ptr(), lse.data_ptr(), None, 0, B, T, H, HD, num_blocks, block_size, top_k, st))
-            z = F.linear(out, w_o)
-            # ---- ReZero gate (model.py:239)
-            y = torch.empty((B, T, D), **f32)
-            _lib.check(lib.naylis_mom_rezero_fwd(z.data_ptr(), _BF16, scale.data_ptr(), y.data_ptr(), z.numel(),
-                                                 st))
+            # ---- o projection and ReZero gate (model.py:251, 239): one GEMM, the gate
+            # folded into the weight
+            y, w_os = gated_linear_forward(lib, out.view(B * T, D), w_o, scale, st)
+            y = y.view(B, T, D)
         ctx.save_for_backward(x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v,
-                              q, order, out, lse, z)
+                              q, order, out, lse, w_os)
         ctx.geom = geom
         ctx.external_bank = k_ext is not None
         ctx.m_shape = None if k_ext is not None else (tuple(M_blocks.shape), m_dtype)
@@ -121,7 +127,7 @@ class MomLayerFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, d_probs, _d_idx):
         (x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order, out, lse,
-         z) = ctx.saved_tensors
+         w_os) = ctx.saved_tensors
         n_heads, num_blocks, block_size, top_k, _ = ctx.geom
         lib = _lib.load()
         B, T, D = x.shape
@@ -133,23 +139,11 @@ class MomLayerFunction(torch.autograd.Function):
         f32 = dict(device=dev, dtype=torch.float32)
         N = B * T
         with _lib.on_device(dev):
-            # ---- ReZero: dz = s dy (bf16), ds = sum(dy z)
+            # ---- o projection with the folded gate (d out, dW_o, ds)
             if dy is None:
-                dy = torch.zeros((B, T, D), **f32)
-            dy = dy.contiguous()
-            dy_dt = _F32 if dy.dtype == torch.float32 else _BF16
-            if dy.dtype not in (torch.float32, torch.bfloat16):
-                dy, dy_dt = dy.float(), _F32
-            dz = torch.empty_like(z)
-            ds = torch.empty(1, **f32)
-            zws = _ws(lib.naylis_mom_rezero_workspace_bytes(z.numel()), dev)
-            _lib.check(lib.naylis_mom_rezero_bwd(dy.data_ptr(), dy_dt, z.data_ptr(), _BF16, scale.data_ptr(),
-                                                 dz.data_ptr(), ds.data_ptr(), zws.data_ptr(), zws.numel(),
-                                                 z.numel(), st))
-            # ---- o projection: d out = dz W_o, dW_o = dz^T out
-            dz2 = dz.view(N, D)
-            dout = torch.mm(dz2, w_o).view(B, T, H, HD)
-            dw_o = _wgrad(lib, out.view(N, D), dz2, w_o.dtype, dev, st)
+                dy = torch.zeros((B, T, D), device=dev, dtype=torch.bfloat16)
+            dout, dw_o, ds = gated_linear_backward(lib, dy.reshape(N, D), out.view(N, D), w_o, w_os, scale, st)
+            dout = dout.view(B, T, H, HD)
             # ---- gated read
             dq = torch.empty_like(q)
             dk = torch.empty_like(k)
@@ -193,22 +187,6 @@ class MomLayerFunction(torch.autograd.Function):
                 dw_up.data_ptr(), rws.data_ptr(), rws.numel(), B, T, D, R, E, top_k, st))
         return (dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None, None, dk_ext,
                 dv_ext)
-
-
-def _wgrad(lib, xin, dy, dtype, dev, st):
-    """dW = dy^T xin over all rows (C ABI naylis_mom_linear_wgrad; its split-K
-    kernel needs N, D_in, D_out multiples of 8 — otherwise the torch product
-    that autograd would use for nn.Linear's weight gradient)."""
-    N, D_in = xin.shape
-    D_out = dy.shape[1]
-    if N % 8 or D_in % 8 or D_out % 8:
-        return torch.mm(dy.t(), xin).to(dtype)
-    ws = _ws(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out), dev)
-    dw = torch.empty((D_out, D_in), device=dev, dtype=dtype)
-    _lib.check(lib.naylis_mom_linear_wgrad(xin.data_ptr(), dy.data_ptr(), dw.data_ptr(),
-                                           _BF16 if dtype == torch.bfloat16 else _F32, ws.data_ptr(), ws.numel(),
-                                           N, D_in, D_out, st))
-    return dw
 
 
 def mom_layer(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, *, n_heads, num_blocks, block_size, top_k,

@@ -40,6 +40,25 @@ def _library_wgrad(x2, dy2, weight):
     return dw
 
 
+def library_wgrad(lib, xin, dy, dtype, dev, st):
+    """dW = dy^T xin over all rows (C ABI naylis_mom_linear_wgrad; its split-K
+    kernel needs N, D_in, D_out multiples of 8 — otherwise the torch product
+    that autograd would use for nn.Linear's weight gradient)."""
+    N, D_in = xin.shape
+    D_out = dy.shape[1]
+    if N % 8 or D_in % 8 or D_out % 8:
+        if dtype == torch.float32:
+            return torch.mm(dy.t(), xin, out_dtype=torch.float32)
+        return torch.mm(dy.t(), xin).to(dtype)
+    ws = torch.empty(max(int(lib.naylis_mom_linear_wgrad_workspace_bytes(N, D_in, D_out)), 1), dtype=torch.uint8,
+                     device=dev)
+    dw = torch.empty((D_out, D_in), device=dev, dtype=dtype)
+    _lib.check(lib.naylis_mom_linear_wgrad(xin.data_ptr(), dy.data_ptr(), dw.data_ptr(),
+                                           _DT[dtype], ws.data_ptr(), ws.numel(),
+                                           N, D_in, D_out, st))
+    return dw
+
+
 class MomLinearFunction(torch.autograd.Function):
 
     @staticmethod

@@ -48,3 +48,25 @@ def test_rezero_deterministic_and_zero_size(dev):
     s = torch.tensor([2.0], device=dev, requires_grad=True)
     mom_kernels.mom_rezero(e, s).backward(torch.zeros(0, device=dev))
     assert float(s.grad) == 0.0
+
+
+@pytest.mark.parametrize("n,xdt,ydt", [
+    (1024 * 1024, torch.bfloat16, torch.bfloat16),   # the o projection's weight, folded gate
+    (1000003, torch.bfloat16, torch.float32),
+    (4099, torch.float32, torch.bfloat16),
+    (7, torch.float32, torch.float32),
+])
+def test_rezero_scale_matches_torch(n, xdt, ydt, dev):
+    """naylis_mom_rezero_scale: y = s x rounded once to y's dtype, bitwise the
+    fp32 product torch forms and rounds (round to nearest even)."""
+    from naylis_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(n % 977)
+    x = torch.randn(n, generator=g).to(xdt).to(dev)
+    s = torch.tensor([0.37], device=dev)
+    y = torch.empty(n, device=dev, dtype=ydt)
+    dt = {torch.float32: 0, torch.bfloat16: 1}
+    _lib.check(lib.naylis_mom_rezero_scale(x.data_ptr(), dt[xdt], s.data_ptr(), y.data_ptr(), dt[ydt], n,
+                                           torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(y, (x.float() * s).to(ydt))
