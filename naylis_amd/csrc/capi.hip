@@ -206,8 +206,8 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   }
   rc = hip_status(launch_read_tile_lists(top_idx, tflags, list, count, d, st), "mom_read_bwd tile lists");
   if (rc) return rc;
-  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dkp, dvp, d,
-                                       st),
+  rc = hip_status(launch_read_bwd_dkdv(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dkp, dvp, dk,
+                                       dv, d, st),
                   "mom_read_bwd dkdv");
   if (rc) return rc;
   return hip_status(launch_read_bwd_reduce(dkp, dvp, count, dlg, top_gates, dk, dv, dgates, d, st),

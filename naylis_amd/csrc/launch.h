@@ -34,8 +34,8 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const void* dout, const float* lse, const float* delta,
-                                const int32_t* list, const int32_t* count, float* dk_part, float* dv_part,
-                                const ReadDims& d, hipStream_t st);
+                                const int32_t* list, const int32_t* count, float* dk_part, float* dv_part, void* dk,
+                                void* dv, const ReadDims& d, hipStream_t st);
 
 hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const int32_t* count,
                                   const float* dlg_part, const float* top_gates, void* dk, void* dv, float* dgates,

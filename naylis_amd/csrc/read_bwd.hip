@@ -639,8 +639,8 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dkdv_kernel(
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, const int32_t* __restrict__ tile_list,
     const int32_t* __restrict__ tile_count, float* __restrict__ dk_part, float* __restrict__ dv_part,
-    const int32_t* __restrict__ order, long ntok, int H, int L, int Lq, int E, int block_size, int topk, float alpha,
-    int R, int n_ttiles) {
+    bf16_t* __restrict__ dk_out, bf16_t* __restrict__ dv_out, float dk_scale, const int32_t* __restrict__ order,
+    long ntok, int H, int L, int Lq, int E, int block_size, int topk, float alpha, int R, int n_ttiles) {
   constexpr int HDP = HD < 32 ? 32 : HD;
   constexpr int KS = HD / 16;
   constexpr int NO = HDP / 32;
@@ -829,9 +829,34 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dkdv_kernel(
       }
     }
   };
-  // this segment's sums into partial r + sgc (rows of the group's slots)
+  // this segment's sums into partial r + sgc (rows of the group's slots); a
+  // segment holding all of the group's items is the group's whole sum and
+  // goes straight to dk / dv as the reduce would write it (the reduce skips
+  // groups with one segment)
   auto flush = [&]() {
     if (!slot_ok) return;
+    if (pre[sgc] >= i_begin && pre[sgc + 1] <= i_end) {
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int f0 = 32 * j + 16 * g;
+        if (f0 < HD) {
+          const long o = (long)slot * D + (long)h * HD + f0;
+          bf16x8 k0, k1, v0, v1;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            k0[e] = (__bf16)(acc_dk[j][e] * dk_scale);
+            k1[e] = (__bf16)(acc_dk[j][8 + e] * dk_scale);
+            v0[e] = (__bf16)acc_dv[j][e];
+            v1[e] = (__bf16)acc_dv[j][8 + e];
+          }
+          *reinterpret_cast<bf16x8*>(dk_out + o) = k0;
+          *reinterpret_cast<bf16x8*>(dk_out + o + 8) = k1;
+          *reinterpret_cast<bf16x8*>(dv_out + o) = v0;
+          *reinterpret_cast<bf16x8*>(dv_out + o + 8) = v1;
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
       const int f0 = 32 * j + 16 * g;
@@ -972,8 +997,9 @@ __global__ __launch_bounds__(256, 2) void read_bwd_dkdv_kernel(
 // sum the dK/dV partials, the rest the per-head dlog partials.
 //
 // dk / dv of a slot = the sum of its group's partials in ascending range order
-// (a fixed order; the work split above), dk scaled.  A workgroup takes whole
-// slot rows; pre: LDS for the group prefix.
+// (a fixed order; the work split above), dk scaled; groups with a single
+// segment were written by the dK/dV kernel.  A workgroup takes whole slot
+// rows; pre: LDS for the group prefix.
 __device__ __forceinline__ void read_bwd_reduce_kv(const float* __restrict__ dk_part,
                                                    const float* __restrict__ dv_part,
                                                    const int32_t* __restrict__ tile_count, bf16_t* __restrict__ dk,
@@ -988,6 +1014,7 @@ __device__ __forceinline__ void read_bwd_reduce_kv(const float* __restrict__ dk_
     const int sg = (int)(slot >> 7);
     const int lo = pre[sg], hi = pre[sg + 1];
     const int r0 = lo / per, n = hi > lo ? (hi - 1) / per - r0 + 1 : 0;
+    if (n == 1) continue;  // the dK/dV kernel wrote the group's rows
     const long base = ((long)(r0 + sg) * 128 + (slot & 127)) * D;
     for (int c4 = threadIdx.x; c4 < D / 4; c4 += blockDim.x) {
       f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1127,29 +1154,31 @@ hipError_t launch_read_tile_lists(const int32_t* top_idx, uint8_t* tile_flags, i
 template <int HD, bool AL, int TK>
 static void dkdv_inst(const void* q, const void* k, const void* v, const int32_t* ti, const float* tg,
                       const void* dout, const float* lse, const float* delta, const int32_t* list,
-                      const int32_t* count, float* dkp, float* dvp, const ReadDims& d, hipStream_t st) {
+                      const int32_t* count, float* dkp, float* dvp, void* dk, void* dv, const ReadDims& d,
+                      hipStream_t st) {
   const int Lq = read_lq(d.L);
   const int R = read_bwd_ranges(d);
   const float alpha = read_scale(HD) * kLog2e;
   NAYLIS_TIMED("read_bwd_dkdv", st,
                hipLaunchKernelGGL((read_bwd_dkdv_kernel<HD, AL, TK, true>), dim3(d.H * R), dim3(256), 0, st,
                                   (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ti, tg, (const bf16_t*)dout,
-                                  lse, delta, list, count, dkp, dvp, d.order, (long)d.B * d.S, d.H, d.L, Lq, d.E,
+                                  lse, delta, list, count, dkp, dvp, (bf16_t*)dk, (bf16_t*)dv, read_scale(HD),
+                                  d.order, (long)d.B * d.S, d.H, d.L, Lq, d.E,
                                   d.block_size, d.topk, alpha, R, read_bwd_n_ttiles(d)));
 }
 
 hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const void* dout, const float* lse, const float* delta,
-                                const int32_t* list, const int32_t* count, float* dk_part, float* dv_part,
-                                const ReadDims& d, hipStream_t st) {
+                                const int32_t* list, const int32_t* count, float* dk_part, float* dv_part, void* dk,
+                                void* dv, const ReadDims& d, hipStream_t st) {
   const bool al = d.block_size % 32 == 0;
 #define NAYLIS_DKDV2(HDV, TKV)                                                                                 \
   if (al)                                                                                                      \
-    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part, d, \
-                              st);                                                                             \
+    dkdv_inst<HDV, true, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part, dk, \
+                              dv, d, st);                                                                      \
   else                                                                                                         \
     dkdv_inst<HDV, false, TKV>(q, k, v, top_idx, top_gates, dout, lse, delta, list, count, dk_part, dv_part,   \
-                               d, st);
+                               dk, dv, d, st);
 #define NAYLIS_DKDV(HDV)        \
   if (d.topk <= 2) {            \
     NAYLIS_DKDV2(HDV, 2)        \
