@@ -10,9 +10,12 @@
 //  1. read_bwd_dq_kernel   — one workgroup per (b, h, 128-token tile), walks
 //     the tile's active slot groups: S^T, dP^T, dS^T, dQ^T += K^T dS^T; also
 //     writes the exact delta (sum_n P dP) and the per-head partial of
-//     dlog_gates (sum of dS over each selected block).
+//     dlog_gates (sum of dS over each selected block).  The staged variant
+//     (read_bwd_dq_fast_kernel, head_dim 64) also writes which blocks each
+//     64-token tile selects.
 //  2. read_tile_flags / read_tile_lists — which 64-token tiles select any
-//     block of each 128-slot group, as compact ascending lists.
+//     block of each 128-slot group, as compact ascending lists (the flags
+//     launch only when the dQ kernel did not write them).
 //  3. read_bwd_dkdv_kernel — one workgroup per (h, equal range of the
 //     (128-slot group, active tile) items), 4 waves of 32 slots; K/V rows of
 //     the current group's slots stay in registers;
