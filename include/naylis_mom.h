@@ -107,7 +107,7 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
  * NAYLIS_ERR_WORKSPACE.  All calls on one device share that array and its
  * contents: calls that overlap on one GPU (on other streams or threads) race,
  * and the caller must order them. */
-#define NAYLIS_READ_BWD_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+#define NAYLIS_READ_BWD_NOALLOC_MAX_BYTES ((size_t)128 << 20)
 int naylis_mom_read_bwd_noalloc(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
                                 const void* dout, void* dq, void* dk, void* dv, float* dgates, int64_t B, int64_t S,

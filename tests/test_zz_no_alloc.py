@@ -67,12 +67,15 @@ def test_read_bwd_noalloc_matches_workspace_entry_point(dev):
     lib = _lib.load()
     st = _lib.stream_of(dev)
     with _lib.on_device(dev):
-        # a config-2-like read (16 heads of 64, 8 blocks of 128 slots, top-2, grouped token order), then a
-        # smaller, ragged one (4 heads of 32, 4 blocks of 64 slots, 300 tokens, sequence order)
-        cases = [_case(dev, 4, 2048, 16, 64, 8, 128, 2, seed=1, grouped=True),
+        # the config-4 read (24 heads of 64, 32 blocks of 128 slots, 16384 tokens, top-2), then a
+        # config-2-like one (16 heads, 8 blocks, grouped token order), then a smaller, ragged one
+        # (4 heads of 32, 4 blocks of 64 slots, 300 tokens, sequence order): each call needs less
+        # scratch than the one before
+        cases = [_case(dev, 4, 4096, 24, 64, 32, 128, 2, seed=4, grouped=False),
+                 _case(dev, 4, 2048, 16, 64, 8, 128, 2, seed=1, grouped=True),
                  _case(dev, 1, 300, 4, 32, 4, 64, 2, seed=2, grouped=False)]
         needs = [lib.naylis_mom_read_workspace_bytes(*c["dims"]) for c in cases]
-        assert 0 < needs[1] < needs[0] <= _max_bytes(), needs
+        assert 0 < needs[2] < needs[1] < needs[0] <= _max_bytes(), needs
         got = []
         for c in cases:                               # the two no-allocation calls, in a row
             outs = _outputs(c)
@@ -93,7 +96,7 @@ def test_read_bwd_noalloc_rejects_reads_beyond_its_scratch(dev):
     """A read whose workspace exceeds the scratch array is refused with
     NAYLIS_ERR_WORKSPACE before anything runs; the next call still works."""
     lib = _lib.load()
-    dims = (1, 64, 16, 128, 128, 128, 2)              # 16384 slots of 16 x 128: 256 MiB of dK/dV partials
+    dims = (1, 64, 16, 128, 128, 128, 2)              # 16384 slots of 16 x 128: ~320 MiB of dK/dV partials
     assert lib.naylis_mom_read_workspace_bytes(*dims) > _max_bytes()
     with _lib.on_device(dev):
         rc = lib.naylis_mom_read_bwd_noalloc(*([1] * 13), *dims, _lib.stream_of(dev))
