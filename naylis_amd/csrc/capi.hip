@@ -683,6 +683,15 @@ static int wgrad_splits(int64_t N, int64_t D_in, int64_t D_out) {
   const int64_t want = (512 + tiles - 1) / tiles;
   int64_t s = 1;
   while (s < want && s < 64 && 2 * s * 1024 <= N) s *= 2;
+  // ... unless its last round of workgroups would be less than a quarter full:
+  // then the largest count that fits one round, if it still splits three ways
+  // (1536 x 1536 at 16384 tokens: 4 splits, 576 workgroups, 126 us; 3 splits,
+  // 432 workgroups, 110 us)
+  const int64_t slots = 512;
+  if (s > 1 && (tiles * s) % slots != 0 && (tiles * s) % slots < slots / 4) {
+    const int64_t one = slots / tiles;
+    if (one >= 3 && one < s && one * 1024 <= N) s = one;
+  }
   return (int)s;
 }
 
