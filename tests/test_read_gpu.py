@@ -205,3 +205,45 @@ def test_read_full_config2_vs_torch_fp32(dev):
     assert_close(kd.grad, kf.grad, "dk")
     assert_close(vd.grad, vf.grad, "dv")
     assert_close(gd.grad, gf.grad, "d_gates")
+
+
+def test_read_dkdv_work_split_edges(dev):
+    """The dK/dV pass cuts each head's (slot group, active tile) items into
+    equal ranges that cross group boundaries.  Two heads give many short
+    ranges; the routing leaves blocks 0-3 unselected (empty groups, zero
+    dK/dV), gives block 4 to one token (a group inside one range), and
+    spreads the rest unevenly (heavy groups over many ranges).  Against the
+    fp32 oracle, and bitwise the same on a second run."""
+    from naylis_amd import mom_kernels
+    B, S, H, HD, NB, BS, topk = 2, 1536, 2, 64, 32, 128, 2
+    g = torch.Generator().manual_seed(77)
+    L, D = NB * BS, H * HD
+    q = (torch.randn(B, S, H, HD, generator=g) * 0.7).bfloat16()
+    k = (torch.randn(L, D, generator=g) * 0.4).bfloat16()
+    v = (torch.randn(L, D, generator=g) * 0.4).bfloat16()
+    gates = F.softmax(torch.randn(B, S, topk, generator=g), -1)
+    w = torch.linspace(1.0, 8.0, NB - 5)                     # blocks 5..31, uneven popularity
+    first = 5 + torch.multinomial(w, B * S * topk, replacement=True, generator=g).view(B, S, topk)
+    top = first.clone()
+    top[..., 1] = torch.where(top[..., 1] == top[..., 0], 5 + (top[..., 0] - 5 + 1) % (NB - 5), top[..., 1])
+    top[1, 700, 1] = 4                                       # block 4: one token
+    dout = torch.randn(B, S, H, HD, generator=g).bfloat16()
+    res = []
+    for _ in range(2):
+        qd, kd, vd, gd = (t.to(dev).requires_grad_(True) for t in (q, k, v, gates))
+        out = mom_kernels.mom_read(qd, kd, vd, top.to(dev), gd, num_blocks=NB, block_size=BS, mode="hip")
+        out.backward(dout.to(dev))
+        res.append([t.detach().clone() for t in (out, qd.grad, kd.grad, vd.grad, gd.grad)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    out, dq, dk, dv, dg = res[0]
+    assert float(dk[:4 * BS].float().abs().max()) == 0.0 and float(dv[:4 * BS].float().abs().max()) == 0.0
+    assert float(dv[4 * BS:5 * BS].float().abs().max()) > 0.0
+    qf, kf, vf, gf = (t.to(dev).float().requires_grad_(True) for t in (q, k, v, gates))
+    ref = oracle.mom_read(qf, kf, vf, top.to(dev), gf, num_blocks=NB, block_size=BS)
+    ref.backward(dout.to(dev).float())
+    assert_close(out, ref, "out")
+    assert_close(dq, qf.grad, "dq")
+    assert_close(dk, kf.grad, "dk")
+    assert_close(dv, vf.grad, "dv")
+    assert_close(dg, gf.grad, "d_gates")
