@@ -70,3 +70,37 @@ def test_rezero_scale_matches_torch(n, xdt, ydt, dev):
                                            torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert torch.equal(y, (x.float() * s).to(ydt))
+
+
+@pytest.mark.parametrize("N,D,s0", [(8 * 2048, 1024, 0.37), (300 * 8, 256, 0.0)])
+def test_gated_linear_matches_fp64(N, D, s0, dev):
+    """mom_gated_linear: y = s (o W^T) in fp32 as one GEMM on the scaled bf16
+    weight W' = bf16(s W) (model.py:251 then 239), and its backward (d o, dW,
+    ds) against fp64 torch on the same bf16 inputs.  The fold rounds W' where
+    the reference rounds o W^T, so y's error is bounded by the weight
+    rounding, 2^-9 |s| sum_j |o_j| |W_ij| per element (checked with a factor 2
+    of margin), not by a fraction of |y|; d o = bf16(dy) W' adds the same
+    rounding of dy and one bf16 rounding of the result.  s = 0 (the ReZero
+    initial value) makes y and d o vanish while ds does not."""
+    from naylis_amd import mom_kernels
+    g = torch.Generator().manual_seed(N + D)
+    o = torch.randn(N, D, generator=g).bfloat16().to(dev).requires_grad_(True)
+    w = (torch.randn(D, D, generator=g) * D ** -0.5).bfloat16().to(dev).requires_grad_(True)
+    s = torch.tensor([s0], device=dev, requires_grad=True)
+    dy = torch.randn(N, D, generator=g).to(dev)
+    y = mom_kernels.mom_gated_linear(o, w, s)
+    assert y.dtype == torch.float32
+    y.backward(dy)
+    od, wd, dyd = o.detach().double(), w.detach().double(), dy.double()
+    z = od @ wd.t()
+    y_bound = 2.0 ** -8 * abs(s0) * (od.abs() @ wd.abs().t()) + 1e-6
+    assert bool(((y.double() - s0 * z).abs() <= y_bound).all()), "y beyond the weight-rounding bound"
+    do_ref = s0 * (dyd @ wd)
+    do_bound = 2.0 ** -7 * abs(s0) * (dyd.abs() @ wd.abs()) + 2.0 ** -8 * do_ref.abs() + 1e-6
+    assert bool(((o.grad.double() - do_ref).abs() <= do_bound).all()), "d o beyond its rounding bound"
+    ref_dw = s0 * (dyd.t() @ od)
+    assert_close(w.grad, ref_dw, "dW", atol=2e-3 * max(1.0, float(ref_dw.abs().max())))
+    # ds = sum bf16(dy) . z: its error is the rounding of dy against z, at most 2^-9 sum |dy z|
+    # (checked with a factor 2), plus fp32 accumulation
+    ref_ds = float((dyd * z).sum())
+    assert abs(float(s.grad) - ref_ds) <= 2.0 ** -8 * float((dyd * z).abs().sum()) + 1e-6
