@@ -719,6 +719,13 @@ __global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restr
   float s = 0.f;
   if (i < n) {
     int c = gq;
+    for (; c + 60 < n_parts; c += 64) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = part[(long)(c + 4 * u) * n + i];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += v[u];
+    }
     for (; c + 28 < n_parts; c += 32) {
       float v[8];
 #pragma unroll

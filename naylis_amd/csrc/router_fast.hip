@@ -156,10 +156,39 @@ __global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restri
   }
 }
 
+// For threads tid < R: the fp64 sum of cs[c * R + tid] over the chunks
+// c_lo <= c < c_hi, added in chunk order.  The chunk sums are staged through
+// LDS (stage: 4096 doubles) 4096 / R chunks at a time, one coalesced load
+// round per block, so the serial part is LDS reads and fp64 adds.  Called by
+// the whole 256-thread workgroup (c_lo, c_hi uniform).
+__device__ __forceinline__ double chunk_carry(const double* __restrict__ cs, int c_lo, int c_hi, int R,
+                                              double* stage, int tid) {
+  double run = 0.0;
+  const int per = 4096 / R;
+  for (int cb = c_lo; cb < c_hi; cb += per) {
+    const int nc = min(per, c_hi - cb), n = nc * R;
+    const double* src = cs + (long)cb * R;
+    double v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = tid + 256 * u < n ? src[tid + 256 * u] : 0.0;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (tid + 256 * u < n) stage[tid + 256 * u] = v[u];
+    __syncthreads();
+    if (tid < R)
+      for (int j = 0; j < nc; ++j) run += stage[j * R + tid];
+    __syncthreads();
+  }
+  return run;
+}
+
 // ---------------------------------------------------------------------------
 // (F2) per (b, 32-token chunk): fp64 carry of the earlier chunks' sums, the
 // in-chunk prefix, z = Z / (t+1), tanh, logits = a W_up^T, softmax probs,
 // top-k (ties -> lowest id) and gates; the tail matches router_fwd_kernel.
+// The prefix is one serial fp64 chain per rank (carry + y_0 + ... + y_t, in
+// token order); everything else runs over (token, rank) pairs or over 8
+// lanes per token (lane p of token t owns experts p, p + 8, ...).
 template <int EMAX, int TK>
 __global__ __launch_bounds__(256) void router_head_kernel(
     const float* __restrict__ y, const double* __restrict__ ycs, const float* __restrict__ w_up,
@@ -169,113 +198,148 @@ __global__ __launch_bounds__(256) void router_head_kernel(
     int topk, int n_ch) {
   constexpr int CT = kFastChunk;
   constexpr int LP = EMAX + 1;
+  constexpr int EPL = EMAX / 8;  // experts per lane
+  constexpr int NONE = 0x7fffffff;
   __shared__ float y_lds[CT * 65];
   __shared__ float a_lds[CT * 65];
+  __shared__ double zs_lds[4096];  // carry staging, then the in-chunk prefix
   __shared__ float wu_lds[EMAX * 65];
   __shared__ float lg_lds[CT * LP];
+  __shared__ float ex_lds[CT * LP];
+  __shared__ float sum_lds[CT];
+  __shared__ double carry_lds[64];
   const int c = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x;
   const int t0 = c * CT, nt = min(CT, T - t0);
-  __shared__ double carry_lds[64];
   for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
   for (int i = tid; i < nt * R; i += 256) y_lds[(i / R) * 65 + i % R] = y[((long)b * T + t0) * R + i];
+  // carry = sum of the earlier chunks' fp64 sums, in chunk order
+  const double carry = chunk_carry(ycs + (long)b * n_ch * R, 0, c, R, zs_lds, tid);
+  if (tid < R) carry_lds[tid] = carry;
+  __syncthreads();
+  // Z_t = carry + y_0 + ... + y_t in token order (fp64), one chain per rank
   if (tid < R) {
-    // carry = sum of the earlier chunks' fp64 sums, in chunk order (loads in
-    // flight 16 at a time)
-    const double* cs = ycs + (long)b * n_ch * R + tid;
-    double run = 0.0;
-    for (int c0 = 0; c0 < c; c0 += 16) {
-      double v[16];
+    double run = carry_lds[tid];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = c0 + i < c ? cs[(long)(c0 + i) * R] : 0.0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) run += v[i];
-    }
-    carry_lds[tid] = run;
+    for (int t = 0; t < CT; ++t)
+      if (t < nt) {
+        run += (double)y_lds[t * 65 + tid];
+        zs_lds[t * 65 + tid] = run;
+      }
   }
   __syncthreads();
-  // (token, rank) pairs in parallel: Z_t = carry + y_0 + ... + y_t in token
-  // order (fp64), z = fp32(Z_t * fp64(1 / (t+1))), a = tanh(z)
+  // z = fp32(Z_t * fp64(1 / (t+1))), a = tanh(z), (token, rank) pairs in parallel
   for (int i = tid; i < nt * R; i += 256) {
     const int t = i / R, r = i % R;
-    double run = carry_lds[r];
-    for (int s2 = 0; s2 <= t; ++s2) run += (double)y_lds[s2 * 65 + r];
-    const float z = (float)(run * (1.0 / (double)(t0 + t + 1)));
+    const float z = (float)(zs_lds[t * 65 + r] * (1.0 / (double)(t0 + t + 1)));
     const float a = tanhf(z);
     a_lds[t * 65 + r] = a;
     act[((long)b * T + t0) * R + i] = a;
   }
   __syncthreads();
+  const int tk = tid >> 3, part = tid & 7;
+  const int tc = min(tk, nt - 1);
+  const bool live = tk < nt;  // the 8 lanes of a token are all live or all idle
+  const long tok = (long)b * T + t0 + tc;
   {
-    const int t = tid >> 3, part = tid & 7;
-    if (t < nt) {
-      const long tok = (long)b * T + t0 + t;
 #pragma unroll
-      for (int e0 = 0; e0 < EMAX; e0 += 8) {
-        const int e = e0 + part;
-        if (e < E) {
-          float lg = 0.f;
-          for (int r = 0; r < R; ++r) lg = fmaf(a_lds[t * 65 + r], wu_lds[e * 65 + r], lg);
-          lg_lds[t * LP + e] = lg;
+    for (int k = 0; k < EPL; ++k) {
+      const int e = part + 8 * k;
+      if (e < E) {
+        float lg = 0.f;
+        for (int r = 0; r < R; ++r) lg = fmaf(a_lds[tc * 65 + r], wu_lds[e * 65 + r], lg);
+        if (live) {
+          lg_lds[tc * LP + e] = lg;
           logits[tok * E + e] = lg;
         }
       }
     }
   }
   __syncthreads();
-  if (tid < nt) {
-    const long tok = (long)b * T + t0 + tid;
-    float lg[EMAX];
+  float lg[EPL], nz[EPL];
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e) lg[e] = e < E ? lg_lds[tid * LP + e] : 0.f;
-    float mx = -INFINITY;
+  for (int k = 0; k < EPL; ++k) {
+    const int e = part + 8 * k;
+    lg[k] = e < E ? lg_lds[tc * LP + e] : 0.f;
+    nz[k] = e < E ? (noise ? noisy_logit(lg[k], noise[tok * E + e], noise_scale, noise_kind) : lg[k]) : -INFINITY;
+  }
+  // softmax: the max over the token's lanes (exact in any order), the sum in
+  // expert order by lane 0
+  float mx = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      if (e < E) mx = fmaxf(mx, lg[e]);
+  for (int k = 0; k < EPL; ++k)
+    if (part + 8 * k < E) mx = fmaxf(mx, lg[k]);
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 8));
+  float ex[EPL];
+#pragma unroll
+  for (int k = 0; k < EPL; ++k) {
+    const int e = part + 8 * k;
+    ex[k] = e < E ? expf(lg[k] - mx) : 0.f;
+    if (live && e < E) ex_lds[tc * LP + e] = ex[k];
+  }
+  __syncthreads();
+  if (live && part == 0) {
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
-      if (e < E) sum += expf(lg[e] - mx);
+      if (e < E) sum += ex_lds[tc * LP + e];
+    sum_lds[tc] = sum;
+  }
+  __syncthreads();
+  if (live) {
+    const float sum = sum_lds[tc];
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      if (e < E) probs[tok * E + e] = expf(lg[e] - mx) / sum;
-    float nz[EMAX];
+    for (int k = 0; k < EPL; ++k)
+      if (part + 8 * k < E) probs[tok * E + part + 8 * k] = ex[k] / sum;
+  }
+  // top-k: per round each lane's best untaken expert (value, then lowest id),
+  // combined over the token's 8 lanes and taken from lane 0 so that every
+  // lane records the same choice
+  int sel[TK];
+  float val[TK];
+  unsigned taken = 0;  // bit k: expert part + 8k of this lane
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      nz[e] = (e < E) ? (noise ? noisy_logit(lg[e], noise[tok * E + e], noise_scale, noise_kind) : lg[e]) : -INFINITY;
-    int sel[TK];
-    float val[TK];
+  for (int s = 0; s < TK; ++s) {
+    sel[s] = 0;
+    val[s] = 0.f;
+    if (s < topk) {
+      int best = NONE;
+      float bv = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < TK; ++t) {
-      sel[t] = 0;
-      val[t] = 0.f;
-      if (t < topk) {
-        int best = -1;
-        float bv = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-          bool taken = false;
-#pragma unroll
-          for (int u = 0; u < TK; ++u)
-            if (u < t && sel[u] == e) taken = true;
-          if (e < E && !taken && (best < 0 || nz[e] > bv)) {
-            best = e;
-            bv = nz[e];
-          }
+      for (int k = 0; k < EPL; ++k) {
+        const int e = part + 8 * k;
+        if (e < E && !((taken >> k) & 1u) && (best == NONE || nz[k] > bv)) {
+          best = e;
+          bv = nz[k];
         }
-        sel[t] = best;
-        val[t] = bv;
       }
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) {
+        const int ob = __shfl_xor(best, m, 8);
+        const float ov = __shfl_xor(bv, m, 8);
+        if (ob != NONE && (best == NONE || ov > bv || (ov == bv && ob < best))) {
+          best = ob;
+          bv = ov;
+        }
+      }
+      best = __shfl(best, 0, 8);
+      bv = __shfl(bv, 0, 8);
+      if (best != NONE && (best & 7) == part) taken |= 1u << (best >> 3);
+      sel[s] = best == NONE ? -1 : best;
+      val[s] = bv;
     }
+  }
+  if (live && part == 0) {
     float gs = 0.f;
 #pragma unroll
-    for (int t = 0; t < TK; ++t)
-      if (t < topk) gs += expf(val[t] - val[0]);
+    for (int s = 0; s < TK; ++s)
+      if (s < topk) gs += expf(val[s] - val[0]);
 #pragma unroll
-    for (int t = 0; t < TK; ++t)
-      if (t < topk) {
-        top_idx[tok * topk + t] = sel[t];
-        top_gates[tok * topk + t] = expf(val[t] - val[0]) / gs;
+    for (int s = 0; s < TK; ++s)
+      if (s < topk) {
+        top_idx[tok * topk + s] = sel[s];
+        top_gates[tok * topk + s] = expf(val[s] - val[0]) / gs;
       }
   }
 }
@@ -547,36 +611,30 @@ __global__ __launch_bounds__(256) void router_bwd_token_fast_kernel(
 
 // (B2) W~_t = sum_{s >= t} w_s within the sequence: per (b, 32-token chunk),
 // the fp64 carry of the later chunks' sums (chunk order) plus the in-chunk
-// suffix (token order, descending), for every (token, rank) pair in parallel.
+// suffix (token order, descending), one serial chain per rank.
 __global__ __launch_bounds__(256) void router_wtilde_kernel(const float* __restrict__ w,
                                                             const double* __restrict__ wcs,
                                                             float* __restrict__ wt, int T, int R, int n_ch) {
   constexpr int CT = kFastChunk;
   __shared__ float w_lds[CT * 65];
-  __shared__ double carry_lds[64];
+  __shared__ double stage[4096];
   const int c = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x;
   const int t0 = c * CT, nt = min(CT, T - t0);
   const long tok0 = (long)b * T + t0;
   for (int i = tid; i < nt * R; i += 256) w_lds[(i / R) * 65 + i % R] = w[tok0 * R + i];
-  if (tid < R) {
-    const double* cs = wcs + (long)b * n_ch * R + tid;
-    double run = 0.0;
-    for (int c0 = c + 1; c0 < n_ch; c0 += 16) {
-      double v[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = c0 + i < n_ch ? cs[(long)(c0 + i) * R] : 0.0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) run += v[i];
-    }
-    carry_lds[tid] = run;
-  }
+  const double carry = chunk_carry(wcs + (long)b * n_ch * R, c + 1, n_ch, R, stage, tid);
   __syncthreads();
-  for (int i = tid; i < nt * R; i += 256) {
-    const int t = i / R, r = i % R;
-    double run = carry_lds[r];
-    for (int s2 = nt - 1; s2 >= t; --s2) run += (double)w_lds[s2 * 65 + r];
-    wt[tok0 * R + i] = (float)run;
+  // W~_t = carry + w_{nt-1} + ... + w_t (token order descending), one fp64
+  // chain per rank
+  if (tid < R) {
+    double run = carry;
+#pragma unroll
+    for (int t = CT - 1; t >= 0; --t)
+      if (t < nt) {
+        run += (double)w_lds[t * 65 + tid];
+        wt[(tok0 + t) * R + tid] = (float)run;
+      }
   }
 }
 
