@@ -401,14 +401,38 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
   constexpr int WV = ST * RW / 256;  // fp32 values of W~ per thread (4 or 8)
   float wreg[WV];
   uint4 xreg[2];
+  // dx_in rows of this lane's token and 16 features, one step ahead (zeros
+  // when there is no dx_in: bf16 0 adds +0.0f)
+  uint4 dcur[2], dnext[2];
+  auto fetch_dx_in = [&](uint4 (&dr)[2], long ts) {
+    const long tok = ts + l32;
+    if (dx_in != nullptr && tok < ntok) {
+      const long o = tok * D + f0 + 16 * g;
+      dr[0] = *reinterpret_cast<const uint4*>(dx_in + o);
+      dr[1] = *reinterpret_cast<const uint4*>(dx_in + o + 8);
+    } else {
+      dr[0] = dr[1] = make_uint4(0, 0, 0, 0);
+    }
+  };
   auto fetch = [&](long ts) {
     {
       const int t = tid / (RW / WV), r0 = (tid % (RW / WV)) * WV;
       const long tk = ts + t;
+      if ((R & 3) == 0 && r0 + WV <= R && tk < ntok) {
 #pragma unroll
-      for (int e = 0; e < WV; ++e) {
-        const int r = r0 + e;
-        wreg[e] = (tk < ntok && r < R) ? wt[tk * R + r] : 0.f;
+        for (int e = 0; e < WV; e += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(wt + tk * R + r0 + e);
+          wreg[e] = v[0];
+          wreg[e + 1] = v[1];
+          wreg[e + 2] = v[2];
+          wreg[e + 3] = v[3];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < WV; ++e) {
+          const int r = r0 + e;
+          wreg[e] = (tk < ntok && r < R) ? wt[tk * R + r] : 0.f;
+        }
       }
     }
 #pragma unroll
@@ -437,12 +461,16 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
 
   const int n_steps = (int)min((long)(kFastDxRange / ST), (ntok - tok_beg + ST - 1) / ST);
   fetch(tok_beg);
+  fetch_dx_in(dcur, tok_beg);
   stash(0);
   __syncthreads();
   for (int st = 0; st < n_steps; ++st) {
     const int buf = st & 1;
     const long ts = tok_beg + (long)st * ST;
-    if (st + 1 < n_steps) fetch(ts + ST);
+    if (st + 1 < n_steps) {
+      fetch(ts + ST);
+      fetch_dx_in(dnext, ts + ST);
+    }
     // ---- dx^T = W_down^T W~^T for this wave's 32 features x 32 tokens
     {
       f32x16 acc = f32x16{};
@@ -459,18 +487,14 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
       if (tok < ntok) {
         const long o = tok * D + f0 + 16 * g;  // this lane half's 16 consecutive features
         float add[16];
-        if (dx_in != nullptr) {
-          const uint4 a0 = *reinterpret_cast<const uint4*>(dx_in + o);
-          const uint4 a1 = *reinterpret_cast<const uint4*>(dx_in + o + 8);
-          const uint32_t w8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        {
+          const uint32_t w8[8] = {dcur[0].x, dcur[0].y, dcur[0].z, dcur[0].w,
+                                  dcur[1].x, dcur[1].y, dcur[1].z, dcur[1].w};
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             add[2 * e] = __uint_as_float(w8[e] << 16);
             add[2 * e + 1] = __uint_as_float(w8[e] & 0xffff0000u);
           }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) add[e] = 0.f;
         }
         bf16x8 lo, hi;
 #pragma unroll
@@ -494,7 +518,11 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
         accw[rt] = mfma32(ax, bh, accw[rt]);
       }
     }
-    if (st + 1 < n_steps) stash(buf ^ 1);  // last read before the previous barrier
+    if (st + 1 < n_steps) {
+      stash(buf ^ 1);  // last read before the previous barrier
+      dcur[0] = dnext[0];
+      dcur[1] = dnext[1];
+    }
     __syncthreads();
   }
   // dW_down partial of this range: accw[rt] row = feature f0 + acc_row(g, v), column = rank
@@ -661,8 +689,9 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
   auto go = [&](auto ksw) {
     constexpr int KSW = decltype(ksw)::value;
     // chunks per workgroup: two when the W_down planes leave room in registers
-    // and the grid still has a workgroup per CU
-    constexpr int NCW = KSW * RT <= 8 ? 2 : 1;
+    // (up to 12 K-steps: 226 VGPRs, one 8-wave workgroup per CU) and the grid
+    // still has a workgroup per CU, so the grid runs in one round
+    constexpr int NCW = KSW * RT <= 12 ? 2 : 1;
     const int nc = (NCW > 1 && (long)((n_ch + 1) / 2) * d.B >= 256) ? 2 : 1;
     if (nc == 2)
       NAYLIS_TIMED("router_proj", st,
@@ -679,8 +708,14 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
     go(std::integral_constant<int, 4>{});
   else if (nks <= 8)
     go(std::integral_constant<int, 8>{});
-  else
+  else if constexpr (RT == 1) {
+    if (nks <= 12)
+      go(std::integral_constant<int, 12>{});
+    else
+      go(std::integral_constant<int, 16>{});
+  } else {
     go(std::integral_constant<int, 16 / RT>{});  // router_fast_fwd_ok bounds nks by 16 / RT
+  }
   NAYLIS_TIMED("router_head", st,
                hipLaunchKernelGGL((router_head_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, y, ycs, w_up,
                                   noise, ns, d.noise_kind, logits, probs, idx, gates, act, d.T, d.R, d.E, d.topk,

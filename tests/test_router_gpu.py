@@ -53,7 +53,8 @@ CASES = [
     (2, 300, 1024, 32, 8, 2, torch.bfloat16), # ragged T
     (8, 2048, 1024, 32, 8, 2, torch.bfloat16),# config 2
     (1, 256, 96, 16, 8, 3, torch.bfloat16),   # top-3, D not a multiple of 256
-    (2, 512, 256, 32, 32, 8, torch.bfloat16), # config-4 head: 32 blocks, top-8
+    (4, 4096, 1536, 32, 32, 2, torch.bfloat16),  # config 4: 12 K-steps per wave, two chunks per workgroup
+    (2, 512, 256, 32, 32, 8, torch.bfloat16), # 32 blocks, top-8
     (1, 300, 128, 16, 64, 5, torch.bfloat16), # 64 blocks, top-5, ragged T
 ]
 
