@@ -46,7 +46,10 @@ int launch_router_fast_scan(const float* act, const float* probs, const int32_t*
 size_t router_stats_ws_bytes(long N, int E);
 hipError_t launch_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* ws, long N, int E,
                                int topk, hipStream_t st);
-void launch_router_fast_dx(const void* x, const float* wt, const float* w_down, const void* dx_in, void* dx,
-                           float* dwd_part, const RouterDims& d, hipStream_t st);
+// true when the dx kernel forms W~ from w and its chunk sums itself (R <= 32,
+// T a multiple of its 256-token range): launch_router_fast_scan then skips B2
+bool router_fast_dx_fuses_scan(const RouterDims& d);
+void launch_router_fast_dx(const void* x, const float* wt, const float* w, const double* wcs, const float* w_down,
+                           const void* dx_in, void* dx, float* dwd_part, const RouterDims& d, hipStream_t st);
 
 }  // namespace naylis

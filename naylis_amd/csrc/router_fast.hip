@@ -156,6 +156,21 @@ __global__ __launch_bounds__(512) void router_proj_kernel(const bf16_t* __restri
   }
 }
 
+// run + p[0] + p[stride] + ... + p[(n-1) stride], added in that order (fp64);
+// the LDS reads are issued 8 at a time so the chain waits on the adds only.
+__device__ __forceinline__ double add_in_order(double run, const double* p, int stride, int n) {
+  int k = 0;
+  for (; k + 8 <= n; k += 8) {
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) run += v[u];
+  }
+  for (; k < n; ++k) run += p[k * stride];
+  return run;
+}
+
 // For threads tid < R: the fp64 sum of cs[c * R + tid] over the chunks
 // c_lo <= c < c_hi, added in chunk order.  The chunk sums are staged through
 // LDS (stage: 4096 doubles) 4096 / R chunks at a time, one coalesced load
@@ -175,8 +190,7 @@ __device__ __forceinline__ double chunk_carry(const double* __restrict__ cs, int
     for (int u = 0; u < 16; ++u)
       if (tid + 256 * u < n) stage[tid + 256 * u] = v[u];
     __syncthreads();
-    if (tid < R)
-      for (int j = 0; j < nc; ++j) run += stage[j * R + tid];
+    if (tid < R) run = add_in_order(run, stage + tid, R, nc);
     __syncthreads();
   }
   return run;
@@ -356,13 +370,21 @@ __global__ __launch_bounds__(256) void router_head_kernel(
 //     with transposing LDS reads from the natural-layout tiles.
 // The range's dW_down partial goes to dwd_part[range][r][f] (summed over
 // ranges in a fixed order by router_reduce_kernel).
-template <int RT>
+//
+// FUSED (R <= 32, T a multiple of the range): W~ is not read from wt but
+// formed here from w and its chunk sums wcs, the range being 8 whole chunks
+// of one sequence.  Thread (chunk j, rank r) adds the chunk sums after its
+// chunk in chunk order (staged through LDS) and then runs the chunk's suffix
+// in place over the range's w rows in LDS: the same fp64 operations in the
+// same order as router_wtilde_kernel, so W~ is bitwise the same.
+template <int RT, bool FUSED>
 __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __restrict__ x,
                                                              const float* __restrict__ wt,
                                                              const float* __restrict__ w_down,
                                                              const bf16_t* __restrict__ dx_in,
                                                              bf16_t* __restrict__ dx, float* __restrict__ dwd_part,
-                                                             int D, int R, long ntok) {
+                                                             int D, int R, long ntok, const float* __restrict__ w,
+                                                             const double* __restrict__ wcs, int T, int n_ch) {
   constexpr int ST = 32;                 // tokens per step
   constexpr int RW = RT * 32;            // staged ranks (zero padded)
   constexpr int WP = RW + 8;             // W~ plane pitch (bf16)
@@ -371,11 +393,15 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
   __shared__ __attribute__((aligned(16))) bf16_t wt_hi[2][ST * WP];
   __shared__ __attribute__((aligned(16))) bf16_t wt_lo[2][ST * WP];
   __shared__ __attribute__((aligned(16))) bf16_t x_lds[2][ST * XP];
+  // FUSED: chunk-sum staging (4096 doubles), then the range's W~ rows
+  // (kFastDxRange x 32 fp32, row pitch 32)
+  __shared__ __attribute__((aligned(16))) double wt_s[FUSED ? 4096 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const long tok_beg = (long)blockIdx.x * kFastDxRange;
   const int slab = blockIdx.y * kFastDxSlab;
   const int f0 = slab + wave * 32;
+  float* const wts = reinterpret_cast<float*>(wt_s);
 
   // A operand of dx^T: W_down[r = 16 ks + 8 g + e][f0 + row_perm32(l32)], hi/lo
   bf16x8 wa_hi[KR], wa_lo[KR];
@@ -415,7 +441,7 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
     }
   };
   auto fetch = [&](long ts) {
-    {
+    if constexpr (!FUSED) {  // FUSED: stash reads W~ from wts
       const int t = tid / (RW / WV), r0 = (tid % (RW / WV)) * WV;
       const long tk = ts + t;
       if ((R & 3) == 0 && r0 + WV <= R && tk < ntok) {
@@ -442,9 +468,13 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
       xreg[u] = tk < ntok ? *reinterpret_cast<const uint4*>(x + tk * D + slab + 8 * c8) : make_uint4(0, 0, 0, 0);
     }
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](int buf, long ts) {
     {
       const int t = tid / (RW / WV), r0 = (tid % (RW / WV)) * WV;
+      if constexpr (FUSED) {
+#pragma unroll
+        for (int e = 0; e < WV; ++e) wreg[e] = r0 + e < R ? wts[(ts - tok_beg + t) * 32 + r0 + e] : 0.f;
+      }
 #pragma unroll
       for (int e = 0; e < WV; ++e) {
         const __bf16 h = (__bf16)wreg[e];
@@ -462,7 +492,53 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
   const int n_steps = (int)min((long)(kFastDxRange / ST), (ntok - tok_beg + ST - 1) / ST);
   fetch(tok_beg);
   fetch_dx_in(dcur, tok_beg);
-  stash(0);
+  if constexpr (FUSED) {
+    constexpr int CPR = kFastDxRange / kFastChunk;  // chunks per range (8)
+    const int b = (int)(tok_beg / T), cf = (int)(tok_beg % T) / kFastChunk;
+    const int j = tid >> 5, r = tid & 31;
+    const double* cs = wcs + (long)b * n_ch * R;
+    // the range's w rows (in flight during the carry below; wt_s holds the
+    // staged chunk sums until then)
+    float wv[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int i = tid + 256 * u;
+      wv[u] = i < kFastDxRange * R ? w[tok_beg * R + i] : 0.f;
+    }
+    // carry of chunk cf + j: chunk sums c = cf + j + 1 .. n_ch - 1 in order
+    double run = 0.0;
+    for (int cb = cf + 1; cb < n_ch; cb += 4096 / R) {
+      const int nc = min(4096 / R, n_ch - cb), n = nc * R;
+      double v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = tid + 256 * u < n ? cs[(long)cb * R + tid + 256 * u] : 0.0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (tid + 256 * u < n) wt_s[tid + 256 * u] = v[u];
+      __syncthreads();
+      const int k0 = max(0, cf + j + 1 - cb);
+      if (r < R) run = add_in_order(run, wt_s + k0 * R + r, R, nc - k0);
+      __syncthreads();
+    }
+    // the w rows to LDS, then the in-chunk suffix in place
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int i = tid + 256 * u;
+      if (i < kFastDxRange * R) wts[R == 32 ? i : (i / R) * 32 + i % R] = wv[u];
+    }
+    __syncthreads();
+    if (r < R) {
+#pragma unroll
+      for (int t = kFastChunk - 1; t >= 0; --t) {
+        float* e = &wts[(j * kFastChunk + t) * 32 + r];
+        run += (double)*e;
+        *e = (float)run;
+      }
+    }
+    static_assert(CPR * 32 == 256, "one thread per (chunk, rank)");
+    __syncthreads();
+  }
+  stash(0, tok_beg);
   __syncthreads();
   for (int st = 0; st < n_steps; ++st) {
     const int buf = st & 1;
@@ -519,7 +595,7 @@ __global__ __launch_bounds__(256) void router_dx_fast_kernel(const bf16_t* __res
       }
     }
     if (st + 1 < n_steps) {
-      stash(buf ^ 1);  // last read before the previous barrier
+      stash(buf ^ 1, ts + ST);  // last read before the previous barrier
       dcur[0] = dnext[0];
       dcur[1] = dnext[1];
     }
@@ -745,18 +821,45 @@ void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_u
     fast_fwd_rt<2>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, d, st);
 }
 
-void launch_router_fast_dx(const void* x, const float* wt, const float* w_down, const void* dx_in, void* dx,
-                           float* dwd_part, const RouterDims& d, hipStream_t st) {
+// The fused prologue (two memory rounds and the carry chains) is paid once
+// per workgroup round: fuse only while the grid fits two workgroups per CU
+// (LDS: 59 KB per workgroup), where it replaces a whole launch.
+static int device_cus() {
+  static int cached[64] = {};  // per device; a racing first call stores the same value
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
+bool router_fast_dx_fuses_scan(const RouterDims& d) {
+  const long ranges = ((long)d.B * d.T + kFastDxRange - 1) / kFastDxRange;
+  return d.R <= 32 && d.T % kFastDxRange == 0 && ranges * (d.D / kFastDxSlab) <= 2L * device_cus();
+}
+
+void launch_router_fast_dx(const void* x, const float* wt, const float* w, const double* wcs, const float* w_down,
+                           const void* dx_in, void* dx, float* dwd_part, const RouterDims& d, hipStream_t st) {
   const long ntok = (long)d.B * d.T;
+  const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
   const dim3 grid((unsigned)((ntok + kFastDxRange - 1) / kFastDxRange), d.D / kFastDxSlab);
-  if (d.R <= 32)
+  if (router_fast_dx_fuses_scan(d))
     NAYLIS_TIMED("router_bwd_dx", st,
-                 hipLaunchKernelGGL((router_dx_fast_kernel<1>), grid, dim3(256), 0, st, (const bf16_t*)x, wt, w_down,
-                                    (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok));
+                 hipLaunchKernelGGL((router_dx_fast_kernel<1, true>), grid, dim3(256), 0, st, (const bf16_t*)x, wt,
+                                    w_down, (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok, w, wcs, d.T,
+                                    n_ch));
+  else if (d.R <= 32)
+    NAYLIS_TIMED("router_bwd_dx", st,
+                 hipLaunchKernelGGL((router_dx_fast_kernel<1, false>), grid, dim3(256), 0, st, (const bf16_t*)x, wt,
+                                    w_down, (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok, w, wcs, d.T,
+                                    n_ch));
   else
     NAYLIS_TIMED("router_bwd_dx", st,
-                 hipLaunchKernelGGL((router_dx_fast_kernel<2>), grid, dim3(256), 0, st, (const bf16_t*)x, wt, w_down,
-                                    (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok));
+                 hipLaunchKernelGGL((router_dx_fast_kernel<2, false>), grid, dim3(256), 0, st, (const bf16_t*)x, wt,
+                                    w_down, (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok, w, wcs, d.T,
+                                    n_ch));
 }
 
 }  // namespace naylis
@@ -786,9 +889,10 @@ int launch_router_fast_scan(const float* act, const float* probs, const int32_t*
   else
     fast_token<64, 8>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
   const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
-  NAYLIS_TIMED("router_bwd_scan", st,
-               hipLaunchKernelGGL(router_wtilde_kernel, dim3(n_ch, d.B), dim3(256), 0, st, w, wcs, wt, d.T, d.R,
-                                  n_ch));
+  if (!router_fast_dx_fuses_scan(d))  // else the dx kernel forms W~ itself
+    NAYLIS_TIMED("router_bwd_scan", st,
+                 hipLaunchKernelGGL(router_wtilde_kernel, dim3(n_ch, d.B), dim3(256), 0, st, w, wcs, wt, d.T, d.R,
+                                    n_ch));
   return d.B * n_ch;  // dW_up partials written
 }
 

@@ -135,7 +135,11 @@ def test_router_noise_hook_and_config4_bias(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(2, 64, 32, 8, 4, 2), (2, 384, 1024, 32, 8, 2), (1, 200, 96, 16, 8, 3)])
+@pytest.mark.parametrize("shape", [(2, 64, 32, 8, 4, 2), (2, 384, 1024, 32, 8, 2), (1, 200, 96, 16, 8, 3),
+                                   # T a multiple of 256 (bf16: the dx kernel forms W~ itself), R < 32
+                                   (2, 512, 256, 16, 8, 2),
+                                   # chunk sums staged in two blocks (143 later chunks > 4096 / R)
+                                   (1, 4608, 128, 32, 8, 2)])
 def test_router_backward(shape, dtype, dev):
     from naylis_amd import mom_kernels
     B, T, D, R, E, k = shape
