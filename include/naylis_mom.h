@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 13
+#define NAYLIS_MOM_ABI_VERSION 14
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -345,6 +345,22 @@ int naylis_mom_rezero_bwd(const void* dy, int dy_dtype, const void* z, int z_dty
  * s then follow from dW' (the gradient of W') by naylis_mom_rezero_bwd over
  * the weight's elements: dW_o = s * dW', ds = sum(dW' * W_o). */
 int naylis_mom_rezero_scale(const void* x, int x_dtype, const float* s, void* y, int y_dtype, int64_t n, void* stream);
+/* The two steps above in one call for the layer's backward (the o projection's
+ * weight gradient, model.py:251, with the gate of model.py:239 folded in):
+ *   dW'[o][i] = sum_t dy[t][o] * x[t][i]   (fp32, as naylis_mom_linear_wgrad)
+ *   dw = bf16(s * dW')                     (the gradient of W_o)
+ *   ds = sum(dW' * w)                      (the gradient of s; w = W_o)
+ * x (N, D_in), dy (N, D_out), w and dw (D_out, D_in), all bf16; s and ds one
+ * fp32 value each on the device.  dW' never leaves the split-K reduction: its
+ * epilogue scales it and forms ds's partials, summed in a fixed order, so
+ * the results are deterministic.  dw equals bf16(s * dW') of the two-step
+ * path's dW' only where both reduce the same K splits; the K range is always
+ * split at least in two here.  Workspace: naylis_mom_gated_wgrad_workspace_bytes.
+ * Constraints as naylis_mom_linear_wgrad, and w, dw, workspace 16-byte aligned. */
+size_t naylis_mom_gated_wgrad_workspace_bytes(int64_t N, int64_t D_in, int64_t D_out);
+int naylis_mom_gated_wgrad(const void* x, const void* dy, const void* w, const float* s, void* dw, float* ds,
+                           void* workspace, size_t workspace_bytes, int64_t N, int64_t D_in, int64_t D_out,
+                           void* stream);
 
 /* --------------------------------------------------------- decode step ---
  * One new token per sequence: the O(1) running-sum form of the prefix-mean

@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -64,6 +64,8 @@ SIGNATURES = {
     "naylis_mom_rezero_bwd": (_int, [_c_void_p, _int, _c_void_p, _int] + [_c_void_p] * 4 + [_size_t, _i64, _c_void_p]),
     "naylis_mom_rezero_scale": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _int, _i64, _c_void_p]),
     "naylis_mom_linear_wgrad": (_int, [_c_void_p] * 3 + [_int, _c_void_p, _size_t] + [_i64] * 3 + [_c_void_p]),
+    "naylis_mom_gated_wgrad_workspace_bytes": (_size_t, [_i64] * 3),
+    "naylis_mom_gated_wgrad": (_int, [_c_void_p] * 7 + [_size_t] + [_i64] * 3 + [_c_void_p]),
     "naylis_mom_bank_kv_bwd": (_int, [_c_void_p] * 6 + [_int, _c_void_p, _c_void_p, _int] + [_i64] * 3
                                + [_c_void_p]),
     "naylis_mom_bank_kv_fwd_grouped": (_int, [_c_void_p] + [_pp] * 4 + [_i64] * 4 + [_c_void_p]),

@@ -20,6 +20,8 @@
 #include "launch.h"
 #include "launch_router.h"
 #include "launch_bank.h"
+#include <algorithm>
+
 #include "launch_gemm.h"
 #include "launch_rezero.h"
 
@@ -741,6 +743,63 @@ int naylis_mom_linear_wgrad(const void* x, const void* dy, void* dw, int dw_dtyp
   if (!gemm_supported(g))
     return fail(NAYLIS_ERR_ARG, "linear_wgrad: needs 16-byte aligned pointers and N * max(D_in, D_out) < 2^30");
   return hip_status(launch_gemm(g, "linear_wgrad", (hipStream_t)stream), "linear_wgrad");
+}
+
+// The gated weight gradient: at least two K splits, so the gate epilogue of
+// the split-K reduction always runs.
+static int gated_wgrad_splits(int64_t N, int64_t D_in, int64_t D_out) {
+  return std::max(2, wgrad_splits(N, D_in, D_out));
+}
+
+static size_t gated_wgrad_part_off(int64_t N, int64_t D_in, int64_t D_out) {
+  return (gemm_ws_bytes(1, (int)D_out, (int)D_in, gated_wgrad_splits(N, D_in, D_out)) + 255) & ~(size_t)255;
+}
+
+size_t naylis_mom_gated_wgrad_workspace_bytes(int64_t N, int64_t D_in, int64_t D_out) {
+  if (check_wgrad_dims(N, D_in, D_out) != NAYLIS_OK) return 0;
+  return gated_wgrad_part_off(N, D_in, D_out) + (size_t)std::max(1, gemm_gate_parts((int)D_out, (int)D_in)) * 4;
+}
+
+int naylis_mom_gated_wgrad(const void* x, const void* dy, const void* w, const float* s, void* dw, float* ds,
+                           void* workspace, size_t workspace_bytes, int64_t N, int64_t D_in, int64_t D_out,
+                           void* stream) {
+  int rc = check_wgrad_dims(N, D_in, D_out);
+  if (rc) return rc;
+  if (!dw || !ds || !w || !s || (N > 0 && (!x || !dy)))
+    return fail(NAYLIS_ERR_ARG, "gated_wgrad: null pointer argument");
+  const size_t need = naylis_mom_gated_wgrad_workspace_bytes(N, D_in, D_out);
+  if (!workspace || workspace_bytes < need)
+    return fail(NAYLIS_ERR_WORKSPACE, "gated_wgrad: workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  if ((((uintptr_t)w | (uintptr_t)dw | (uintptr_t)workspace) & 15) != 0)
+    return fail(NAYLIS_ERR_ARG, "gated_wgrad: w, dw and the workspace must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (N == 0) {  // no tokens: both gradients are zero
+    hipError_t e = launch_zero(dw, (size_t)D_out * D_in * 2, st);
+    if (e == hipSuccess) e = launch_zero(ds, sizeof(float), st);
+    return hip_status(e, "gated_wgrad");
+  }
+  GemmLaunch g{};
+  g.njobs = 1;
+  g.M = (int)D_out;
+  g.N = (int)D_in;
+  g.K = g.K1 = (int)N;
+  g.out = kGemmOutBF16;
+  g.splits = gated_wgrad_splits(N, D_in, D_out);
+  g.ws = workspace;
+  g.job[0].a = GemmOp{dy, nullptr, D_out, false};  // A(o, t) = dy[t][o]
+  g.job[0].b = GemmOp{x, nullptr, D_in, false};    // B(t, i) = x[t][i]
+  g.job[0].c = dw;
+  g.job[0].ldc = D_in;
+  float* part = (float*)((char*)workspace + gated_wgrad_part_off(N, D_in, D_out));
+  g.gate_w = w;
+  g.gate_s = s;
+  g.gate_part = part;
+  if (!gemm_supported(g))
+    return fail(NAYLIS_ERR_ARG, "gated_wgrad: needs 16-byte aligned pointers and N * max(D_in, D_out) < 2^30");
+  hipError_t e = launch_gemm(g, "linear_wgrad", st);
+  if (e == hipSuccess) e = launch_rezero_reduce(part, gemm_gate_parts((int)D_out, (int)D_in), ds, st);
+  return hip_status(e, "gated_wgrad");
 }
 
 // -------------------------------------------------------------------- ReZero

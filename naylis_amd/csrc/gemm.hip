@@ -392,6 +392,49 @@ bool gemm_supported(const GemmLaunch& g) {
   return true;
 }
 
+// Split-K reduction with the gate epilogue (GemmLaunch::gate_w): the
+// ascending sum of the partials is dW'; C = bf16(s dW') and one partial of
+// sum dW' * W per workgroup (4 elements per thread, added in a fixed tree).
+__global__ __launch_bounds__(256) void gemm_reduce_gate_kernel(const float* __restrict__ ws, long mn, int splits,
+                                                               const bf16_t* __restrict__ w,
+                                                               const float* __restrict__ s, bf16_t* __restrict__ c,
+                                                               float* __restrict__ part) {
+  __shared__ float red[256];
+  const int tid = threadIdx.x;
+  const long i = ((long)blockIdx.x * 256 + tid) * 4;
+  float acc = 0.f;
+  if (i < mn) {
+    const float* p = ws + i;
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    for (int sp = 1; sp < splits; ++sp) {
+      const f32x4 u = *reinterpret_cast<const f32x4*>(p + sp * mn);
+      v[0] += u[0];
+      v[1] += u[1];
+      v[2] += u[2];
+      v[3] += u[3];
+    }
+    const float sc = *s;
+    const uint2 wb = *reinterpret_cast<const uint2*>(w + i);
+    const float wf[4] = {__uint_as_float(wb.x << 16), __uint_as_float(wb.x & 0xffff0000u),
+                         __uint_as_float(wb.y << 16), __uint_as_float(wb.y & 0xffff0000u)};
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16(sc * v[0]) | ((uint32_t)f32_to_bf16(sc * v[1]) << 16);
+    o.y = (uint32_t)f32_to_bf16(sc * v[2]) | ((uint32_t)f32_to_bf16(sc * v[3]) << 16);
+    *reinterpret_cast<uint2*>(c + i) = o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = fmaf(v[e], wf[e], acc);
+  }
+  red[tid] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) red[tid] += red[tid + o];
+    __syncthreads();
+  }
+  if (tid == 0) part[blockIdx.x] = red[0];
+}
+
+int gemm_gate_parts(int M, int N) { return (int)(((long)M * N / 4 + 255) / 256); }
+
 size_t gemm_ws_bytes(int njobs, int M, int N, int splits) {
   return splits > 1 ? (size_t)njobs * splits * M * N * sizeof(float) : 0;
 }
@@ -407,7 +450,12 @@ static void gemm_dispatch(const DevJobs& dj, const GemmLaunch& g, int kper, int 
                  hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 2>), grid, dim3(C::NT), 0, st, dj, g.M, g.N, g.K1, kper,
                                     tiles_m, tiles_n, splits, g.njobs, g.K, ws));
     const dim3 rg((unsigned)(((long)g.M * g.N / 4 + 255) / 256), g.njobs);
-    if (g.out == kGemmOutF32)
+    if (g.gate_w != nullptr)
+      NAYLIS_TIMED("gemm_reduce", st,
+                   hipLaunchKernelGGL(gemm_reduce_gate_kernel, dim3(gemm_gate_parts(g.M, g.N)), dim3(256), 0, st, ws,
+                                      (long)g.M * g.N, splits, (const bf16_t*)g.gate_w, g.gate_s,
+                                      (bf16_t*)g.job[0].c, g.gate_part));
+    else if (g.out == kGemmOutF32)
       NAYLIS_TIMED("gemm_reduce", st,
                    hipLaunchKernelGGL((gemm_reduce_kernel<0>), rg, dim3(256), 0, st, dj, ws, g.M, g.N, splits));
     else

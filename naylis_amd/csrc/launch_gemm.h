@@ -35,7 +35,14 @@ struct GemmLaunch {
   GemmOut out;
   int splits;
   void* ws;
+  // Gate epilogue (one job, splits > 1, C contiguous bf16): the partials sum
+  // to dW', C = bf16(gate_s * dW') and gate_part[wg] = sum of dW' * gate_w
+  // over the reduction workgroup's elements (gemm_gate_parts of them).
+  const void* gate_w = nullptr;
+  const float* gate_s = nullptr;
+  float* gate_part = nullptr;
 };
+int gemm_gate_parts(int M, int N);
 
 // true when the fast kernel supports the shapes and layouts (M, N, K, leading
 // dimensions multiples of 8, 16-byte aligned pointers, K1 a multiple of 64)

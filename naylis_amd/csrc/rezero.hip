@@ -200,6 +200,12 @@ static void bwd_launch(const void* dy, const void* z, const float* s, void* dz, 
                                   (const DT*)dy, (const ZT*)z, s, (ZT*)dz, part, n, vec));
 }
 
+hipError_t launch_rezero_reduce(const float* part, int nparts, float* ds, hipStream_t st) {
+  NAYLIS_TIMED("rezero_bwd", st,
+               hipLaunchKernelGGL(rezero_reduce_kernel, dim3(1), dim3(kRzThreads), 0, st, part, nparts, ds));
+  return hipGetLastError();
+}
+
 hipError_t launch_rezero_bwd(const void* dy, bool dy_bf16, const void* z, bool z_bf16, const float* s, void* dz,
                              float* ds, void* ws, long n, hipStream_t st) {
   float* part = (float*)ws;

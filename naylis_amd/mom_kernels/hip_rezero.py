@@ -40,6 +40,20 @@ def gated_linear_backward(lib, dy2, out2, w_o, w_os, s, st):
     dev = out2.device
     dy2 = dy2.to(torch.bfloat16).contiguous()
     dout2 = torch.mm(dy2, w_os)
+    N, D_in = out2.shape
+    D_out = dy2.shape[1]
+    if (out2.dtype == torch.bfloat16 and w_o.dtype == torch.bfloat16 and w_o.is_contiguous() and out2.is_contiguous()
+            and N % 8 == 0 and D_in % 8 == 0 and D_out % 8 == 0):
+        # dW' = dy^T out stays inside the split-K reduction, whose epilogue
+        # writes dW_o = s dW' and the partials of ds = sum(dW' W_o)
+        ws = torch.empty(max(int(lib.naylis_mom_gated_wgrad_workspace_bytes(N, D_in, D_out)), 1), device=dev,
+                         dtype=torch.uint8)
+        dw_o = torch.empty_like(w_o)
+        ds = torch.empty(1, device=dev, dtype=torch.float32)
+        _lib.check(lib.naylis_mom_gated_wgrad(out2.data_ptr(), dy2.data_ptr(), w_o.data_ptr(), s.data_ptr(),
+                                              dw_o.data_ptr(), ds.data_ptr(), ws.data_ptr(), ws.numel(), N, D_in,
+                                              D_out, st))
+        return dout2, dw_o, ds
     dw_s = library_wgrad(lib, out2, dy2, torch.float32, dev, st)
     dw_o = torch.empty_like(w_o)
     ds = torch.empty(1, device=dev, dtype=torch.float32)

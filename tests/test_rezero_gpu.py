@@ -104,3 +104,49 @@ def test_gated_linear_matches_fp64(N, D, s0, dev):
     # (checked with a factor 2), plus fp32 accumulation
     ref_ds = float((dyd * z).sum())
     assert abs(float(s.grad) - ref_ds) <= 2.0 ** -8 * float((dyd * z).abs().sum()) + 1e-6
+
+
+@pytest.mark.parametrize("N,D_in,D_out", [(8 * 2048, 1024, 1024), (2400, 256, 512), (0, 64, 64)])
+def test_gated_wgrad_matches_two_steps(N, D_in, D_out, dev):
+    """naylis_mom_gated_wgrad (dW' kept inside the split-K reduction, whose
+    epilogue writes dw = bf16(s dW') and the partials of ds = sum(dW' w))
+    against naylis_mom_linear_wgrad's fp32 dW' followed by naylis_mom_rezero_bwd
+    over the weight.  dw is bitwise equal where both split K alike (config-2
+    shape: 8 splits), else within one bf16 rounding; ds differs only in its
+    fp32 summation order.  N = 0 gives zeros over poisoned outputs."""
+    from naylis_amd import _lib
+    from naylis_amd.mom_kernels.hip_linear import library_wgrad
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(N + D_in)
+    x = torch.randn(N, D_in, generator=g).bfloat16().to(dev)
+    dy = torch.randn(N, D_out, generator=g).bfloat16().to(dev)
+    w = (torch.randn(D_out, D_in, generator=g) * 0.05).bfloat16().to(dev)
+    s = torch.tensor([0.37], device=dev)
+    nb = int(lib.naylis_mom_gated_wgrad_workspace_bytes(N, D_in, D_out))
+    assert nb > 0
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    dw = torch.full((D_out, D_in), 7.0, device=dev, dtype=torch.bfloat16)
+    ds = torch.full((1,), 7.0, device=dev)
+    _lib.check(lib.naylis_mom_gated_wgrad(x.data_ptr() if N else None, dy.data_ptr() if N else None, w.data_ptr(),
+                                          s.data_ptr(), dw.data_ptr(), ds.data_ptr(), ws.data_ptr(), nb, N, D_in,
+                                          D_out, st))
+    torch.cuda.synchronize()
+    if N == 0:
+        assert not dw.any() and float(ds) == 0.0
+        return
+    dwp = library_wgrad(lib, x, dy, torch.float32, dev, st)
+    dw_ref = torch.empty_like(w)
+    ds_ref = torch.empty(1, device=dev)
+    rz = torch.empty(max(int(lib.naylis_mom_rezero_workspace_bytes(w.numel())), 1), dtype=torch.uint8, device=dev)
+    _lib.check(lib.naylis_mom_rezero_bwd(dwp.data_ptr(), 0, w.data_ptr(), 1, s.data_ptr(), dw_ref.data_ptr(),
+                                         ds_ref.data_ptr(), rz.data_ptr(), rz.numel(), w.numel(), st))
+    torch.cuda.synchronize()
+    if N == 8 * 2048:
+        assert torch.equal(dw, dw_ref), f"{int((dw != dw_ref).sum())} elements differ"
+    else:
+        d = (dw.float() - dw_ref.float()).abs()
+        # one bf16 rounding, plus the fp32 summation-order difference of dW' near zero
+        assert bool((d <= 2.0 ** -7 * dw_ref.float().abs() + 1e-3).all()), f"max {float(d.max())}"
+    mag = float((dwp.double() * w.double()).abs().sum())
+    assert abs(float(ds) - float(ds_ref)) <= 1e-5 * mag + 1e-6
