@@ -1021,7 +1021,22 @@ __device__ __forceinline__ void read_bwd_reduce_kv(const float* __restrict__ dk_
     const long base = ((long)(r0 + sg) * 128 + (slot & 127)) * D;
     for (int c4 = threadIdx.x; c4 < D / 4; c4 += blockDim.x) {
       f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int i = 0; i < n; ++i) {
+      // partials in order, their loads issued four at a time
+      int i = 0;
+      for (; i + 4 <= n; i += 4) {
+        f32x4 pk[4], pv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          pk[u] = *reinterpret_cast<const f32x4*>(dk_part + base + (i + u) * stride + 4 * c4);
+          pv[u] = *reinterpret_cast<const f32x4*>(dv_part + base + (i + u) * stride + 4 * c4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          sk += pk[u];
+          sv += pv[u];
+        }
+      }
+      for (; i < n; ++i) {
         sk += *reinterpret_cast<const f32x4*>(dk_part + base + i * stride + 4 * c4);
         sv += *reinterpret_cast<const f32x4*>(dv_part + base + i * stride + 4 * c4);
       }
@@ -1044,7 +1059,15 @@ __device__ __forceinline__ void read_bwd_reduce_gates(const float* __restrict__ 
                                                       float* __restrict__ dgates, long n, int H, long blk, long nblk) {
   for (long i = blk * (long)blockDim.x + threadIdx.x; i < n; i += nblk * blockDim.x) {
     float s = 0.f;
-    for (int h = 0; h < H; ++h) s += dlg_part[(long)h * n + i];
+    int h = 0;
+    for (; h + 8 <= H; h += 8) {  // head partials in order, loads issued eight at a time
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = dlg_part[(long)(h + u) * n + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; h < H; ++h) s += dlg_part[(long)h * n + i];
     const float gt = top_gates[i];
     dgates[i] = gt >= 1e-9f ? s / gt : 0.f;
   }
