@@ -152,7 +152,15 @@ __global__ __launch_bounds__(kRzThreads) void rezero_reduce_kernel(const float* 
                                                                    float* __restrict__ ds) {
   __shared__ float red[kRzThreads];
   float acc = 0.f;
-  for (int i = threadIdx.x; i < nparts; i += kRzThreads) acc += part[i];
+  int i = threadIdx.x;
+  for (; i + 3 * kRzThreads < nparts; i += 4 * kRzThreads) {  // loads four at a time, adds in order
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = part[i + u * kRzThreads];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += v[u];
+  }
+  for (; i < nparts; i += kRzThreads) acc += part[i];
   red[threadIdx.x] = acc;
   __syncthreads();
   for (int w = kRzThreads / 2; w > 0; w >>= 1) {
