@@ -508,7 +508,8 @@ hipError_t launch_gemm(const GemmLaunch& g, const char* name, hipStream_t st) {
   const long wide = wgs(CfgWide::BM, CfgWide::BN);
   if (wide >= cus && wide % cus == 0)
     gemm_layouts<CfgWide>(dj, gl, kper, splits, name, st);
-  else if (wgs(CfgSmall::BM, CfgSmall::BN) >= cus)
+  else if (wgs(CfgSmall::BM, CfgSmall::BN) >= cus &&
+           !(g.whole_rounds && wgs(CfgSmall::BM, CfgSmall::BN) % cus != 0 && wgs(CfgMid::BM, CfgMid::BN) % cus == 0))
     gemm_layouts<CfgSmall>(dj, gl, kper, splits, name, st);
   else if (wgs(CfgMid::BM, CfgMid::BN) >= cus)
     gemm_layouts<CfgMid>(dj, gl, kper, splits, name, st);

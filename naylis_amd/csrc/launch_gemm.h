@@ -41,6 +41,9 @@ struct GemmLaunch {
   const void* gate_w = nullptr;
   const float* gate_s = nullptr;
   float* gate_part = nullptr;
+  // Take the 64 x 128 tile over 128 x 128 when that turns a grid of uneven
+  // rounds (not a multiple of the CU count) into whole rounds.
+  bool whole_rounds = false;
 };
 int gemm_gate_parts(int M, int N);
 
