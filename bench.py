@@ -164,7 +164,7 @@ def executed_tiles(idx, E, tile=128):
     order = read_order(idx.to(torch.int32).contiguous(), E)
     flat = idx.reshape(N, K).long()
     if int(order[0]) == 1:
-        flat = flat[order[1:].long()]
+        flat = flat[order[1:1 + N].long()]
     n_tiles = (N + tile - 1) // tile
     oh = torch.zeros(n_tiles * tile, E, dtype=torch.bool, device=idx.device)
     oh[:N].scatter_(1, flat, True)

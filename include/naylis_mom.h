@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 14
+#define NAYLIS_MOM_ABI_VERSION 15
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -63,18 +63,32 @@ const char* naylis_mom_last_error(void);
  *                                          log(max(g, 1e-9)) on each selected
  *                                          block (duplicate ids add up)
  *   out      (B, S, H, head_dim) bf16
+ *   side     naylis_mom_read_side_bytes() bytes, or NULL: what the
+ *                                          pair-tiled forward leaves for the
+ *                                          pair-tiled backward (o's bf16
+ *                                          remainder o - bf16(o), so delta =
+ *                                          rowsum(o * dO) has fp32 accuracy,
+ *                                          and each row's share of its weight
+ *                                          on the pair's first block).  Used
+ *                                          when side_bytes > 0 and a
+ *                                          token_order is given; with NULL the
+ *                                          backward takes the two-pass
+ *                                          kernels.  Ignored otherwise.
  *   lse      (H, B, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
- *   token_order (1 + B*S) int32 or NULL  the order in which the read walks
+ *   token_order  int32 or NULL             the order in which the read walks
  *                                          the flattened tokens b*S + s, as
- *                                          written by naylis_mom_read_order:
- *                                          word 0 = 1 when words 1.. hold a
- *                                          grouped order, 0 for sequence
- *                                          order; NULL is sequence order.
- *                                          Results do not depend on it beyond
- *                                          fp32 rounding of the dK/dV sums;
- *                                          the backward must get the
- *                                          forward's order.
+ *                                          written by naylis_mom_read_order
+ *                                          into naylis_mom_read_order_words()
+ *                                          words: word 0 = 1 when words
+ *                                          1..B*S hold a grouped order, 0 for
+ *                                          sequence order, then (top-2 over
+ *                                          at most 32 blocks) the pair plan of
+ *                                          the pair-tiled kernels; NULL is
+ *                                          sequence order.  Results do not
+ *                                          depend on it beyond fp32 rounding
+ *                                          of the dK/dV sums; the backward
+ *                                          must get the forward's order.
  * Constraints: head_dim a power of two in [16, 128]; 1 <= k <= min(8, E);
  * E <= 1024; L <= 16384.  The forward needs no workspace (pass NULL, 0); the
  * backward needs naylis_mom_read_workspace_bytes() bytes.
@@ -82,18 +96,27 @@ const char* naylis_mom_last_error(void);
 size_t naylis_mom_read_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks,
                                        int64_t block_size, int64_t top_k);
 
+/* Bytes of the side buffer when, given a token_order from
+ * naylis_mom_read_order and that buffer, the read takes the pair-tiled path
+ * both ways (head_dim 64, block size 128, top-2, num_blocks <= 8,
+ * 1 <= B*S <= 2^18; the forward alone also for num_blocks <= 32); 0
+ * otherwise (no side buffer needed). */
+size_t naylis_mom_read_side_bytes(int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks,
+                                  int64_t block_size, int64_t top_k);
+
 int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                        const float* top_gates, const int32_t* token_order, void* out, float* lse, void* workspace,
-                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        const float* top_gates, const int32_t* token_order, void* out, void* side, float* lse,
+                        void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
                         int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
 
 /* Backward of the read: dq (B,S,H,head_dim) bf16; dk, dv (L, D) bf16 reduced
  * over all N tokens (deterministic, fixed-order); dgates (B,S,k) fp32 =
- * d loss / d top_gates.  `out` and `lse` are the forward's outputs. */
+ * d loss / d top_gates.  `out`, `side` and `lse` are the forward's
+ * outputs (side may be NULL, see above). */
 int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                        const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
-                        const void* dout, void* dq, void* dk, void* dv, float* dgates, void* workspace,
-                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        const float* top_gates, const int32_t* token_order, const void* out, const void* side,
+                        const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dgates,
+                        void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
                         int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
 
 /* The read backward with no workspace argument: no counterpart in the
@@ -101,28 +124,35 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
  * graph capture, tight training or serving loops, harnesses that forbid
  * hipMalloc); it allocates nothing.  Same arguments (less the workspace),
  * results (bitwise) and errors as naylis_mom_read_bwd.  Its workspace is a
- * scratch array of NAYLIS_READ_BWD_NOALLOC_MAX_BYTES that the library holds
- * on each device it runs on until the process ends; a read whose
- * naylis_mom_read_workspace_bytes() exceeds that returns
- * NAYLIS_ERR_WORKSPACE.  All calls on one device share that array and its
- * contents: calls that overlap on one GPU (on other streams or threads) race,
- * and the caller must order them. */
+ * scratch array of NAYLIS_READ_BWD_NOALLOC_MAX_BYTES (128 MiB) in the
+ * library's code object: every device the library is loaded on reserves it
+ * from the load until the process ends, whether or not this entry point is
+ * ever called.  A read whose naylis_mom_read_workspace_bytes() exceeds it
+ * returns NAYLIS_ERR_WORKSPACE.  `stream` must belong to the current device
+ * (the array's address is looked up there); otherwise NAYLIS_ERR_ARG.  All
+ * calls on one device share that array and its contents: calls that overlap
+ * on one GPU (on other streams or threads) race, and the caller must order
+ * them. */
 #define NAYLIS_READ_BWD_NOALLOC_MAX_BYTES ((size_t)128 << 20)
 int naylis_mom_read_bwd_noalloc(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                                const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
-                                const void* dout, void* dq, void* dk, void* dv, float* dgates, int64_t B, int64_t S,
-                                int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
-                                void* stream);
+                                const float* top_gates, const int32_t* token_order, const void* out,
+                                const void* side, const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                                float* dgates, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                                int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream);
 
 /* Token order for the read (no counterpart in the reference, which walks
  * tokens in sequence order with BLOCK_M = 128, triton_gpu.py:50,98): the
  * bank's K/V are shared by the whole batch, so tokens may be read in any
- * order.  order (1 + B*S) int32: for top-2 routing over at most 32 blocks,
- * words 1.. receive the flattened tokens grouped by their block pair (stable
- * within a pair) and word 0 = 1, when that lowers the number of (128-token
- * tile, block) pairs by at least 10 %; otherwise word 0 = 0 (sequence order;
- * also for every other routing and for more than 2^18 tokens).  A function
- * of top_idx only.  Workspace: naylis_mom_read_order_workspace_bytes(). */
+ * order.  order: naylis_mom_read_order_words() int32 (1 + B*S, plus the pair
+ * plan when there is one).  For top-2 routing over at most 32 blocks and at
+ * most 2^18 tokens, words 1..B*S receive the flattened tokens grouped by
+ * their block pair (stable within a pair), and the words after them the pair
+ * plan (the pair-tiled kernels' 32-token tiles and work items); word 0 = 1
+ * when the grouping lowers the number of (128-token tile, block) pairs by at
+ * least 10 % (the two-pass kernels then follow it), else 0.  Every other
+ * routing: word 0 = 0 (sequence order) and nothing else.  A function of
+ * top_idx only.  Workspace: naylis_mom_read_order_workspace_bytes(). */
+int64_t naylis_mom_read_order_words(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k);
 size_t naylis_mom_read_order_workspace_bytes(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k);
 int naylis_mom_read_order(const int32_t* top_idx, int32_t* order, void* workspace, size_t workspace_bytes, int64_t B,
                           int64_t S, int64_t num_blocks, int64_t top_k, void* stream);

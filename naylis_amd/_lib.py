@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1
@@ -33,9 +33,11 @@ SIGNATURES = {
     "naylis_mom_abi_version": (_int, []),
     "naylis_mom_last_error": (ctypes.c_char_p, []),
     "naylis_mom_read_workspace_bytes": (_size_t, [_i64] * 7),
-    "naylis_mom_read_fwd": (_int, [_c_void_p] * 8 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
-    "naylis_mom_read_bwd": (_int, [_c_void_p] * 13 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
-    "naylis_mom_read_bwd_noalloc": (_int, [_c_void_p] * 13 + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_read_side_bytes": (_size_t, [_i64] * 7),
+    "naylis_mom_read_fwd": (_int, [_c_void_p] * 9 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_read_bwd": (_int, [_c_void_p] * 14 + [_c_void_p, _size_t] + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_read_bwd_noalloc": (_int, [_c_void_p] * 14 + [_i64] * 7 + [_c_void_p]),
+    "naylis_mom_read_order_words": (_i64, [_i64] * 4),
     "naylis_mom_read_order_workspace_bytes": (_size_t, [_i64] * 4),
     "naylis_mom_read_order": (_int, [_c_void_p, _c_void_p, _c_void_p, _size_t] + [_i64] * 4 + [_c_void_p]),
     "naylis_mom_router_workspace_bytes": (_size_t, [_i64] * 6),

@@ -114,6 +114,31 @@ ReadWs plan_read_ws(const ReadDims& d) {
   return w;
 }
 
+// The pair-tiled backward's workspace: per-head gate-gradient partials and
+// the dK / dV partials of its (range, pair) segments.
+struct PairWs {
+  size_t dlg, dk_part, dv_part, total;
+};
+
+PairWs plan_pair_ws(const ReadDims& d) {
+  PairWs w{};
+  const size_t ntok = (size_t)d.B * d.S;
+  const size_t part = align256(read_pair_part_bytes(d));
+  size_t off = 0;
+  w.dlg = off;
+  off += align256(ntok * d.H * 2 * 4);
+  w.dk_part = off;
+  off += part;
+  w.dv_part = off;
+  off += part;
+  w.total = off;
+  return w;
+}
+
+// Shapes for which a call with a token order and a side buffer takes the pair-tiled
+// backward.
+bool pair_bwd_shapes(const ReadDims& d) { return read_pair_bwd_shapes(d, (long)d.B * d.S); }
+
 int check_router_dims(int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, RouterDims* d) {
   if (B < 0 || T < 0 || D <= 0)
     return fail(NAYLIS_ERR_ARG, "mom_route: bad shape B=%lld T=%lld D=%lld", (long long)B, (long long)T,
@@ -156,13 +181,21 @@ size_t naylis_mom_read_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t 
                                        int64_t block_size, int64_t top_k) {
   ReadDims d;
   if (check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d) != NAYLIS_OK) return 0;
-  return plan_read_ws(d).total;
+  const size_t two_pass = plan_read_ws(d).total;
+  return pair_bwd_shapes(d) ? std::max(two_pass, plan_pair_ws(d).total) : two_pass;
+}
+
+size_t naylis_mom_read_side_bytes(int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks,
+                                  int64_t block_size, int64_t top_k) {
+  ReadDims d;
+  if (check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d) != NAYLIS_OK) return 0;
+  return pair_bwd_shapes(d) ? read_pair_side_bytes(d) : 0;
 }
 
 int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32_t* top_idx, const float* top_gates,
-                        const int32_t* token_order, void* out, float* lse, void* workspace, size_t workspace_bytes,
-                        int64_t B, int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                        int64_t top_k, void* stream) {
+                        const int32_t* token_order, void* out, void* side, float* lse, void* workspace,
+                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
   ReadDims d;
@@ -172,14 +205,20 @@ int naylis_mom_read_fwd(const void* q, const void* k, const void* v, const int32
   if (B * S == 0) return NAYLIS_OK;
   if (!q || !k || !v || !top_idx || !top_gates || !out || !lse)
     return fail(NAYLIS_ERR_ARG, "mom_read_fwd: null pointer argument");
-  return hip_status(launch_read_fwd(q, k, v, top_idx, top_gates, out, lse, d, (hipStream_t)stream), "mom_read_fwd");
+  hipStream_t st = (hipStream_t)stream;
+  if (read_pair_fwd_ok(d, (long)B * S))
+    return hip_status(launch_read_fwd_pair(q, k, v, top_idx, top_gates, out, read_pair_bwd_ok(d, (long)B * S) ? side
+                                                                                                : nullptr,
+                                           lse, d, st),
+                      "mom_read_fwd");
+  return hip_status(launch_read_fwd(q, k, v, top_idx, top_gates, out, lse, d, st), "mom_read_fwd");
 }
 
 int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32_t* top_idx, const float* top_gates,
-                        const int32_t* token_order, const void* out, const float* lse, const void* dout, void* dq,
-                        void* dk, void* dv, float* dgates, void* workspace, size_t workspace_bytes, int64_t B,
-                        int64_t S, int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                        int64_t top_k, void* stream) {
+                        const int32_t* token_order, const void* out, const void* side, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, float* dgates, void* workspace,
+                        size_t workspace_bytes, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream) {
   ReadDims d;
   int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
   if (rc) return rc;
@@ -187,11 +226,22 @@ int naylis_mom_read_bwd(const void* q, const void* k, const void* v, const int32
   if (!k || !v || !dk || !dv || !workspace) return fail(NAYLIS_ERR_ARG, "mom_read_bwd: null pointer argument");
   if (B * S > 0 && (!q || !top_idx || !top_gates || !out || !lse || !dout || !dq || !dgates))
     return fail(NAYLIS_ERR_ARG, "mom_read_bwd: null pointer argument");
+  hipStream_t st = (hipStream_t)stream;
+  if (side != nullptr && read_pair_bwd_ok(d, (long)B * S)) {
+    const PairWs pw = plan_pair_ws(d);
+    if (workspace_bytes < pw.total)
+      return fail(NAYLIS_ERR_WORKSPACE, "mom_read_bwd: workspace of %zu bytes is smaller than the %zu required",
+                  workspace_bytes, pw.total);
+    char* ws = (char*)workspace;
+    return hip_status(launch_read_bwd_pair(q, k, v, top_idx, top_gates, out, side, dout, lse, dq, dk, dv, dgates,
+                                           (float*)(ws + pw.dlg), (float*)(ws + pw.dk_part),
+                                           (float*)(ws + pw.dv_part), d, st),
+                      "mom_read_bwd");
+  }
   const ReadWs w = plan_read_ws(d);
   if (workspace_bytes < w.total)
     return fail(NAYLIS_ERR_WORKSPACE, "mom_read_bwd: workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, w.total);
-  hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   float* delta = (float*)(ws + w.delta);
   float* dlg = (float*)(ws + w.dlg);
@@ -232,11 +282,21 @@ constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
 std::atomic<void*> g_scratch_addr[kScratchDevices];
 
-// The scratch array's address on the current device.
-int scratch_address(void** out) {
+// The scratch array's address on the device the stream belongs to, which must
+// be the current device: hipGetSymbolAddress answers for the current device,
+// and the kernels run on the stream's.
+int scratch_address(hipStream_t stream, void** out) {
   int dev = -1;
   int rc = hip_status(hipGetDevice(&dev), "mom_read_bwd_noalloc: hipGetDevice");
   if (rc) return rc;
+  hipDevice_t sdev = -1;
+  rc = hip_status(hipStreamGetDevice(stream, &sdev), "mom_read_bwd_noalloc: hipStreamGetDevice");
+  if (rc) return rc;
+  if ((int)sdev != dev)
+    return fail(NAYLIS_ERR_ARG,
+                "mom_read_bwd_noalloc: the stream belongs to device %d but device %d is current; make the stream's "
+                "device current before the call",
+                (int)sdev, dev);
   if (dev < 0 || dev >= kScratchDevices)
     return fail(NAYLIS_ERR_ARG, "mom_read_bwd_noalloc: device %d beyond the %d the library tracks", dev,
                 kScratchDevices);
@@ -258,23 +318,25 @@ int scratch_address(void** out) {
 }  // namespace
 
 int naylis_mom_read_bwd_noalloc(const void* q, const void* k, const void* v, const int32_t* top_idx,
-                                const float* top_gates, const int32_t* token_order, const void* out, const float* lse,
-                                const void* dout, void* dq, void* dk, void* dv, float* dgates, int64_t B, int64_t S,
-                                int64_t H, int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t top_k,
-                                void* stream) {
+                                const float* top_gates, const int32_t* token_order, const void* out,
+                                const void* side, const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                                float* dgates, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                                int64_t num_blocks, int64_t block_size, int64_t top_k, void* stream) {
   ReadDims d;
   int rc = check_read_dims(B, S, H, head_dim, num_blocks, block_size, top_k, &d);
   if (rc) return rc;
-  const size_t need = plan_read_ws(d).total;
+  d.order = token_order;
+  const size_t need = (side != nullptr && read_pair_bwd_ok(d, (long)B * S)) ? plan_pair_ws(d).total
+                                                                               : plan_read_ws(d).total;
   if (need > NAYLIS_READ_BWD_NOALLOC_MAX_BYTES)
     return fail(NAYLIS_ERR_WORKSPACE,
                 "mom_read_bwd_noalloc: this read needs %zu bytes of workspace, more than the %zu of the library's "
                 "scratch array; call naylis_mom_read_bwd with a workspace",
                 need, (size_t)NAYLIS_READ_BWD_NOALLOC_MAX_BYTES);
   void* ws = nullptr;
-  if ((rc = scratch_address(&ws))) return rc;
-  return naylis_mom_read_bwd(q, k, v, top_idx, top_gates, token_order, out, lse, dout, dq, dk, dv, dgates, ws,
-                             NAYLIS_READ_BWD_NOALLOC_MAX_BYTES, B, S, H, head_dim, num_blocks, block_size, top_k,
+  if ((rc = scratch_address((hipStream_t)stream, &ws))) return rc;
+  return naylis_mom_read_bwd(q, k, v, top_idx, top_gates, token_order, out, side, lse, dout, dq, dk, dv, dgates,
+                             ws, NAYLIS_READ_BWD_NOALLOC_MAX_BYTES, B, S, H, head_dim, num_blocks, block_size, top_k,
                              stream);
 }
 
@@ -288,6 +350,11 @@ static int check_order_dims(int64_t B, int64_t S, int64_t num_blocks, int64_t to
     return fail(NAYLIS_ERR_ARG, "mom_read_order: top_k %lld must be in [1, min(%d, num_blocks=%lld)]",
                 (long long)top_k, NAYLIS_MAX_TOPK, (long long)num_blocks);
   return NAYLIS_OK;
+}
+
+int64_t naylis_mom_read_order_words(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k) {
+  if (check_order_dims(B, S, num_blocks, top_k) != NAYLIS_OK) return 0;
+  return read_order_words((long)(B * S), (int)num_blocks, (int)top_k);
 }
 
 size_t naylis_mom_read_order_workspace_bytes(int64_t B, int64_t S, int64_t num_blocks, int64_t top_k) {

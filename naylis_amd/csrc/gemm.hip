@@ -445,7 +445,9 @@ static void gemm_dispatch(const DevJobs& dj, const GemmLaunch& g, int kper, int 
   const int tiles_m = (g.M + C::BM - 1) / C::BM, tiles_n = (g.N + C::BN - 1) / C::BN;
   const dim3 grid(tiles_m * tiles_n * splits * g.njobs);
   float* ws = (float*)g.ws;
-  if (splits > 1) {
+  // The gate epilogue lives in the split-K reduction, so a gated launch takes
+  // the fp32-partial path even when K fits one split (K <= 64 tokens).
+  if (splits > 1 || g.gate_w != nullptr) {
     NAYLIS_TIMED(name, st,
                  hipLaunchKernelGGL((gemm_kernel<C, AKC, BKC, 2>), grid, dim3(C::NT), 0, st, dj, g.M, g.N, g.K1, kper,
                                     tiles_m, tiles_n, splits, g.njobs, g.K, ws));

@@ -9,15 +9,20 @@ namespace naylis {
 
 struct ReadDims {
   int B, S, H, HD, L, E, block_size, topk;
-  // Token order of the read's tiles, from launch_read_order: 1 + N int32,
-  // word 0 = 1 when words 1..N map position -> flattened token b*S + s, 0 for
-  // sequence order; nullptr is sequence order too.
+  // Token order of the read's tiles, from launch_read_order: word 0 = 1 when
+  // words 1..N map position -> flattened token b*S + s (grouped order), 0 for
+  // sequence order, then the pair plan when read_has_pair_plan; nullptr is
+  // sequence order.
   const int32_t* order = nullptr;
 };
 
 // The read's token order (read_order.hip): tokens grouped by selected blocks
 // when that lowers the (tile, block) pairs, else the sequence-order mode word.
 size_t read_order_ws_bytes(long N, int E, int topk);
+// true when launch_read_order also writes the pair plan (top-2 over at most
+// 32 blocks, 1 <= N <= 2^18); the order buffer then has read_order_words words
+bool read_has_pair_plan(long N, int E, int topk);
+long read_order_words(long N, int E, int topk);
 hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, int32_t* order, void* ws,
                              hipStream_t st);
 
@@ -40,6 +45,25 @@ hipError_t launch_read_bwd_dkdv(const void* q, const void* k, const void* v, con
 hipError_t launch_read_bwd_reduce(const float* dk_part, const float* dv_part, const int32_t* count,
                                   const float* dlg_part, const float* top_gates, void* dk, void* dv, float* dgates,
                                   const ReadDims& d, hipStream_t st);
+
+// Pair-tiled read (read_pair.hip): head_dim 64, block size 128, top-2 over at
+// most 32 blocks (backward: 8), with the pair plan in d.order.
+bool read_pair_fwd_shapes(const ReadDims& d, long N);  // the shape conditions alone
+bool read_pair_bwd_shapes(const ReadDims& d, long N);
+bool read_pair_fwd_ok(const ReadDims& d, long N);  // shapes and an order buffer (with its plan)
+bool read_pair_bwd_ok(const ReadDims& d, long N);
+int read_pair_ranges(const ReadDims& d);
+int read_pair_segments(const ReadDims& d);
+size_t read_pair_part_bytes(const ReadDims& d);  // one of the dK / dV partial arrays
+// bytes of the side buffer the pair forward writes for the pair backward
+size_t read_pair_side_bytes(const ReadDims& d);
+hipError_t launch_read_fwd_pair(const void* q, const void* k, const void* v, const int32_t* top_idx,
+                                const float* top_gates, void* out, void* side, float* lse, const ReadDims& d,
+                                hipStream_t st);
+hipError_t launch_read_bwd_pair(const void* q, const void* k, const void* v, const int32_t* top_idx,
+                                const float* top_gates, const void* o, const void* side, const void* dout,
+                                const float* lse, void* dq, void* dk, void* dv, float* dgates, float* dlg_part,
+                                float* dk_part, float* dv_part, const ReadDims& d, hipStream_t st);
 
 // Decode step (decode.hip): B sequences, D = H * HD features, router rank R,
 // E experts (= bank blocks) of block_size slots, top-k blocks per token.

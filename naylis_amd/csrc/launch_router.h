@@ -37,19 +37,24 @@ bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const Router
 void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_up, const float* noise,
                             float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
                             float* act, float* y, double* ycs, const RouterDims& d, hipStream_t st);
-// fast backward (B1 + B2): w, its 32-token chunk sums, W~ and the dW_up
-// partials; returns the number of dW_up partials
+// fast backward (B1 + B2): w, its 32-token chunk sums, W~ (skipped when
+// fuse_scan: the dx kernel then forms it) and the dW_up partials; returns the
+// number of dW_up partials
 int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,
                             const float* dg, const float* dp, const float* dl, const float* w_up, float* w,
-                            double* wcs, float* wt, float* dwup_part, const RouterDims& d, hipStream_t st);
+                            double* wcs, float* wt, float* dwup_part, bool fuse_scan, const RouterDims& d,
+                            hipStream_t st);
 // Load-balance statistics of a routing (router_stats.hip): stats[2E + 3].
 size_t router_stats_ws_bytes(long N, int E);
 hipError_t launch_router_stats(const float* probs, const int32_t* top_idx, float* stats, void* ws, long N, int E,
                                int topk, hipStream_t st);
-// true when the dx kernel forms W~ from w and its chunk sums itself (R <= 32,
-// T a multiple of its 256-token range): launch_router_fast_scan then skips B2
+// true when the dx kernel can form W~ from w and its chunk sums itself (R <=
+// 32, T a multiple of its 256-token range, one round of workgroups).  The
+// caller decides once per backward and passes the same flag to
+// launch_router_fast_scan (which then skips B2) and launch_router_fast_dx.
 bool router_fast_dx_fuses_scan(const RouterDims& d);
 void launch_router_fast_dx(const void* x, const float* wt, const float* w, const double* wcs, const float* w_down,
-                           const void* dx_in, void* dx, float* dwd_part, const RouterDims& d, hipStream_t st);
+                           const void* dx_in, void* dx, float* dwd_part, bool fuse_scan, const RouterDims& d,
+                           hipStream_t st);
 
 }  // namespace naylis

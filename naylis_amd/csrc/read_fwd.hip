@@ -303,32 +303,6 @@ __global__ __launch_bounds__(512) void read_fwd_kernel(
 // rescale of O.  The row sum l adds the bf16 weights that multiply V
 // (v_dot2c_f32_bf16), so O / l is a convex combination of V rows exactly as
 // the MFMA sees them.
-__device__ __forceinline__ float pair_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float max16(const f32x16& x) {
-  float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
-#pragma unroll
-  for (int v = 3; v < 15; v += 2) m = fmaxf(fmaxf(m, x[v]), x[v + 1]);
-  return fmaxf(m, x[15]);
-}
-// Sum of 8 bf16 values into an fp32 accumulator (v_dot2c_f32_bf16 against 1.0).
-__device__ __forceinline__ float add_bf16x8(const bf16x8& p, float acc) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  const uint4 u = __builtin_bit_cast(uint4, p);
-  float s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.x), one, acc, false);
-  float s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.y), one, 0.f, false);
-  s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.z), one, s0, false);
-  s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u.w), one, s1, false);
-  return s0 + s1;
-}
-
 template <int TK>
 __global__ __launch_bounds__(256, 4) void read_fwd_fast_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,

@@ -22,7 +22,10 @@
 // Kernels: (1) per 1024-token chunk, each token's rank among the chunk's
 // earlier tokens of the same key, the chunk's key histogram and its tiles'
 // sequence-order block counts; (2) per chunk, key offsets (a scan over the
-// histograms), the decision, and the placement of the chunk's tokens.
+// histograms), the decision, and the placement of the chunk's tokens.  The
+// second launch also writes the pair plan (read_common.h): the grouped table
+// (always, whatever the decision), the keys with tokens, their 32-token tiles
+// and the forward's work items; its first workgroup writes the lists.
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
@@ -127,25 +130,112 @@ __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* _
   }
 }
 
+// Inclusive scan of x over the first n threads of the workgroup (n <= 1024),
+// in LDS array a; every thread of the workgroup must call it.
+__device__ __forceinline__ void block_scan_incl(int32_t* a, int n, int x) {
+  const int tid = threadIdx.x;
+  if (tid < n) a[tid] = x;
+  __syncthreads();
+  for (int st = 1; st < n; st <<= 1) {
+    const int add = (tid < n && tid >= st) ? a[tid - st] : 0;
+    __syncthreads();
+    if (tid < n) a[tid] += add;
+    __syncthreads();
+  }
+}
+
+// Largest i in [0, n) with a[i] <= x (a ascending, a[0] <= x).
+__device__ __forceinline__ int last_le(const int32_t* a, int n, int x) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a[mid] <= x) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// The pair plan (layout in read_common.h), written by one workgroup of the
+// scatter launch from the key totals (`all` of thread t = tokens of key t,
+// ends / nzs the inclusive scans of the totals and of "key has tokens").
+__device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int nkeys, int all,
+                                const int32_t* ends, const int32_t* nzs, int32_t* tsc, int32_t* fsc, int32_t* ktile,
+                                int32_t* kfit, int32_t* kpos, int32_t* kcnt, int32_t* kab) {
+  const PairPlanLayout pl = pair_plan_layout(N, E);
+  int32_t* hdr = order + pl.hdr;
+  int32_t* kl = order + pl.keys;
+  int32_t* tl = order + pl.tiles;
+  int32_t* fl = order + pl.fitems;
+  const int tid = threadIdx.x;
+  const int nt = tid < nkeys ? (all + kPairTile - 1) / kPairTile : 0;
+  const int nf = (nt + kPairFwdItem - 1) / kPairFwdItem;
+  block_scan_incl(tsc, nkeys, nt);
+  block_scan_incl(fsc, nkeys, nf);
+  if (tid < nkeys && all > 0) {
+    const int k = nzs[tid] - 1;
+    const int a = tid / E, b = tid % E;
+    ktile[k] = tsc[tid] - nt;
+    kfit[k] = fsc[tid] - nf;
+    kpos[k] = ends[tid] - all;
+    kcnt[k] = all;
+    kab[k] = a | (b << 5);
+    kl[4 * k + 0] = a;
+    kl[4 * k + 1] = b;
+    kl[4 * k + 2] = tsc[tid] - nt;
+    kl[4 * k + 3] = nt;
+  }
+  __syncthreads();
+  const int nnz = nzs[nkeys - 1];
+  const int n_tiles = tsc[nkeys - 1], n_fit = fsc[nkeys - 1];
+  if (tid == 0) {
+    hdr[0] = n_tiles;
+    hdr[1] = nnz;
+    hdr[2] = n_fit;
+    for (int i = 3; i < 8; ++i) hdr[i] = 0;
+  }
+  for (int t = tid; t < n_tiles; t += blockDim.x) {
+    const int k = last_le(ktile, nnz, t);
+    const int j = t - ktile[k];
+    const int cnt = min(kPairTile, kcnt[k] - j * kPairTile);
+    const int ab = kab[k];
+    tl[2 * t] = kpos[k] + j * kPairTile;
+    tl[2 * t + 1] = cnt | ((ab & 31) << 6) | (((ab >> 5) & 31) << 11) | (k << 16);
+  }
+  constexpr int item_tokens = kPairFwdItem * kPairTile;
+  for (int i = tid; i < n_fit; i += blockDim.x) {
+    const int k = last_le(kfit, nnz, i);
+    const int c = i - kfit[k];
+    const int ab = kab[k];
+    fl[2 * i] = kpos[k] + c * item_tokens;
+    fl[2 * i + 1] = min(item_tokens, kcnt[k] - c * item_tokens) | ((ab & 31) << 16) | (((ab >> 5) & 31) << 21);
+  }
+}
+
 // (2) per chunk: key offsets = (tokens of smaller keys) + (tokens of the same
 // key in earlier chunks).  Every workgroup also evaluates the decision from
 // the same data: in the grouped order a tile's blocks are the union of the
 // block pairs of the keys whose segments overlap it, which the offsets give
 // exactly.  Grouping is kept when it lowers the (tile, block) pairs by at
-// least 10 %: then order[1 + offset + rank] = token and the mode word
-// order[0] = 1; otherwise order[0] = 0 and the table is not written.
+// least 10 %: then the mode word order[0] = 1, otherwise 0.  The table
+// order[1 + offset + rank] = token is written when grouping is kept or when
+// the pair plan is (write_plan), which the first workgroup adds.
 __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t* __restrict__ keys,
                                                                   const int32_t* __restrict__ rank,
                                                                   const int32_t* __restrict__ hist,
                                                                   const int32_t* __restrict__ seqcnt,
                                                                   int32_t* __restrict__ order, long N, int E,
-                                                                  int nchunks) {
+                                                                  int nchunks, bool write_plan) {
   __shared__ int32_t off[kOrdMaxE * kOrdMaxE];
   __shared__ int32_t ends[kOrdMaxE * kOrdMaxE];  // inclusive scan of the key totals
   __shared__ int32_t nzs[kOrdMaxE * kOrdMaxE];   // inclusive scan of "key has tokens"
   __shared__ int32_t cend[kOrdMaxE * kOrdMaxE];  // the keys with tokens, ascending: segment end
   __shared__ uint32_t cmask[kOrdMaxE * kOrdMaxE];  // and block pair mask
   __shared__ long red[2][kOrdWaves];
+  // pair plan (first workgroup): inclusive scans over keys of their tiles and
+  // forward items, and per key with tokens (ascending) its first tile, first
+  // item, first position, token count and blocks
+  __shared__ int32_t tsc[kOrdMaxE * kOrdMaxE], fsc[kOrdMaxE * kOrdMaxE];
+  __shared__ int32_t ktile[kOrdMaxE * kOrdMaxE], kfit[kOrdMaxE * kOrdMaxE], kpos[kOrdMaxE * kOrdMaxE];
+  __shared__ int32_t kcnt[kOrdMaxE * kOrdMaxE], kab[kOrdMaxE * kOrdMaxE];
   const int nkeys = E * E;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x;
@@ -220,8 +310,9 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
   }
   const bool grouped = g_all * 10 <= s_all * 9;
   if (c == 0 && tid == 0) order[0] = grouped ? 1 : 0;  // the mode word
+  if (write_plan && c == 0) write_pair_plan(order, N, E, nkeys, all, ends, nzs, tsc, fsc, ktile, kfit, kpos, kcnt, kab);
   const long tok = (long)c * kOrdChunk + tid;
-  if (tok >= N || !grouped) return;
+  if (tok >= N || !(grouped || write_plan)) return;
   const long dst = (long)off[keys[tok]] + rank[tok];
   if (dst >= 0 && dst < N) order[1 + dst] = (int32_t)tok;
 }
@@ -233,6 +324,12 @@ __global__ __launch_bounds__(64) void order_sequence_kernel(int32_t* __restrict_
 
 size_t read_order_ws_bytes(long N, int E, int topk) {
   return ord_grouping(N, E, topk) ? plan_order_ws(N, E).total : 256;
+}
+
+bool read_has_pair_plan(long N, int E, int topk) { return N > 0 && ord_grouping(N, E, topk); }
+
+long read_order_words(long N, int E, int topk) {
+  return read_has_pair_plan(N, E, topk) ? pair_plan_layout(N, E).words : 1 + N;
 }
 
 hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, int32_t* order, void* ws,
@@ -254,7 +351,7 @@ hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, in
                                   seqcnt, N, E));
   NAYLIS_TIMED("read_order", st,
                hipLaunchKernelGGL(order_scatter_kernel, dim3(nchunks), dim3(kOrdChunk), 0, st, keys, rank, hist,
-                                  seqcnt, order, N, E, nchunks));
+                                  seqcnt, order, N, E, nchunks, true));
   return hipGetLastError();
 }
 

@@ -889,10 +889,11 @@ hipError_t launch_router_bwd(const void* x, bool x_bf16, const float* w_down, co
   }
   const bool fast = router_fast_bwd_ok(x, x_bf16, dx, d);
   if (fast) {
+    const bool fuse_scan = router_fast_dx_fuses_scan(d);  // decided once: both launches must agree
     const int n_up = launch_router_fast_scan(act, probs, top_idx, top_gates, d_gates, d_probs, d_logits, w_up, wbuf,
-                                             (double*)(base + w.scan_csum), wt, dwup_part, d, st);
+                                             (double*)(base + w.scan_csum), wt, dwup_part, fuse_scan, d, st);
     launch_router_fast_dx(x, wt, wbuf, (const double*)(base + w.scan_csum), w_down, dx_accumulate ? dx : nullptr, dx,
-                          dwd_part, d, st);
+                          dwd_part, fuse_scan, d, st);
     launch_router_reduce2(dwd_part, dw_down, nwd, (int)((ntok + kDxRange - 1) / kDxRange), dwup_part, dw_up, nwu,
                           n_up, st);
     return hipGetLastError();

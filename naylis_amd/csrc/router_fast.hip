@@ -21,6 +21,7 @@
 // w_t = dz_t / (t+1) (router.hip).  W~ enters the MFMA as a bf16 hi/lo pair,
 // W_down as a hi/lo pair; the three significant products give 2^-16 relative
 // accuracy for the bf16 dx, and x is exact for dW_down.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -825,13 +826,16 @@ void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_u
 // per workgroup round: fuse only while the grid fits two workgroups per CU
 // (LDS: 59 KB per workgroup), where it replaces a whole launch.
 static int device_cus() {
-  static int cached[64] = {};  // per device; a racing first call stores the same value
+  static std::atomic<int> cached[64] = {};  // per device; a racing first call stores the same value
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev >= 0 && dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cached[dev] = n;
+  if (dev >= 0 && dev < 64 && n > 0) cached[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
@@ -841,11 +845,12 @@ bool router_fast_dx_fuses_scan(const RouterDims& d) {
 }
 
 void launch_router_fast_dx(const void* x, const float* wt, const float* w, const double* wcs, const float* w_down,
-                           const void* dx_in, void* dx, float* dwd_part, const RouterDims& d, hipStream_t st) {
+                           const void* dx_in, void* dx, float* dwd_part, bool fuse_scan, const RouterDims& d,
+                           hipStream_t st) {
   const long ntok = (long)d.B * d.T;
   const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
   const dim3 grid((unsigned)((ntok + kFastDxRange - 1) / kFastDxRange), d.D / kFastDxSlab);
-  if (router_fast_dx_fuses_scan(d))
+  if (fuse_scan)
     NAYLIS_TIMED("router_bwd_dx", st,
                  hipLaunchKernelGGL((router_dx_fast_kernel<1, true>), grid, dim3(256), 0, st, (const bf16_t*)x, wt,
                                     w_down, (const bf16_t*)dx_in, (bf16_t*)dx, dwd_part, d.D, d.R, ntok, w, wcs, d.T,
@@ -879,7 +884,8 @@ static void fast_token(const float* act, const float* probs, const int32_t* idx,
 
 int launch_router_fast_scan(const float* act, const float* probs, const int32_t* idx, const float* gates,
                             const float* dg, const float* dp, const float* dl, const float* w_up, float* w,
-                            double* wcs, float* wt, float* dwup_part, const RouterDims& d, hipStream_t st) {
+                            double* wcs, float* wt, float* dwup_part, bool fuse_scan, const RouterDims& d,
+                            hipStream_t st) {
   if (d.E <= 8 && d.topk <= 2)
     fast_token<8, 2>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
   else if (d.E <= 8)
@@ -889,7 +895,7 @@ int launch_router_fast_scan(const float* act, const float* probs, const int32_t*
   else
     fast_token<64, 8>(act, probs, idx, gates, dg, dp, dl, w_up, w, wcs, dwup_part, d, st);
   const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
-  if (!router_fast_dx_fuses_scan(d))  // else the dx kernel forms W~ itself
+  if (!fuse_scan)  // else the dx kernel forms W~ itself
     NAYLIS_TIMED("router_bwd_scan", st,
                  hipLaunchKernelGGL(router_wtilde_kernel, dim3(n_ch, d.B), dim3(256), 0, st, w, wcs, wt, d.T, d.R,
                                     n_ch));

@@ -24,7 +24,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from .hip_linear import library_wgrad as _wgrad
-from .hip_read import read_order
+from .hip_read import _ptr, read_order, read_side
 from .hip_rezero import gated_linear_backward, gated_linear_forward
 from .hip_router import d_probs_arg
 
@@ -107,16 +107,18 @@ class MomLayerFunction(torch.autograd.Function):
             q = F.linear(x, w_q)
             order = read_order(top_idx, num_blocks)
             out = torch.empty_like(q)
+            side = read_side(lib, out.view(B, T, H, HD), num_blocks, block_size, top_k)
             lse = torch.empty((H, B, T), **f32)
             _lib.check(lib.naylis_mom_read_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), order.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), None, 0, B, T, H, HD, num_blocks, block_size, top_k, st))
+                out.data_ptr(), _ptr(side), lse.data_ptr(), None, 0, B, T, H, HD, num_blocks, block_size, top_k,
+                st))
             # ---- o projection and ReZero gate (model.py:251, 239): one GEMM, the gate
             # folded into the weight
             y, w_os = gated_linear_forward(lib, out.view(B * T, D), w_o, scale, st)
             y = y.view(B, T, D)
         ctx.save_for_backward(x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v,
-                              q, order, out, lse, w_os)
+                              q, order, out, side, lse, w_os)
         ctx.geom = geom
         ctx.external_bank = k_ext is not None
         ctx.m_shape = None if k_ext is not None else (tuple(M_blocks.shape), m_dtype)
@@ -126,8 +128,8 @@ class MomLayerFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, d_probs, _d_idx):
-        (x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order, out, lse,
-         w_os) = ctx.saved_tensors
+        (x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order, out, side,
+         lse, w_os) = ctx.saved_tensors
         n_heads, num_blocks, block_size, top_k, _ = ctx.geom
         lib = _lib.load()
         B, T, D = x.shape
@@ -155,7 +157,8 @@ class MomLayerFunction(torch.autograd.Function):
             rws = _ws(nbytes, dev)
             _lib.check(lib.naylis_mom_read_bwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), gates.data_ptr(), order.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                out.data_ptr(), _ptr(side), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                dv.data_ptr(),
                 dgates.data_ptr(), rws.data_ptr(), rws.numel(), B, T, H, HD, num_blocks, block_size, top_k, st))
             del rws, dout
             # ---- bank K/V (the caller's grouped node takes dK, dV when it projected the bank)

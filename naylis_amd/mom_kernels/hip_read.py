@@ -19,13 +19,18 @@ def _workspace(nbytes, device):
 
 def read_order(top_idx, num_blocks):
     """The token order the read uses for this routing (C ABI:
-    naylis_mom_read_order): an int32 tensor of 1 + B*S words, word 0 = 1 when
-    words 1.. hold the grouped position -> token table, 0 for sequence order.
-    Launched on the current stream; top_idx must be int32 (B, S, k)."""
+    naylis_mom_read_order): an int32 tensor of naylis_mom_read_order_words()
+    words, word 0 = 1 when words 1..B*S hold the grouped position -> token
+    table, 0 for sequence order, followed (top-2 over at most 32 blocks) by
+    the pair plan of the pair-tiled kernels.  Launched on the current stream;
+    top_idx must be int32 (B, S, k)."""
     lib = _lib.load()
     B, S, topk = top_idx.shape
     dev = top_idx.device
-    order = torch.empty((1 + B * S,), device=dev, dtype=torch.int32)
+    words = int(lib.naylis_mom_read_order_words(B, S, num_blocks, topk))
+    if words <= 0:
+        _lib.check(_lib.NAYLIS_ERR_ARG)
+    order = torch.empty((words,), device=dev, dtype=torch.int32)
     ows = _workspace(lib.naylis_mom_read_order_workspace_bytes(B, S, num_blocks, topk), dev)
     with _lib.on_device(dev):
         rc = lib.naylis_mom_read_order(top_idx.data_ptr(), order.data_ptr(), ows.data_ptr(), ows.numel(),
@@ -36,9 +41,9 @@ def read_order(top_idx, num_blocks):
 
 class MomReadFunction(torch.autograd.Function):
     """Forward computes the token order (tokens grouped by selected blocks, or
-    sequence order when that does not pay) and saves (q, k, v, top_idx,
-    top_gates, order, o, lse); backward runs the dq / dk-dv / reduce launches
-    of the library with the same order."""
+    sequence order when that does not pay, plus the pair plan) and saves (q,
+    k, v, top_idx, top_gates, order, o, the pair path's side buffer when
+    it is used, lse); backward runs the library's backward with the same order."""
 
     @staticmethod
     def forward(ctx, q_sh, k, v, top_idx, top_gates, num_blocks, block_size):
@@ -47,23 +52,24 @@ class MomReadFunction(torch.autograd.Function):
         topk = top_idx.shape[-1]
         dev = q_sh.device
         out = torch.empty_like(q_sh)
+        side = read_side(lib, out, num_blocks, block_size, topk)
         lse = torch.empty((H, B, S), device=dev, dtype=torch.float32)
-        order = read_order(top_idx, num_blocks)  # mode word + table
+        order = read_order(top_idx, num_blocks)  # mode word + table (+ pair plan)
         with _lib.on_device(dev):
             st = _lib.stream_of(dev)
             rc = lib.naylis_mom_read_fwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
-                order.data_ptr(), out.data_ptr(), lse.data_ptr(), None, 0,
+                order.data_ptr(), out.data_ptr(), _ptr(side), lse.data_ptr(), None, 0,
                 B, S, H, HD, num_blocks, block_size, topk, st)
         _lib.check(rc)
-        ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, order, out, lse)
+        ctx.save_for_backward(q_sh, k, v, top_idx, top_gates, order, out, side, lse)
         ctx.geom = (num_blocks, block_size)
         return out
 
     @staticmethod
     def backward(ctx, dout):
         lib = _lib.load()
-        q_sh, k, v, top_idx, top_gates, order, out, lse = ctx.saved_tensors
+        q_sh, k, v, top_idx, top_gates, order, out, side, lse = ctx.saved_tensors
         num_blocks, block_size = ctx.geom
         B, S, H, HD = q_sh.shape
         topk = top_idx.shape[-1]
@@ -82,12 +88,28 @@ class MomReadFunction(torch.autograd.Function):
         with _lib.on_device(dev):
             rc = lib.naylis_mom_read_bwd(
                 q_sh.data_ptr(), k.data_ptr(), v.data_ptr(), top_idx.data_ptr(), top_gates.data_ptr(),
-                order.data_ptr(), out.data_ptr(), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                order.data_ptr(), out.data_ptr(), _ptr(side), lse.data_ptr(), dout.data_ptr(), dq.data_ptr(),
+                dk.data_ptr(),
                 dv.data_ptr(),
                 dgates.data_ptr(), ws.data_ptr(), ws.numel(),
                 B, S, H, HD, num_blocks, block_size, topk, _lib.stream_of(dev))
         _lib.check(rc)
         return dq, dk, dv, None, dgates, None, None
+
+
+def read_side(lib, out, num_blocks, block_size, top_k):
+    """The side buffer the pair-tiled forward leaves for its backward (o's
+    bf16 remainder, block shares), when the read takes that path both ways
+    (naylis_mom_read_side_bytes > 0), else None."""
+    B, S, H, HD = out.shape
+    nbytes = int(lib.naylis_mom_read_side_bytes(B, S, H, HD, num_blocks, block_size, top_k))
+    if nbytes > 0:
+        return torch.empty(nbytes, dtype=torch.uint8, device=out.device)
+    return None
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
 
 
 def mom_read(q_sh, k, v, top_idx, top_gates, *, num_blocks, block_size):

@@ -47,8 +47,8 @@ READ_OK = dict(B=2, S=64, H=2, hd=16, nb=4, bs=16, k=2)
 
 def read_fwd(lib, **kw):
     a = dict(READ_OK, **kw)
-    return lib.naylis_mom_read_fwd(1, 1, 1, 1, 1, None, 1, 1, None, 0, a["B"], a["S"], a["H"], a["hd"], a["nb"],
-                                   a["bs"], a["k"], None)
+    return lib.naylis_mom_read_fwd(1, 1, 1, 1, 1, None, 1, None, 1, None, 0, a["B"], a["S"], a["H"], a["hd"],
+                                   a["nb"], a["bs"], a["k"], None)
 
 
 @pytest.mark.parametrize("bad", [dict(hd=96), dict(hd=256), dict(hd=8), dict(k=0), dict(k=9), dict(k=5, nb=4),
@@ -62,20 +62,52 @@ def test_read_rejects_bad_arguments(lib, bad):
 
 
 def test_read_null_pointers_and_workspace(lib):
-    rc = lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, 0, 2, 64, 2, 16, 4, 16, 2, None)
+    rc = lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, None, 0, 2, 64, 2, 16, 4, 16,
+                                 2, None)
     assert rc == _lib.NAYLIS_ERR_ARG and b"null" in lib.naylis_mom_last_error()
-    ws = lib.naylis_mom_read_workspace_bytes(8, 2048, 16, 64, 8, 128, 2)
-    assert ws > 0
-    rc = lib.naylis_mom_read_bwd(*([1] * 13), 1, ws - 1, 8, 2048, 16, 64, 8, 128, 2, None)
-    assert rc == _lib.NAYLIS_ERR_WORKSPACE
+    # both backward paths refuse a workspace one byte short of the query: the two-pass kernels
+    # (16 blocks) and the pair-tiled ones (8 blocks, an order and a side buffer given)
+    for nb in (16, 8):
+        ws = lib.naylis_mom_read_workspace_bytes(8, 2048, 16, 64, nb, 128, 2)
+        assert ws > 0
+        rc = lib.naylis_mom_read_bwd(*([1] * 14), 1, ws - 1, 8, 2048, 16, 64, nb, 128, 2, None)
+        assert rc == _lib.NAYLIS_ERR_WORKSPACE, nb
     # empty sequences are a valid no-op for the forward
-    assert lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, 0, 2, 0, 2, 16, 4, 16, 2,
-                                   None) == _lib.NAYLIS_OK
+    assert lib.naylis_mom_read_fwd(None, None, None, None, None, None, None, None, None, None, 0, 2, 0, 2, 16, 4, 16,
+                                   2, None) == _lib.NAYLIS_OK
     # the token order: argument checks, workspace, empty input
     assert lib.naylis_mom_read_order_workspace_bytes(8, 2048, 8, 2) > 0
     assert lib.naylis_mom_read_order_workspace_bytes(8, 2048, 8, 9) == 0
     assert lib.naylis_mom_read_order(1, 1, 1, 1, 8, 2048, 8, 2, None) == _lib.NAYLIS_ERR_WORKSPACE
     assert lib.naylis_mom_read_order(None, None, None, 0, 0, 2048, 8, 2, None) == _lib.NAYLIS_OK
+    # the order buffer: 1 + N words, plus the pair plan for top-2 over at most 32 blocks
+    N = 8 * 2048
+    assert lib.naylis_mom_read_order_words(8, 2048, 8, 3) == 1 + N
+    assert lib.naylis_mom_read_order_words(8, 2048, 64, 2) == 1 + N
+    plan = lib.naylis_mom_read_order_words(8, 2048, 8, 2)
+    keys = 8 * 9 // 2
+    tiles = N // 32 + keys
+    assert plan == ((1 + N + 3) // 4) * 4 + 8 + 4 * keys + 4 * tiles
+    assert lib.naylis_mom_read_order_words(8, 2048, 8, 9) == 0
+
+
+@pytest.mark.parametrize("dims,want", [
+    ((8, 2048, 16, 64, 8, 128, 2), 1),    # config 2: the pair-tiled backward
+    ((1, 300, 4, 64, 4, 128, 2), 1),      # ragged, 4 blocks
+    ((4, 4096, 24, 64, 32, 128, 2), 0),   # config 4: 32 blocks (pair forward only)
+    ((8, 2048, 16, 32, 8, 128, 2), 0),    # head_dim 32
+    ((8, 2048, 16, 64, 8, 64, 2), 0),     # 64-slot blocks
+    ((8, 2048, 16, 64, 8, 128, 3), 0),    # top-3
+    ((8, 0, 16, 64, 8, 128, 2), 0),       # no tokens
+])
+def test_read_side_bytes_rule(lib, dims, want):
+    """naylis_mom_read_side_bytes > 0 exactly where the pair-tiled backward
+    applies: o's bf16 remainder (N x D bf16) and the block-a shares (H x N)."""
+    nbytes = lib.naylis_mom_read_side_bytes(*dims)
+    assert (nbytes > 0) == bool(want)
+    if want:
+        B, S, H, hd = dims[:4]
+        assert nbytes == -(-B * S * H * hd * 2 // 256) * 256 + B * S * H * 4
 
 
 def test_router_and_bank_reject_bad_arguments(lib):
@@ -251,9 +283,9 @@ def test_read_bwd_noalloc_refuses_before_touching_a_device(lib):
     max_bytes = int(m.group(1)) << int(m.group(2))
     dims = (1, 64, 16, 128, 128, 128, 2)              # 16384 slots of 16 x 128: 256 MiB of dK/dV partials
     assert lib.naylis_mom_read_workspace_bytes(*dims) > max_bytes
-    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), *dims, None) == _lib.NAYLIS_ERR_WORKSPACE
+    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 14), *dims, None) == _lib.NAYLIS_ERR_WORKSPACE
     assert b"scratch" in lib.naylis_mom_last_error()
-    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 13), 1, 64, 2, 96, 4, 16, 2, None) == _lib.NAYLIS_ERR_ARG
+    assert lib.naylis_mom_read_bwd_noalloc(*([1] * 14), 1, 64, 2, 96, 4, 16, 2, None) == _lib.NAYLIS_ERR_ARG
 
 
 def test_bank_grouped_rejects_bad_arguments(lib):

@@ -29,6 +29,9 @@ CASES = [
     (1, 192, 2, 64, 8, 32, 3, "distinct"),   # top-3
     (1, 256, 2, 64, 32, 128, 2, "distinct"), # 32 blocks (config-4 geometry)
     (1, 96, 2, 32, 3, 48, 2, "random"),      # block_size 48: not a multiple of 32
+    # the pair-tiled path (head_dim 64, 128-slot blocks, top-2, at most 8 blocks)
+    (2, 200, 2, 64, 4, 128, 2, "random"),    # duplicate ids: one-block pairs, ragged tiles
+    (1, 2048, 4, 64, 8, 128, 2, "distinct"), # many ranges per head, ranges crossing pairs
 ]
 
 
@@ -89,8 +92,8 @@ def test_read_fwd_bwd_matches_oracle(case, dev):
     assert worst < 2e-2, worst
 
 
-@pytest.mark.parametrize("big_block", [1, 0])
-def test_read_score_jump_moves_the_reference(big_block, dev):
+@pytest.mark.parametrize("big_block,BS", [(1, 64), (0, 64), (1, 128), (0, 128)])
+def test_read_score_jump_moves_the_reference(big_block, BS, dev):
     """Every token selects blocks 0 and 1; the scores of one block sit about
     2^138 above the other's in p.  With the large block second, the forward's
     reference (set from a score of the token's first selected chunk) is far
@@ -99,9 +102,10 @@ def test_read_score_jump_moves_the_reference(big_block, dev):
     backward against the fp32 oracle.  All the weight lands on one block, so
     the gates' true gradient is ~0: the backward must normalise its recomputed
     weights by their sum (the forward's lse carries the rounding of its bf16
-    row sum) for the gate gradient to come out ~0 too."""
+    row sum) for the gate gradient to come out ~0 too.  128-slot blocks take
+    the pair-tiled kernels, whose delta comes from o and its bf16 remainder."""
     from naylis_amd import mom_kernels
-    B, S, H, HD, NB, BS = 1, 128, 2, 64, 4, 64
+    B, S, H, HD, NB = 1, 128, 2, 64, 4
     g = torch.Generator().manual_seed(21)
     L, D = NB * BS, H * HD
     q = (1.0 + 0.1 * torch.randn(B, S, H, HD, generator=g)).bfloat16()
@@ -239,6 +243,51 @@ def test_read_dkdv_work_split_edges(dev):
     out, dq, dk, dv, dg = res[0]
     assert float(dk[:4 * BS].float().abs().max()) == 0.0 and float(dv[:4 * BS].float().abs().max()) == 0.0
     assert float(dv[4 * BS:5 * BS].float().abs().max()) > 0.0
+    qf, kf, vf, gf = (t.to(dev).float().requires_grad_(True) for t in (q, k, v, gates))
+    ref = oracle.mom_read(qf, kf, vf, top.to(dev), gf, num_blocks=NB, block_size=BS)
+    ref.backward(dout.to(dev).float())
+    assert_close(out, ref, "out")
+    assert_close(dq, qf.grad, "dq")
+    assert_close(dk, kf.grad, "dk")
+    assert_close(dv, vf.grad, "dv")
+    assert_close(dg, gf.grad, "d_gates")
+
+
+def test_read_pair_path_edges(dev):
+    """The pair-tiled kernels (head_dim 64, 128-slot blocks, top-2): two heads
+    give many short backward ranges, each crossing several pairs (their
+    dK / dV go out as (range, pair) partials); blocks 0 and 1 are never
+    selected (zero dK / dV rows), block 2 by one token (a pair of one tile),
+    the rest unevenly, with a few duplicate selections (one-block pairs).
+    The library must take the pair path (its launches are timed under their
+    own names), match the fp32 oracle and repeat bitwise."""
+    from naylis_amd import _lib, mom_kernels
+    B, S, H, HD, NB, BS, topk = 2, 1000, 2, 64, 8, 128, 2
+    g = torch.Generator().manual_seed(91)
+    L, D = NB * BS, H * HD
+    q = (torch.randn(B, S, H, HD, generator=g) * 0.7).bfloat16()
+    k = (torch.randn(L, D, generator=g) * 0.4).bfloat16()
+    v = (torch.randn(L, D, generator=g) * 0.4).bfloat16()
+    gates = F.softmax(torch.randn(B, S, topk, generator=g), -1)
+    w = torch.tensor([1.0, 2.0, 3.0, 5.0, 8.0])             # blocks 3..7, uneven popularity
+    top = 3 + torch.multinomial(w, B * S * topk, replacement=True, generator=g).view(B, S, topk)
+    top[0, 17, 1] = 2                                        # block 2: one token
+    dout = torch.randn(B, S, H, HD, generator=g).bfloat16()
+    res = []
+    for rep in range(2):
+        qd, kd, vd, gd = (t.to(dev).requires_grad_(True) for t in (q, k, v, gates))
+        with _lib.KernelTimer():
+            out = mom_kernels.mom_read(qd, kd, vd, top.to(dev), gd, num_blocks=NB, block_size=BS, mode="hip")
+            out.backward(dout.to(dev))
+            torch.cuda.synchronize()
+        names = _lib.KernelTimer.results()
+        assert "read_bwd_pair" in names and "read_bwd_dq" not in names, sorted(names)
+        res.append([t.detach().clone() for t in (out, qd.grad, kd.grad, vd.grad, gd.grad)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    out, dq, dk, dv, dg = res[0]
+    assert float(dk[:2 * BS].float().abs().max()) == 0.0 and float(dv[:2 * BS].float().abs().max()) == 0.0
+    assert float(dv[2 * BS:3 * BS].float().abs().max()) > 0.0
     qf, kf, vf, gf = (t.to(dev).float().requires_grad_(True) for t in (q, k, v, gates))
     ref = oracle.mom_read(qf, kf, vf, top.to(dev), gf, num_blocks=NB, block_size=BS)
     ref.backward(dout.to(dev).float())

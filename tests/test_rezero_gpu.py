@@ -72,7 +72,7 @@ def test_rezero_scale_matches_torch(n, xdt, ydt, dev):
     assert torch.equal(y, (x.float() * s).to(ydt))
 
 
-@pytest.mark.parametrize("N,D,s0", [(8 * 2048, 1024, 0.37), (300 * 8, 256, 0.0)])
+@pytest.mark.parametrize("N,D,s0", [(8 * 2048, 1024, 0.37), (300 * 8, 256, 0.0), (8, 256, 0.37), (64, 128, -0.6)])
 def test_gated_linear_matches_fp64(N, D, s0, dev):
     """mom_gated_linear: y = s (o W^T) in fp32 as one GEMM on the scaled bf16
     weight W' = bf16(s W) (model.py:251 then 239), and its backward (d o, dW,
@@ -106,14 +106,17 @@ def test_gated_linear_matches_fp64(N, D, s0, dev):
     assert abs(float(s.grad) - ref_ds) <= 2.0 ** -8 * float((dyd * z).abs().sum()) + 1e-6
 
 
-@pytest.mark.parametrize("N,D_in,D_out", [(8 * 2048, 1024, 1024), (2400, 256, 512), (0, 64, 64)])
+@pytest.mark.parametrize("N,D_in,D_out", [(8 * 2048, 1024, 1024), (2400, 256, 512), (0, 64, 64), (8, 256, 128),
+                                          (64, 128, 256)])
 def test_gated_wgrad_matches_two_steps(N, D_in, D_out, dev):
     """naylis_mom_gated_wgrad (dW' kept inside the split-K reduction, whose
     epilogue writes dw = bf16(s dW') and the partials of ds = sum(dW' w))
     against naylis_mom_linear_wgrad's fp32 dW' followed by naylis_mom_rezero_bwd
     over the weight.  dw is bitwise equal where both split K alike (config-2
     shape: 8 splits), else within one bf16 rounding; ds differs only in its
-    fp32 summation order.  N = 0 gives zeros over poisoned outputs."""
+    fp32 summation order.  N = 0 gives zeros over poisoned outputs; N = 8 and
+    64 fit one K split, where the gate epilogue must still run (its outputs
+    start poisoned)."""
     from naylis_amd import _lib
     from naylis_amd.mom_kernels.hip_linear import library_wgrad
     lib = _lib.load()
