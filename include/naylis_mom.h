@@ -65,15 +65,16 @@ const char* naylis_mom_last_error(void);
  *   out      (B, S, H, head_dim) bf16
  *   side     naylis_mom_read_side_bytes() bytes, or NULL: what the
  *                                          pair-tiled forward leaves for the
- *                                          pair-tiled backward (o's bf16
- *                                          remainder o - bf16(o), so delta =
- *                                          rowsum(o * dO) has fp32 accuracy,
- *                                          and each row's share of its weight
- *                                          on the pair's first block).  Used
+ *                                          pair-tiled backward (each row's
+ *                                          share of its weight on the pair's
+ *                                          first block, (H, B, S) fp32).  Used
  *                                          when side_bytes > 0 and a
  *                                          token_order is given; with NULL the
  *                                          backward takes the two-pass
- *                                          kernels.  Ignored otherwise.
+ *                                          kernels.  Ignored otherwise.  The
+ *                                          pair-tiled backward computes its
+ *                                          products in fp16 (inputs beyond
+ *                                          +-65504 saturate).
  *   lse      (H, B, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
  *   token_order  int32 or NULL             the order in which the read walks

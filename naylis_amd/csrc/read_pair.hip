@@ -10,13 +10,13 @@
 // resident for all of its tiles, with no per-tile block lists and no
 // per-chunk selection tests:
 //
-//  * forward: one workgroup per (head, up to 8 tiles of one pair), 4 waves;
+//  * forward: persistent workgroups over the (head, up to 8 tiles of one
+//    pair) items, 4 waves;
 //    K and V of the pair staged in LDS once, each wave walks its tiles
 //    (S^T = K Q^T per 32-slot chunk, online softmax per token column, O^T +=
 //    V^T P^T), as the sequence-order kernel of read_fwd.hip does per chunk.
-//    It also writes, into a side buffer for the backward, o's bf16 remainder
-//    (o - bf16(o)), from which the backward forms delta = rowsum(o * dO) to
-//    fp32 accuracy, and each row's share of its weight on block a.
+//    It also writes, into a side buffer for the backward, each row's share of
+//    its weight on block a (the backward's gate gradients use it).
 //  * backward: one workgroup per (head, equal range of the head's tiles), 8
 //    waves each owning 32 of the pair's 256 slots.  Per tile S = Q K^T,
 //    dP - delta = dO V^T - delta, P and dS once, then dV^T += dO^T P and dK^T
@@ -31,6 +31,8 @@
 //    order, dK scaled; d(gates) = per-head partials summed in head order.
 // No floating-point atomics: results are bitwise reproducible.
 #include <algorithm>
+#include <atomic>
+#include <type_traits>
 
 #include "launch.h"
 #include "read_common.h"
@@ -47,9 +49,75 @@ constexpr int kPSlots = 2 * kPBS;     // slots of a pair
 constexpr int kPDsPitch = kPairTile + 8;  // LDS row pitch of dS^T (slot rows, token columns)
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f32x4v mfma16(const bf16x8& a, const bf16x8& b, const f32x4v& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+// Buffer accesses of the tile pipelines.  A lane with nothing to load or
+// store passes an offset past every buffer's end: the load returns 0 and the
+// store is dropped, so every lane issues the same memory instructions and
+// the compiler's in-order counter waits only for what each use needs (a load
+// or store skipped on some path makes it wait for everything outstanding).
+constexpr uint32_t kOob = 0x80000000u;
+__device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint4 bld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void bst32(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void bst64(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t a, uint32_t b) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{a, b}, r, off, 0, 0);
+}
+__device__ __forceinline__ void bst128(__amdgpu_buffer_rsrc_t r, uint32_t off, const uint4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, r, off, 0, 0);
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// The backward's products run in fp16: its LDS tiles hold fp16 bits (bf16
+// inputs convert exactly within fp16's range), and P, dS (|P| <= 1) keep 11
+// significant bits, where bf16 would keep 8.
+__device__ __forceinline__ f32x16 mfma32h(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+__device__ __forceinline__ f32x4v mfma16h(const bf16x8& a, const bf16x8& b, const f32x4v& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+// registers lo .. lo + 7 of an accumulator as an fp16x8 fragment (fp16 bits)
+__device__ __forceinline__ bf16x8 pack8h(const f32x16& acc, int lo) {
+  f16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[lo + e];
+  return __builtin_bit_cast(bf16x8, r);
+}
+// sum of the 8 fp16 values of a fragment into acc (v_dot2c_f32_f16 against 1.0)
+__device__ __forceinline__ float add_f16x8(const bf16x8& p, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  const uint4 u = __builtin_bit_cast(uint4, p);
+  float s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.x), one, acc, false);
+  float s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.y), one, 0.f, false);
+  s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.z), one, s0, false);
+  s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.w), one, s1, false);
+  return s0 + s1;
+}
+// 8 bf16 values (a 16-byte piece) to fp16 bits, saturated to +-65504 so an
+// out-of-range input stays finite
+__device__ __forceinline__ uint4 bf16x8_to_f16(const uint4& v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float a = fminf(fmaxf(__uint_as_float(w[u] << 16), -65504.f), 65504.f);
+    const float b = fminf(fmaxf(__uint_as_float(w[u] & 0xffff0000u), -65504.f), 65504.f);
+    const f16x2 h = {(_Float16)a, (_Float16)b};
+    o[u] = __builtin_bit_cast(uint32_t, h);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Bias (log2 domain) of a token on block e and whether any selection hits it;
@@ -80,7 +148,7 @@ __device__ __forceinline__ float pair_bias(int i0, int i1, float l0, float l1, i
 __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
-    bf16_t* __restrict__ out_lo, float* __restrict__ frac_a, float* __restrict__ lse,
+    float* __restrict__ frac_a, float* __restrict__ lse,
     const int32_t* __restrict__ plan, long N, int H, int L, int E, float alpha, int max_items) {
   constexpr int HD = kPHD, KS = HD / 16, NO = HD / 32, PITCH = kPPitch, NT = 256, NW = NT / 64;
   constexpr int PER = kPSlots * HD / 8 / NT;  // 16-byte pieces per thread per staged tensor
@@ -89,19 +157,24 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
 
   const PairPlanLayout pl = pair_plan_layout(N, E);
   const int32_t* ord = plan + 1;
-  const int wid = xcd_remap(blockIdx.x, H * max_items);  // head-major: a head's items share one L2
-  const int h = wid / max_items, it = wid % max_items;
-  // the item count and the item's words in one round trip (entries past the
-  // count are unwritten, but inside the plan's storage)
+  (void)max_items;
+  // Persistent workgroups: the (head, item) pairs, head-major, are dealt out
+  // in one contiguous share per XCD (the hardware deals workgroup i to XCD
+  // i % 8), so each L2 holds the K / V of about H / 8 heads; inside a share
+  // workgroup j takes items j, j + (workgroups of the XCD), ...
   const int n_fit = plan[pl.hdr + 2];
+  const int n_all = H * n_fit;
+  const int G = gridDim.x, xcd = blockIdx.x & 7, gw = G >> 3, lw = blockIdx.x >> 3;
+  const int f_beg = (int)((long)n_all * xcd / 8), f_end = (int)((long)n_all * (xcd + 1) / 8);
+  const int D = H * HD;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, col = lane & 31;
+  for (int f = f_beg + lw; f < f_end; f += gw) {
+  const int h = f / n_fit, it = f % n_fit;
   const int2 itw = *reinterpret_cast<const int2*>(plan + pl.fitems + 2 * it);
-  if (it >= n_fit) return;  // uniform over the workgroup
   const int pos0 = itw.x, ntok = pair_item_tokens(itw.y);
   const int ba = pair_item_a(itw.y), bb = pair_item_b(itw.y);
   const int nblk = ba == bb ? 1 : 2;
   const int nsl = (ntok + kPairTile - 1) / kPairTile;  // 32-position slices of the item
-  const int D = H * HD;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, col = lane & 31;
 
   // per-slice token state: this lane's token (column col of the slice), its
   // routing and q fragments (B operand: q[token][16 ks + 8 g ..])
@@ -117,31 +190,40 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
     ok = j < nsl && p < ntok;
     return (long)pos0 + p;
   };
+  const uint32_t nd_bytes = (uint32_t)(N * D * 2);
+  const __amdgpu_buffer_rsrc_t ord_rs = make_rsrc(ord, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(q, nd_bytes);
+  const __amdgpu_buffer_rsrc_t idx_rs = make_rsrc(top_idx, (uint32_t)N * 8u);
+  const __amdgpu_buffer_rsrc_t gate_rs = make_rsrc(top_gates, (uint32_t)N * 8u);
+  auto fetch_order = [&](bool ok, long pos) { return (long)(int)bld32(ord_rs, ok ? (uint32_t)pos * 4u : kOob); };
   auto fetch_data = [&](Slice& sc, long raw, long pos) {
     sc.tok = sc.ok ? ((raw >= 0 && raw < N) ? raw : pos) : 0;  // a malformed entry falls back to its position
-    sc.i0 = sc.i1 = -1;
-    sc.g0 = sc.g1 = 1.f;
-    if (sc.ok) {
-      sc.i0 = top_idx[2 * sc.tok];
-      sc.i1 = top_idx[2 * sc.tok + 1];
-      sc.g0 = top_gates[2 * sc.tok];
-      sc.g1 = top_gates[2 * sc.tok + 1];
-    }
+    const uint32_t ro = sc.ok ? (uint32_t)sc.tok * 8u : kOob;
+    const int i0v = (int)bld32(idx_rs, ro), i1v = (int)bld32(idx_rs, ro + 4u);
+    const float g0v = __uint_as_float(bld32(gate_rs, ro)), g1v = __uint_as_float(bld32(gate_rs, ro + 4u));
+    const uint32_t qo = sc.ok ? (uint32_t)((sc.tok * D + (long)h * HD + 8 * g) * 2) : kOob;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      sc.qf[ks] = sc.ok ? *reinterpret_cast<const bf16x8*>(q + sc.tok * D + (long)h * HD + 16 * ks + 8 * g)
-                        : bf16x8{};
+    for (int ks = 0; ks < KS; ++ks) sc.qf[ks] = __builtin_bit_cast(bf16x8, bld128(q_rs, qo + 32u * ks));
+    sc.i0 = sc.ok ? i0v : -1;
+    sc.i1 = sc.ok ? i1v : -1;
+    sc.g0 = sc.ok ? g0v : 1.f;
+    sc.g1 = sc.ok ? g1v : 1.f;
   };
 
   // ---- the wave's first slice: token and data issued ahead of the K / V staging
   Slice cur;
   {
     const long p = slice_pos(wave, cur.ok);
-    const long raw = cur.ok ? (long)ord[p] : 0;
-    fetch_data(cur, raw, p);
+    fetch_data(cur, fetch_order(cur.ok, p), p);
   }
 
+  const __amdgpu_buffer_rsrc_t out_rs = make_rsrc(out, nd_bytes);
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (long)h * N, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t fa_rs = make_rsrc(frac_a + (long)h * N, (uint32_t)N * 4u);
+
   // ---- K and V rows of the pair: slots 0..127 block a, 128..255 block b
+  // (every wave is done with the previous item's rows)
+  if (f != f_beg + lw) lds_barrier();
   {
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(k, (uint32_t)L * (uint32_t)D * 2u);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v, (uint32_t)L * (uint32_t)D * 2u);
@@ -169,7 +251,7 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
     // the next slice's order entry, in flight during this slice's block a
     Slice nxt;
     const long pn = slice_pos(j + NW, nxt.ok);
-    const long rawn = nxt.ok ? (long)ord[pn] : 0;
+    const long rawn = fetch_order(nxt.ok, pn);
 
     bool sa, sb;
     const float l0 = log2f(fmaxf(cur.g0, 1e-9f)), l1 = log2f(fmaxf(cur.g1, 1e-9f));
@@ -260,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
     // ---- epilogue: normalise; o, its bf16 remainder, lse and block a's share
     const float l = pair_sum(l_run);
     const float la_tot = pair_sum(la_run);
-    if (cur.ok) {
+    {
       const long tok = cur.tok;
       const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
@@ -269,26 +351,19 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
         f32x16 y;
 #pragma unroll
         for (int e = 0; e < 16; ++e) y[e] = o[jj][e] * inv;
-        bf16x8 hi0, hi1, lo0, lo1;
-        pack8_hilo(y, 0, hi0, lo0);
-        pack8_hilo(y, 8, hi1, lo1);
-        bf16_t* dst = out + tok * D + (long)h * HD + f0;
-        *reinterpret_cast<bf16x8*>(dst) = hi0;
-        *reinterpret_cast<bf16x8*>(dst + 8) = hi1;
-        if (out_lo != nullptr) {
-          bf16_t* dl = out_lo + tok * D + (long)h * HD + f0;
-          *reinterpret_cast<bf16x8*>(dl) = lo0;
-          *reinterpret_cast<bf16x8*>(dl + 8) = lo1;
-        }
+        const bf16x8 hi0 = pack8(y, 0), hi1 = pack8(y, 8);
+        const uint32_t oo = cur.ok ? (uint32_t)((tok * D + (long)h * HD + f0) * 2) : kOob;
+        bst128(out_rs, oo, __builtin_bit_cast(uint4, hi0));
+        bst128(out_rs, oo + 16u, __builtin_bit_cast(uint4, hi1));
       }
-      if (g == 0) {
-        lse[(long)h * N + tok] = m_run + log2f(l);
-        // the share of the row's weight on block a (1 for a one-block pair)
-        if (frac_a != nullptr) frac_a[(long)h * N + tok] = nblk == 1 ? 1.f : (l > 0.f ? la_tot / l : 0.f);
-      }
+      const uint32_t so = (cur.ok && g == 0) ? (uint32_t)tok * 4u : kOob;
+      bst32(lse_rs, so, __float_as_uint(m_run + log2f(l)));
+      // the share of the row's weight on block a (1 for a one-block pair)
+      if (frac_a != nullptr) bst32(fa_rs, so, __float_as_uint(nblk == 1 ? 1.f : (l > 0.f ? la_tot / l : 0.f)));
     }
     cur = nxt;
   }
+  }  // items
 }
 
 // ----------------------------------------------------------------- backward
@@ -297,7 +372,7 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
 __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
-    const bf16_t* __restrict__ o_lo, const float* __restrict__ frac_a, const bf16_t* __restrict__ dout,
+    const float* __restrict__ frac_a, const bf16_t* __restrict__ dout,
     const float* __restrict__ lse,
     const int32_t* __restrict__ plan, bf16_t* __restrict__ dq, float* __restrict__ dlg_part,
     float* __restrict__ dk_part, float* __restrict__ dv_part, long N, int H, int L, int E, float alpha,
@@ -313,8 +388,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   __shared__ float fa_lds[2][TQ];                                 // the forward's weight share of block a
   __shared__ __attribute__((aligned(16))) bf16_t kt_lds[kPSlots * PITCH];  // the pair's K rows
   __shared__ __attribute__((aligned(16))) bf16_t vt_lds[kPSlots * PITCH];  // the pair's V rows
-  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[kPSlots * DSP];    // dS^T of the tile: bf16(dS)
-  __shared__ __attribute__((aligned(16))) bf16_t dsl_lds[kPSlots * DSP];   // and bf16(dS - bf16(dS))
+  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[kPSlots * DSP];    // dS^T of the tile
   __shared__ float dl_lds[4][TQ];  // gate-gradient partials: (block a | b) x (slot half)
   __shared__ int2 tl_lds[kPairBwdMaxRange];  // the range's tile words (first position, count | blocks | pair)
 
@@ -336,24 +410,40 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   auto tile_w0 = [&](int t) { return tl_lds[t - i0].x; };
   auto tile_w1 = [&](int t) { return tl_lds[t - i0].y; };
 
-  // ---- tile staging: threads 0..255 hold dO, o, o_lo pieces (token row p >> 3,
-  // features 8 (p & 7) ..), threads 256..511 a Q piece; threads 0..31 the row's routing
-  const int sp = tid & 255, srow = sp >> 3, sc8 = sp & 7;
-  const bool s_do = tid < 256;
-  uint4 r_a = make_uint4(0, 0, 0, 0), r_o = r_a, r_ol = r_a;  // dO (or Q) / o / o_lo piece
-  int r_tok = -1, r_i0 = -1, r_i1 = -1;                         // threads 0..31: row tid
-  float r_g0 = 1.f, r_g1 = 1.f, r_lse = 0.f, r_fa = 1.f;
-  // order entries of the staged piece's row and (threads 0..31) of row tid,
-  // fetched a tile ahead of the loads that use them
-  int nx_raw = 0, nx_pos = -1, nr_raw = 0, nr_pos = -1;
-  auto fetch_tokens = [&](int t) {
-    const int pos0 = tile_w0(t), cnt = pair_tile_count(tile_w1(t));
-    nx_pos = srow < cnt ? pos0 + srow : -1;
-    if (nx_pos >= 0) nx_raw = ord[nx_pos];
-    if (tid < TQ) {
-      nr_pos = tid < cnt ? pos0 + tid : -1;
-      if (nr_pos >= 0) nr_raw = ord[nr_pos];
-    }
+  // ---- tile staging: waves 0..3 hold dO and o pieces (token row p >> 3,
+  // features 8 (p & 7) ..), waves 4..7 a Q piece; every thread the routing of
+  // row tid % 32 (threads 0..31 keep it)
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int sp = tid & 255, srow = sp >> 3, sc8 = sp & 7, rrow = tid & 31;
+  const bool s_do = wave_u < 4;  // wave-uniform
+  const uint32_t nd_bytes = (uint32_t)(N * D * 2);
+  const __amdgpu_buffer_rsrc_t ord_rs = make_rsrc(ord, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t a_rs = make_rsrc(s_do ? dout : q, nd_bytes);
+  const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(o, nd_bytes);
+  const __amdgpu_buffer_rsrc_t idx_rs = make_rsrc(top_idx, (uint32_t)N * 8u);
+  const __amdgpu_buffer_rsrc_t gate_rs = make_rsrc(top_gates, (uint32_t)N * 8u);
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (long)h * N, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t fa_rs = make_rsrc(frac_a + (long)h * N, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq, nd_bytes);
+  const __amdgpu_buffer_rsrc_t dlg_rs = make_rsrc(dlg_part + (long)h * N * 2, (uint32_t)N * 8u);
+  // Staging of one tile: order entries (of the staged piece's row and of row
+  // tid % 32), then its data: the dO (or Q) / o piece and the routing
+  // of row tid % 32.  Two sets of each rotate, so a tile's order entries are
+  // fetched three tiles and its data two tiles ahead of the tile's use.
+  struct TokSet {
+    int nx_pos, nx_raw, nr_pos, nr_raw;
+  };
+  struct DataSet {
+    uint4 a, o;
+    int tok, i0, i1;
+    float g0, g1, lse, fa;
+  };
+  auto fetch_tokens = [&](TokSet& ts, int t) {
+    const int pos0 = t < i1 ? tile_w0(t) : 0, cnt = t < i1 ? pair_tile_count(tile_w1(t)) : 0;
+    ts.nx_pos = srow < cnt ? pos0 + srow : -1;
+    ts.nr_pos = rrow < cnt ? pos0 + rrow : -1;
+    ts.nx_raw = (int)bld32(ord_rs, ts.nx_pos >= 0 ? (uint32_t)ts.nx_pos * 4u : kOob);
+    ts.nr_raw = (int)bld32(ord_rs, ts.nr_pos >= 0 ? (uint32_t)ts.nr_pos * 4u : kOob);
   };
   // a malformed order entry falls back to its position (wrong results, never
   // an access out of bounds)
@@ -361,51 +451,37 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     if (pos < 0) return -1;
     return (raw >= 0 && raw < N) ? (long)raw : (long)pos;
   };
-  auto load_tile = [&]() {
-    const long tk = token_of(nx_pos, nx_raw);
-    r_a = r_o = r_ol = make_uint4(0, 0, 0, 0);
-    if (tk >= 0) {
-      const long off = tk * D + (long)h * HD + 8 * sc8;
-      if (s_do) {
-        r_a = *reinterpret_cast<const uint4*>(dout + off);
-        r_o = *reinterpret_cast<const uint4*>(o + off);
-        r_ol = *reinterpret_cast<const uint4*>(o_lo + off);
-      } else {
-        r_a = *reinterpret_cast<const uint4*>(q + off);
-      }
-    }
-    if (tid < TQ) {
-      const long tr = token_of(nr_pos, nr_raw);
-      r_tok = (int)tr;
-      r_i0 = r_i1 = -1;
-      r_g0 = r_g1 = 1.f;
-      r_lse = 0.f;
-      r_fa = 1.f;
-      if (tr >= 0) {
-        r_i0 = top_idx[2 * tr];
-        r_i1 = top_idx[2 * tr + 1];
-        r_g0 = top_gates[2 * tr];
-        r_g1 = top_gates[2 * tr + 1];
-        r_lse = lse[(long)h * N + tr];
-        r_fa = frac_a[(long)h * N + tr];
-      }
-    }
+  auto load_tile = [&](DataSet& ds, const TokSet& ts) {
+    const long tk = token_of(ts.nx_pos, ts.nx_raw);
+    const uint32_t off = tk >= 0 ? (uint32_t)((tk * D + (long)h * HD + 8 * sc8) * 2) : kOob;
+    ds.a = bld128(a_rs, off);
+    ds.o = bld128(o_rs, s_do ? off : kOob);
+    const long tr = token_of(ts.nr_pos, ts.nr_raw);
+    ds.tok = (int)tr;
+    const uint32_t ro = tr >= 0 ? (uint32_t)tr * 8u : kOob, rl = tr >= 0 ? (uint32_t)tr * 4u : kOob;
+    ds.i0 = (int)bld32(idx_rs, ro);
+    ds.i1 = (int)bld32(idx_rs, ro + 4u);
+    ds.g0 = __uint_as_float(bld32(gate_rs, ro));
+    ds.g1 = __uint_as_float(bld32(gate_rs, ro + 4u));
+    ds.lse = __uint_as_float(bld32(lse_rs, rl));
+    ds.fa = __uint_as_float(bld32(fa_rs, rl));
   };
   // into buffer `buf`, for the pair (a, b): Q / dO rows, the per-row bias and
   // delta tables, tokens and selections
-  auto store_tile = [&](int buf, int a, int b) {
+  auto store_tile = [&](int buf, int a, int b, const DataSet& ds) {
     if (s_do) {
-      *reinterpret_cast<uint4*>(&do_lds[buf][srow * PITCH + 8 * sc8]) = r_a;
-      // delta = sum_f dO_f (o_f + o_lo_f) over the 8 features of the piece, then over the row's 8 threads
-      const uint32_t dw[4] = {r_a.x, r_a.y, r_a.z, r_a.w};
-      const uint32_t ow[4] = {r_o.x, r_o.y, r_o.z, r_o.w};
-      const uint32_t lw[4] = {r_ol.x, r_ol.y, r_ol.z, r_ol.w};
+      *reinterpret_cast<uint4*>(&do_lds[buf][srow * PITCH + 8 * sc8]) = bf16x8_to_f16(ds.a);
+      // delta = sum_f dO_f o_f over the 8 features of the piece, then over the
+      // row's 8 threads (o is the forward's bf16 output; its rounding moves
+      // the block sums of dS by (delta' - delta) M_x, which finish_gates
+      // removes, and dQ, dK by far less than their tolerance)
+      const uint32_t dw[4] = {ds.a.x, ds.a.y, ds.a.z, ds.a.w};
+      const uint32_t ow[4] = {ds.o.x, ds.o.y, ds.o.z, ds.o.w};
       float dsum = 0.f;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float d0 = __uint_as_float(dw[u] << 16), d1 = __uint_as_float(dw[u] & 0xffff0000u);
-        const float o0 = __uint_as_float(ow[u] << 16) + __uint_as_float(lw[u] << 16);
-        const float o1 = __uint_as_float(ow[u] & 0xffff0000u) + __uint_as_float(lw[u] & 0xffff0000u);
+        const float o0 = __uint_as_float(ow[u] << 16), o1 = __uint_as_float(ow[u] & 0xffff0000u);
         dsum = fmaf(d0, o0, dsum);
         dsum = fmaf(d1, o1, dsum);
       }
@@ -414,18 +490,20 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       dsum += dpp_f32<0x141>(dsum);
       if (sc8 == 0) ctab[buf][2][srow] = -dsum;
     } else {
-      *reinterpret_cast<uint4*>(&q_lds[buf][srow * PITCH + 8 * sc8]) = r_a;
+      *reinterpret_cast<uint4*>(&q_lds[buf][srow * PITCH + 8 * sc8]) = bf16x8_to_f16(ds.a);
     }
     if (tid < TQ) {
-      const float l0 = log2f(fmaxf(r_g0, 1e-9f)), l1 = log2f(fmaxf(r_g1, 1e-9f));
+      const bool ok = ds.tok >= 0;
+      const int i0v = ok ? ds.i0 : -1, i1v = ok ? ds.i1 : -1;
+      const float l0 = log2f(fmaxf(ok ? ds.g0 : 1.f, 1e-9f)), l1 = log2f(fmaxf(ok ? ds.g1 : 1.f, 1e-9f));
       bool sa, sb;
-      const float ca = pair_bias(r_i0, r_i1, l0, l1, a, sa);
-      const float cb = pair_bias(r_i0, r_i1, l0, l1, b, sb);
-      ctab[buf][0][tid] = sa ? ca - r_lse : -INFINITY;
-      ctab[buf][1][tid] = (sb && b != a) ? cb - r_lse : -INFINITY;
-      tok_lds[buf][tid] = r_tok;
-      fa_lds[buf][tid] = r_fa;
-      sel_lds[buf][tid] = (r_i0 == a ? 1 : 0) | (r_i1 == a ? 2 : 0) | (r_i0 == b ? 4 : 0) | (r_i1 == b ? 8 : 0);
+      const float ca = pair_bias(i0v, i1v, l0, l1, a, sa);
+      const float cb = pair_bias(i0v, i1v, l0, l1, b, sb);
+      ctab[buf][0][tid] = sa ? ca - ds.lse : -INFINITY;
+      ctab[buf][1][tid] = (sb && b != a) ? cb - ds.lse : -INFINITY;
+      tok_lds[buf][tid] = ds.tok;
+      fa_lds[buf][tid] = ok ? ds.fa : 1.f;
+      sel_lds[buf][tid] = (i0v == a ? 1 : 0) | (i1v == a ? 2 : 0) | (i0v == b ? 4 : 0) | (i1v == b ? 8 : 0);
     }
   };
 
@@ -436,7 +514,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   f32x16 acc_dk[NO], acc_dv[NO];
   const int w_slot = 32 * wave + col;  // this lane's slot in the pair (0..255)
   auto enter_pair = [&](int t) {
-    const int w1 = tile_w1(t);
+    const int w1 = __builtin_amdgcn_readfirstlane(tile_w1(t));
     key = pair_tile_key(w1);
     pa = pair_tile_a(w1);
     pb = pair_tile_b(w1);
@@ -448,8 +526,10 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       const int p = tid + NT * rr;
       const int row = p >> 3, c8 = p & 7;
       const long off = ((long)(row < kPBS ? pa : pb) * kPBS + (row & (kPBS - 1))) * D + (long)h * HD + 8 * c8;
-      *reinterpret_cast<uint4*>(&kt_lds[row * PITCH + 8 * c8]) = *reinterpret_cast<const uint4*>(k + off);
-      *reinterpret_cast<uint4*>(&vt_lds[row * PITCH + 8 * c8]) = *reinterpret_cast<const uint4*>(v + off);
+      *reinterpret_cast<uint4*>(&kt_lds[row * PITCH + 8 * c8]) =
+          bf16x8_to_f16(*reinterpret_cast<const uint4*>(k + off));
+      *reinterpret_cast<uint4*>(&vt_lds[row * PITCH + 8 * c8]) =
+          bf16x8_to_f16(*reinterpret_cast<const uint4*>(v + off));
     }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
@@ -492,37 +572,42 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   // the exact A_a - delta M_a.  M_a / S is the forward's share of the row
   // weight on block a (its error only scales that small residue).
   auto finish_gates = [&](int buf) {
-    if (tid < TQ) {
-      const int tk = tok_lds[buf][tid];
-      if (tk >= 0) {
-        const int sm = sel_lds[buf][tid];
-        const float fa = fa_lds[buf][tid];
-        const float g0 = dl_lds[0][tid] + dl_lds[1][tid];
-        const float g1 = dl_lds[2][tid] + dl_lds[3][tid];
-        const float tot = g0 + g1;
-        const float ga = g0 - fa * tot;
-        const float gb = g1 - (1.f - fa) * tot;
-        float* dst = dlg_part + ((long)h * N + tk) * 2;
-        dst[0] = (sm & 1) ? ga : ((sm & 4) ? gb : 0.f);
-        dst[1] = (sm & 2) ? ga : ((sm & 8) ? gb : 0.f);
-      }
-    }
+    // every thread computes row tid % 32; threads 0..31 store it
+    const int tk = tok_lds[buf][rrow];
+    const int sm = sel_lds[buf][rrow];
+    const float fa = fa_lds[buf][rrow];
+    const float g0 = dl_lds[0][rrow] + dl_lds[1][rrow];
+    const float g1 = dl_lds[2][rrow] + dl_lds[3][rrow];
+    const float tot = g0 + g1;
+    const float ga = g0 - fa * tot;
+    const float gb = g1 - (1.f - fa) * tot;
+    const float d0 = (sm & 1) ? ga : ((sm & 4) ? gb : 0.f);
+    const float d1 = (sm & 2) ? ga : ((sm & 8) ? gb : 0.f);
+    bst64(dlg_rs, (tid < TQ && tk >= 0) ? (uint32_t)tk * 8u : kOob, __float_as_uint(d0), __float_as_uint(d1));
   };
 
-  // ---- prologue: tile i0 staged, its pair entered, tile i0 + 1 in flight
+  // ---- prologue: tile i0 staged and its pair entered; the data of tiles
+  // i0 + 1, i0 + 2 and the order entries of tile i0 + 3 in flight.  Tile i
+  // uses LDS buffer (i - i0) & 1 and staging sets of that parity.
+  TokSet tks[2];
+  DataSet dts[2];
   enter_pair(i0);
-  fetch_tokens(i0);
-  load_tile();
-  store_tile(0, pa, pb);
-  if (i0 + 1 < i1) {
-    fetch_tokens(i0 + 1);
-    load_tile();
-  }
+  fetch_tokens(tks[0], i0);
+  load_tile(dts[0], tks[0]);
+  store_tile(0, pa, pb, dts[0]);
+  fetch_tokens(tks[1], i0 + 1);
+  fetch_tokens(tks[0], i0 + 2);
+  load_tile(dts[1], tks[1]);
+  load_tile(dts[0], tks[0]);
+  fetch_tokens(tks[1], i0 + 3);
   lds_barrier();
 
-  for (int i = i0; i < i1; ++i) {
-    const int buf = (i - i0) & 1;
-    if (i + 2 < i1) fetch_tokens(i + 2);
+  // one tile; P = (i - i0) & 1 as a compile-time constant (the loop below is
+  // unrolled by two), so the staging sets stay in registers
+  auto tile_step = [&](auto par, int i) {
+    constexpr int P = decltype(par)::value;
+    const int buf = P;
+    fetch_tokens(tks[P], i + 4);        // tks[P] was last read by tile i + 2's load
     if (i > i0) finish_gates(buf ^ 1);  // the previous tile's gate gradients (its partials are complete)
 
     // ---- S, dP - delta, P, dS for this wave's 32 slots x the tile's 32 tokens
@@ -543,8 +628,8 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
         const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[buf][off]);
         const bf16x8 bk = *reinterpret_cast<const bf16x8*>(&kt_lds[offk]);
         const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&vt_lds[offk]);
-        acc_s = mfma32(aq, bk, acc_s);
-        acc_p = mfma32(ad, bv, acc_p);
+        acc_s = mfma32h(aq, bk, acc_s);
+        acc_p = mfma32h(ad, bv, acc_p);
       }
       // registers 4 j4 .. 4 j4 + 3 are tokens 8 j4 + 4 g + 0..3
 #pragma unroll
@@ -558,37 +643,29 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
           acc_p[vv] = p * acc_p[vv];
         }
       }
-      // ---- dV^T += dO^T P (P as a bf16 hi + lo pair: dV sums P over many
-      // tokens), dK^T += Q^T dS; dS^T to LDS for dQ
+      // ---- dV^T += dO^T P, dK^T += Q^T dS (fp16 P, dS); dS^T to LDS for dQ
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        bf16x8 bp, bp_lo, bd, bd_lo;
-        pack8_hilo(acc_s, 8 * kk, bp, bp_lo);
-        pack8_hilo(acc_p, 8 * kk, bd, bd_lo);
+        const bf16x8 bp = pack8h(acc_s, 8 * kk), bd = pack8h(acc_p, 8 * kk);
 #pragma unroll
         for (int j = 0; j < NO; ++j) {
           const bf16x8 a_do = lds_frag_T<true, true>(do_lds[buf], PITCH, 16 * kk, 32 * j);
           const bf16x8 a_q = lds_frag_T<true, true>(q_lds[buf], PITCH, 16 * kk, 32 * j);
-          acc_dv[j] = mfma32(a_do, bp, acc_dv[j]);
-          acc_dv[j] = mfma32(a_do, bp_lo, acc_dv[j]);
-          acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
+          acc_dv[j] = mfma32h(a_do, bp, acc_dv[j]);
+          acc_dk[j] = mfma32h(a_q, bd, acc_dk[j]);
         }
         // registers 8 kk .. 8 kk + 7 are tokens 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3
         const uint4 u = __builtin_bit_cast(uint4, bd);
-        const uint4 ul = __builtin_bit_cast(uint4, bd_lo);
         const int dso = w_slot * DSP + 16 * kk + 4 * g;
         *reinterpret_cast<uint2*>(&ds_lds[dso]) = make_uint2(u.x, u.y);
         *reinterpret_cast<uint2*>(&ds_lds[dso + 8]) = make_uint2(u.z, u.w);
-        *reinterpret_cast<uint2*>(&dsl_lds[dso]) = make_uint2(ul.x, ul.y);
-        *reinterpret_cast<uint2*>(&dsl_lds[dso + 8]) = make_uint2(ul.z, ul.w);
       }
     }
     lds_barrier();  // dS^T of the tile complete
 
     // ---- dQ^T tile (features 16 (w & 3) .., tokens 16 (w >> 2) ..) over the
     // pair's slots, and the gate-gradient partials: wave with w & 3 == c sums
-    // dS (as its bf16 hi + lo pair: the block sums need fp32 accuracy) over
-    // K-steps 2c, 2c + 1 (block a for c < 2, b otherwise)
+    // dS over K-steps 2c, 2c + 1 (block a for c < 2, b otherwise)
     {
       const int tq = wave >> 2, fq = wave & 3;
       const int q4 = (lane >> 4) & 3, j = lane & 15;
@@ -601,16 +678,14 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
           // A: K^T (features 16 fq .., slots 32 kk ..); B: dS^T (slots, tokens 16 tq ..)
           const bf16x8 akt = frag16_T(kt_lds, PITCH, 32 * kk, 16 * fq);
           const bf16x8 bds = frag16_T(ds_lds, DSP, 32 * kk, 16 * tq);
-          accq = mfma16(akt, bds, accq);
+          accq = mfma16h(akt, bds, accq);
         }
       }
       if (2 * fq < nks) {
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           const int kk = 2 * fq + jj;
-          const bf16x8 bds = frag16_T(ds_lds, DSP, 32 * kk, 16 * tq);
-          const bf16x8 bdl = frag16_T(dsl_lds, DSP, 32 * kk, 16 * tq);
-          gsum = add_bf16x8(bdl, add_bf16x8(bds, gsum));
+          gsum = add_f16x8(frag16_T(ds_lds, DSP, 32 * kk, 16 * tq), gsum);
         }
       }
       // the four 16-lane groups hold different slots of the same token
@@ -619,31 +694,29 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       if (lane < 16) dl_lds[fq][16 * tq + lane] = gsum;
       // dQ rows: lane holds features 16 fq + 4 (l / 16) + 0..3 of token row 16 tq + l % 16
       const int tk = tok_lds[buf][16 * tq + j];
-      if (tk >= 0) {
-        uint2 pk;
-        pk.x = (uint32_t)f32_to_bf16(accq[0] * dq_scale) | ((uint32_t)f32_to_bf16(accq[1] * dq_scale) << 16);
-        pk.y = (uint32_t)f32_to_bf16(accq[2] * dq_scale) | ((uint32_t)f32_to_bf16(accq[3] * dq_scale) << 16);
-        *reinterpret_cast<uint2*>(dq + (long)tk * D + (long)h * HD + 16 * fq + 4 * q4) = pk;
-      }
+      const uint32_t px = (uint32_t)f32_to_bf16(accq[0] * dq_scale) | ((uint32_t)f32_to_bf16(accq[1] * dq_scale) << 16);
+      const uint32_t py = (uint32_t)f32_to_bf16(accq[2] * dq_scale) | ((uint32_t)f32_to_bf16(accq[3] * dq_scale) << 16);
+      bst64(dq_rs, tk >= 0 ? (uint32_t)(((long)tk * D + (long)h * HD + 16 * fq + 4 * q4) * 2) : kOob, px, py);
     }
 
     // ---- next tile: its pair (flush and reload on a change), staging, barrier
     if (i + 1 < i1) {
-      const int nkey = pair_tile_key(tile_w1(i + 1));
+      const int nkey = __builtin_amdgcn_readfirstlane(pair_tile_key(tile_w1(i + 1)));
       if (nkey != key) {
         // other waves may still read kt_lds in their dQ products: wait for
         // them before the next pair's rows overwrite it
         flush();
         lds_barrier();
         enter_pair(i + 1);
-        store_tile(buf ^ 1, pa, pb);
-        if (i + 2 < i1) load_tile();
-      } else {
-        store_tile(buf ^ 1, pa, pb);
-        if (i + 2 < i1) load_tile();
       }
+      store_tile(buf ^ 1, pa, pb, dts[P ^ 1]);  // tile i + 1
+      load_tile(dts[P ^ 1], tks[P ^ 1]);         // tile i + 3 (its order entries: fetched by tile i - 1)
     }
     lds_barrier();
+  };
+  for (int i = i0; i < i1; i += 2) {
+    tile_step(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < i1) tile_step(std::integral_constant<int, 1>{}, i + 1);
   }
   finish_gates((i1 - 1 - i0) & 1);
   flush();
@@ -745,8 +818,10 @@ __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
 
 // ------------------------------------------------------------------ host side
 bool read_pair_fwd_shapes(const ReadDims& d, long N) {
+  // (byte offsets of the token-indexed buffers and of K / V fit 31 bits)
   return d.HD == kPHD && d.block_size == kPBS && d.topk == 2 && d.E <= kPairMaxE &&
-         read_has_pair_plan(N, d.E, d.topk) && (long)d.L * d.H * d.HD * 2 < (1L << 31);
+         read_has_pair_plan(N, d.E, d.topk) && (long)d.L * d.H * d.HD * 2 < (1L << 31) &&
+         N * d.H * d.HD * 2 < (1L << 31);
 }
 bool read_pair_bwd_shapes(const ReadDims& d, long N) { return read_pair_fwd_shapes(d, N) && d.E <= kPairBwdMaxE; }
 bool read_pair_fwd_ok(const ReadDims& d, long N) { return d.order != nullptr && read_pair_fwd_shapes(d, N); }
@@ -772,29 +847,34 @@ size_t read_pair_part_bytes(const ReadDims& d) {
   return (size_t)d.H * read_pair_segments(d) * kPSlots * kPHD * sizeof(float);
 }
 
-size_t read_pair_side_bytes(const ReadDims& d) {
-  const size_t N = (size_t)d.B * d.S;
-  return ((N * d.H * d.HD * 2 + 255) & ~(size_t)255) + N * d.H * 4;
-}
+// the side buffer: each row's share of its weight on block a, (H, N) fp32
+size_t read_pair_side_bytes(const ReadDims& d) { return (size_t)d.B * d.S * d.H * 4; }
 
-// the side buffer: o's bf16 remainder (N, D), then block a's weight share (H, N)
-static bf16_t* side_out_lo(void* side) { return (bf16_t*)side; }
-static float* side_frac_a(void* side, const ReadDims& d) {
-  const size_t N = (size_t)d.B * d.S;
-  return (float*)((char*)side + ((N * d.H * d.HD * 2 + 255) & ~(size_t)255));
+// Compute units of the current device (cached per device; 256 on MI355X).
+static int pair_device_cus() {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int c = cached[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+  cached[dev].store(c, std::memory_order_relaxed);
+  return c;
 }
 
 hipError_t launch_read_fwd_pair(const void* q, const void* k, const void* v, const int32_t* top_idx,
                                 const float* top_gates, void* out, void* side, float* lse, const ReadDims& d,
                                 hipStream_t st) {
   const long N = (long)d.B * d.S;
-  const int mi = pair_fwd_max_items(N, d.E);
+  // two workgroups per CU (LDS: 72 KiB each), a multiple of the 8 XCDs, no
+  // more than the items can use
+  const long items = (long)d.H * pair_fwd_max_items(N, d.E);
+  const int mi = (int)std::max<long>(8, std::min<long>(2L * pair_device_cus(), (items + 7) / 8 * 8) / 8 * 8);
   const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;
-  bf16_t* olo = side ? side_out_lo(side) : nullptr;
-  float* fa = side ? side_frac_a(side, d) : nullptr;
+  float* fa = (float*)side;
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL(read_fwd_pair_kernel, dim3(d.H * mi), dim3(256), 0, st, (const bf16_t*)q,
-                                  (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates, (bf16_t*)out, olo, fa,
+               hipLaunchKernelGGL(read_fwd_pair_kernel, dim3(mi), dim3(256), 0, st, (const bf16_t*)q,
+                                  (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates, (bf16_t*)out, fa,
                                   lse, d.order, N, d.H, d.L, d.E, alpha, mi));
   return hipGetLastError();
 }
@@ -811,7 +891,7 @@ hipError_t launch_read_bwd_pair(const void* q, const void* k, const void* v, con
   NAYLIS_TIMED("read_bwd_pair", st,
                hipLaunchKernelGGL(read_bwd_pair_kernel, dim3(d.H * R), dim3(512), 0, st, (const bf16_t*)q,
                                   (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates, (const bf16_t*)o,
-                                  side_out_lo((void*)side), side_frac_a((void*)side, d), (const bf16_t*)dout, lse,
+                                  (const float*)side, (const bf16_t*)dout, lse,
                                   d.order, (bf16_t*)dq, dlg_part,
                                   dk_part, dv_part, N, d.H, d.L, d.E, alpha, scale, R, ns));
   const int kv_blocks = d.H * d.E * 4;

@@ -102,12 +102,12 @@ def test_read_null_pointers_and_workspace(lib):
 ])
 def test_read_side_bytes_rule(lib, dims, want):
     """naylis_mom_read_side_bytes > 0 exactly where the pair-tiled backward
-    applies: o's bf16 remainder (N x D bf16) and the block-a shares (H x N)."""
+    applies: the rows' block-a shares, (H, B, S) fp32."""
     nbytes = lib.naylis_mom_read_side_bytes(*dims)
     assert (nbytes > 0) == bool(want)
     if want:
-        B, S, H, hd = dims[:4]
-        assert nbytes == -(-B * S * H * hd * 2 // 256) * 256 + B * S * H * 4
+        B, S, H = dims[:3]
+        assert nbytes == B * S * H * 4
 
 
 def test_router_and_bank_reject_bad_arguments(lib):
