@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NAYLIS_MOM_ABI_VERSION 15
+#define NAYLIS_MOM_ABI_VERSION 16
 
 #define NAYLIS_OK 0
 #define NAYLIS_ERR_ARG 1       /* invalid shape / argument (the reference raises RuntimeError) */
@@ -65,16 +65,18 @@ const char* naylis_mom_last_error(void);
  *   out      (B, S, H, head_dim) bf16
  *   side     naylis_mom_read_side_bytes() bytes, or NULL: what the
  *                                          pair-tiled forward leaves for the
- *                                          pair-tiled backward (each row's
- *                                          share of its weight on the pair's
- *                                          first block, (H, B, S) fp32).  Used
+ *                                          pair-tiled backward, (H, B, S, 4)
+ *                                          32-bit words per row: its log2
+ *                                          bias minus lse on the pair's first
+ *                                          and second block (-inf: not
+ *                                          selected), its share of the row
+ *                                          weight on the first block, and
+ *                                          which selections hit which block
+ *                                          (bits 0-1: first, 2-3: second).  Used
  *                                          when side_bytes > 0 and a
  *                                          token_order is given; with NULL the
  *                                          backward takes the two-pass
- *                                          kernels.  Ignored otherwise.  The
- *                                          pair-tiled backward computes its
- *                                          products in fp16 (inputs beyond
- *                                          +-65504 saturate).
+ *                                          kernels.  Ignored otherwise.
  *   lse      (H, B, S) fp32                log2-domain log-sum-exp per row,
  *                                          saved for the backward
  *   token_order  int32 or NULL             the order in which the read walks

@@ -14,7 +14,7 @@ import threading
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libnaylis_mom.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 NAYLIS_OK = 0
 NAYLIS_ERR_ARG = 1

@@ -169,12 +169,17 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(JOBS jobs, int M, int N, in
   const int wm = (wave % C::WAVES_M) * 32 * C::TM, wn = (wave / C::WAVES_M) * 32 * C::TN;
 
   // buffer resources over each operand segment, based at this tile's first
-  // row (or column) and the segment's first k
-  auto rsrc = [&](const bf16_t* p, long ld, bool kc, int row0) {
-    return make_rsrc(kc ? p + (long)row0 * ld : p + row0, 0x7fffffff);
+  // row (or column) and the segment's first k, sized to the segment's last
+  // element: a stage's rows past the segment's k (a K that is not a multiple
+  // of kGK) load zeros instead of reading past the operand
+  auto rsrc = [&](const bf16_t* p, long ld, bool kc, int row0, int nrows, int kseg) {
+    const long ext = kc ? (long)(nrows - row0 - 1) * ld + kseg : (long)(kseg - 1) * ld + (nrows - row0);
+    return make_rsrc(kc ? p + (long)row0 * ld : p + row0, (uint32_t)(kseg > 0 && ext > 0 ? ext * 2 : 0));
   };
-  const __amdgpu_buffer_rsrc_t ra1 = rsrc(job.a.p1, job.a.ld, AKC, m0), ra2 = rsrc(job.a.p2, job.a.ld, AKC, m0);
-  const __amdgpu_buffer_rsrc_t rb1 = rsrc(job.b.p1, job.b.ld, BKC, n0), rb2 = rsrc(job.b.p2, job.b.ld, BKC, n0);
+  const __amdgpu_buffer_rsrc_t ra1 = rsrc(job.a.p1, job.a.ld, AKC, m0, M, K1),
+                               ra2 = rsrc(job.a.p2, job.a.ld, AKC, m0, M, K - K1);
+  const __amdgpu_buffer_rsrc_t rb1 = rsrc(job.b.p1, job.b.ld, BKC, n0, N, K1),
+                               rb2 = rsrc(job.b.p2, job.b.ld, BKC, n0, N, K - K1);
   // byte offset of k inside its segment
   auto koff = [&](int k, long ld, bool kc) { return (int)(kc ? (long)k * 2 : (long)k * ld * 2); };
 

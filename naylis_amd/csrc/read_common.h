@@ -32,13 +32,14 @@ __device__ __forceinline__ const int32_t* order_table(const int32_t* __restrict_
 //   keys   [max_keys][4] block a, block b (a <= b), first tile, tiles
 //   tiles  [max_tiles][2] first position, count | a << 6 | b << 11 | key << 16
 //   fitems [max_tiles][2] forward work items (up to kPairFwdItem consecutive
-//                         tiles of one key): first position,
-//                         tokens | a << 16 | b << 21
+//                         tiles of one key, one per forward wave): first
+//                         position, tokens | a << 16 | b << 21
 constexpr int kPairTile = 32;
-constexpr int kPairFwdItem = 8;
+constexpr int kPairFwdItem = 4;
 constexpr int kPairMaxE = 32;      // pair plan and pair-tiled forward
 constexpr int kPairBwdMaxE = 8;    // pair-tiled backward: its dK / dV partials grow with the pairs
 constexpr int kPairBwdMaxRange = 256;  // tiles per backward range (their plan words sit in LDS)
+constexpr int kPairFwdMaxRange = 256;  // work items per forward range (likewise)
 
 struct PairPlanLayout {
   long hdr, keys, tiles, fitems, words;

@@ -23,7 +23,9 @@
 //    += Q^T dS into the waves' register accumulators, dS^T through LDS into
 //    dQ^T = K^T dS^T (16 x 16 x 32 products, each wave one 16 x 16 tile over
 //    all 256 slots, so dQ is complete in the workgroup and written once) and
-//    the per-head gate gradients sum_{n in block} dS.  A range that crosses
+//    the per-head gate gradients sum_{n in block} dS (from dS as bf16 plus
+//    its bf16 remainder; the products themselves take bf16 operands, whose
+//    exponent range holds gradients of any scale).  A range that crosses
 //    from one pair to the next writes the pair's dK / dV sums as a partial
 //    (segment = range + pair index: unique per (range, pair)) and loads the
 //    next pair's rows.
@@ -74,50 +76,9 @@ __device__ __forceinline__ void bst128(__amdgpu_buffer_rsrc_t r, uint32_t off, c
   __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, r, off, 0, 0);
 }
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-// The backward's products run in fp16: its LDS tiles hold fp16 bits (bf16
-// inputs convert exactly within fp16's range), and P, dS (|P| <= 1) keep 11
-// significant bits, where bf16 would keep 8.
-__device__ __forceinline__ f32x16 mfma32h(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                0);
-}
-__device__ __forceinline__ f32x4v mfma16h(const bf16x8& a, const bf16x8& b, const f32x4v& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                0);
-}
-// registers lo .. lo + 7 of an accumulator as an fp16x8 fragment (fp16 bits)
-__device__ __forceinline__ bf16x8 pack8h(const f32x16& acc, int lo) {
-  f16x8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (_Float16)acc[lo + e];
-  return __builtin_bit_cast(bf16x8, r);
-}
-// sum of the 8 fp16 values of a fragment into acc (v_dot2c_f32_f16 against 1.0)
-__device__ __forceinline__ float add_f16x8(const bf16x8& p, float acc) {
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-  const uint4 u = __builtin_bit_cast(uint4, p);
-  float s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.x), one, acc, false);
-  float s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.y), one, 0.f, false);
-  s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.z), one, s0, false);
-  s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u.w), one, s1, false);
-  return s0 + s1;
-}
-// 8 bf16 values (a 16-byte piece) to fp16 bits, saturated to +-65504 so an
-// out-of-range input stays finite
-__device__ __forceinline__ uint4 bf16x8_to_f16(const uint4& v) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const float a = fminf(fmaxf(__uint_as_float(w[u] << 16), -65504.f), 65504.f);
-    const float b = fminf(fmaxf(__uint_as_float(w[u] & 0xffff0000u), -65504.f), 65504.f);
-    const f16x2 h = {(_Float16)a, (_Float16)b};
-    o[u] = __builtin_bit_cast(uint32_t, h);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+// 16 x 16 x 32 bf16 product (the backward's dQ^T tiles)
+__device__ __forceinline__ f32x4v mfma16(const bf16x8& a, const bf16x8& b, const f32x4v& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // Bias (log2 domain) of a token on block e and whether any selection hits it;
@@ -140,209 +101,220 @@ __device__ __forceinline__ float pair_bias(int i0, int i1, float l0, float l1, i
 }  // namespace
 
 // ------------------------------------------------------------------ forward
-// Workgroup (head h, forward item): the item's tiles are 32-position slices
-// of one pair's run of the order, wave w takes slices w, w + 4, ...  Each
-// wave fetches the next slice's tokens while it computes the current one
-// (order entry at the slice's start, routing and q after block a), so the
-// dependent loads of a slice overlap the previous slice's products.
+// Persistent workgroups of 4 waves over equal ranges of the head-major list
+// of (head, work item), an item being up to 4 consecutive tiles of one pair
+// (tile w for wave w): the 8 XCDs take one contiguous share each (the
+// hardware deals workgroup i to XCD i % 8, so an L2 holds the K / V and q
+// columns of about H / 8 heads) and workgroup j of an XCD a contiguous piece
+// of that share.  The pair's K / V rows are staged in LDS when the (head,
+// pair) changes from one item to the next; the waves then run through the
+// pair's items without synchronising.  Per tile (32 tokens; lane column =
+// token) a wave forms S^T = K Q^T for all of the pair's slots (eight 32-slot
+// chunks held in registers), takes each token's exact maximum m of alpha s +
+// c over its selected blocks, then P = exp2(alpha s + c - m) (<= 1: no
+// rescaling) with its bf16 row sums, and O^T += V^T P^T.  The wave's next
+// tile has its order entry in flight during the scores, its routing and q
+// during the weights.  The side table gets each row's backward constants
+// (c_a - lse, c_b - lse, block a's share of the row weight, which selections
+// hit a / b).
 __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, bf16_t* __restrict__ out,
-    float* __restrict__ frac_a, float* __restrict__ lse,
-    const int32_t* __restrict__ plan, long N, int H, int L, int E, float alpha, int max_items) {
-  constexpr int HD = kPHD, KS = HD / 16, NO = HD / 32, PITCH = kPPitch, NT = 256, NW = NT / 64;
+    float* __restrict__ rowtab, float* __restrict__ lse, const int32_t* __restrict__ plan, long N, int H, int L,
+    int E, float alpha) {
+  constexpr int HD = kPHD, KS = HD / 16, NO = HD / 32, PITCH = kPPitch, NT = 256;
+  constexpr int NC = kPSlots / 32;            // 32-slot chunks of a pair
   constexpr int PER = kPSlots * HD / 8 / NT;  // 16-byte pieces per thread per staged tensor
+  static_assert(NT / 64 == kPairFwdItem, "one wave per tile of an item");
   __shared__ __attribute__((aligned(16))) bf16_t k_lds[kPSlots * PITCH];
   __shared__ __attribute__((aligned(16))) bf16_t v_lds[kPSlots * PITCH];
+  __shared__ int2 tl_lds[kPairFwdMaxRange];  // the range's item words (first position, tokens | blocks)
 
   const PairPlanLayout pl = pair_plan_layout(N, E);
   const int32_t* ord = plan + 1;
-  (void)max_items;
-  // Persistent workgroups: the (head, item) pairs, head-major, are dealt out
-  // in one contiguous share per XCD (the hardware deals workgroup i to XCD
-  // i % 8), so each L2 holds the K / V of about H / 8 heads; inside a share
-  // workgroup j takes items j, j + (workgroups of the XCD), ...
+  const int32_t* fitems = plan + pl.fitems;
   const int n_fit = plan[pl.hdr + 2];
-  const int n_all = H * n_fit;
+  const long T = (long)H * n_fit;
   const int G = gridDim.x, xcd = blockIdx.x & 7, gw = G >> 3, lw = blockIdx.x >> 3;
-  const int f_beg = (int)((long)n_all * xcd / 8), f_end = (int)((long)n_all * (xcd + 1) / 8);
-  const int D = H * HD;
+  const long s0 = T * xcd / 8, sn = T * (xcd + 1) / 8 - s0;
+  const int u0 = (int)(s0 + sn * lw / gw);
+  // (the host sizes the grid so a range fits kPairFwdMaxRange)
+  const int u1 = (int)std::min<long>(s0 + sn * (lw + 1) / gw, (long)u0 + kPairFwdMaxRange);
+  if (u0 >= u1) return;  // uniform over the workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, col = lane & 31;
-  for (int f = f_beg + lw; f < f_end; f += gw) {
-  const int h = f / n_fit, it = f % n_fit;
-  const int2 itw = *reinterpret_cast<const int2*>(plan + pl.fitems + 2 * it);
-  const int pos0 = itw.x, ntok = pair_item_tokens(itw.y);
-  const int ba = pair_item_a(itw.y), bb = pair_item_b(itw.y);
-  const int nblk = ba == bb ? 1 : 2;
-  const int nsl = (ntok + kPairTile - 1) / kPairTile;  // 32-position slices of the item
+  const int D = H * HD;
+  for (int i = tid; i < u1 - u0; i += NT) {
+    const int it = (u0 + i) % n_fit;
+    tl_lds[i] = make_int2(fitems[2 * it], fitems[2 * it + 1]);
+  }
+  __syncthreads();
 
-  // per-slice token state: this lane's token (column col of the slice), its
-  // routing and q fragments (B operand: q[token][16 ks + 8 g ..])
-  struct Slice {
-    long tok;
-    bool ok;
-    int i0, i1;
-    float g0, g1;
-    bf16x8 qf[KS];
-  };
-  auto slice_pos = [&](int j, bool& ok) {
-    const int p = j * kPairTile + col;
-    ok = j < nsl && p < ntok;
-    return (long)pos0 + p;
-  };
   const uint32_t nd_bytes = (uint32_t)(N * D * 2);
   const __amdgpu_buffer_rsrc_t ord_rs = make_rsrc(ord, (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(q, nd_bytes);
   const __amdgpu_buffer_rsrc_t idx_rs = make_rsrc(top_idx, (uint32_t)N * 8u);
   const __amdgpu_buffer_rsrc_t gate_rs = make_rsrc(top_gates, (uint32_t)N * 8u);
-  auto fetch_order = [&](bool ok, long pos) { return (long)(int)bld32(ord_rs, ok ? (uint32_t)pos * 4u : kOob); };
-  auto fetch_data = [&](Slice& sc, long raw, long pos) {
-    sc.tok = sc.ok ? ((raw >= 0 && raw < N) ? raw : pos) : 0;  // a malformed entry falls back to its position
-    const uint32_t ro = sc.ok ? (uint32_t)sc.tok * 8u : kOob;
+  const __amdgpu_buffer_rsrc_t out_rs = make_rsrc(out, nd_bytes);
+  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse, (uint32_t)(N * H) * 4u);
+  const __amdgpu_buffer_rsrc_t row_rs = make_rsrc(rowtab, rowtab != nullptr ? (uint32_t)(N * H) * 16u : 0u);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(k, (uint32_t)L * (uint32_t)D * 2u);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v, (uint32_t)L * (uint32_t)D * 2u);
+
+  // A tile's token state for this lane (column col): its order entry (first
+  // stage), then the token's routing and q fragments (B operand:
+  // q[token][16 ks + 8 g ..]).  u = -1 / past the range: nothing.
+  struct TileIn {
+    int u;
+    bool ok;
+    int pos, raw;
+    long tok;
+    int i0, i1;
+    float g0, g1;
+    bf16x8 qf[KS];
+  };
+  auto stage_order = [&](TileIn& x, int u) {
+    x.u = u;
+    int pos0 = 0, cnt = 0;
+    if (u < u1) {
+      const int2 w = tl_lds[u - u0];
+      pos0 = w.x + kPairTile * wave;
+      cnt = pair_item_tokens(w.y) - kPairTile * wave;
+    }
+    x.ok = col < cnt;
+    x.pos = pos0 + col;
+    x.raw = (int)bld32(ord_rs, x.ok ? (uint32_t)x.pos * 4u : kOob);
+  };
+  auto stage_data = [&](TileIn& x) {
+    const int h = x.u < u1 ? x.u / n_fit : 0;
+    // a malformed order entry falls back to its position (wrong results, never
+    // an access out of bounds)
+    x.tok = x.ok ? ((x.raw >= 0 && x.raw < N) ? (long)x.raw : (long)x.pos) : 0;
+    const uint32_t ro = x.ok ? (uint32_t)x.tok * 8u : kOob;
     const int i0v = (int)bld32(idx_rs, ro), i1v = (int)bld32(idx_rs, ro + 4u);
     const float g0v = __uint_as_float(bld32(gate_rs, ro)), g1v = __uint_as_float(bld32(gate_rs, ro + 4u));
-    const uint32_t qo = sc.ok ? (uint32_t)((sc.tok * D + (long)h * HD + 8 * g) * 2) : kOob;
+    const uint32_t qo = x.ok ? (uint32_t)((x.tok * D + (long)h * HD + 8 * g) * 2) : kOob;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) sc.qf[ks] = __builtin_bit_cast(bf16x8, bld128(q_rs, qo + 32u * ks));
-    sc.i0 = sc.ok ? i0v : -1;
-    sc.i1 = sc.ok ? i1v : -1;
-    sc.g0 = sc.ok ? g0v : 1.f;
-    sc.g1 = sc.ok ? g1v : 1.f;
+    for (int ks = 0; ks < KS; ++ks) x.qf[ks] = __builtin_bit_cast(bf16x8, bld128(q_rs, qo + 32u * ks));
+    x.i0 = x.ok ? i0v : -1;
+    x.i1 = x.ok ? i1v : -1;
+    x.g0 = x.ok ? g0v : 1.f;
+    x.g1 = x.ok ? g1v : 1.f;
   };
 
-  // ---- the wave's first slice: token and data issued ahead of the K / V staging
-  Slice cur;
-  {
-    const long p = slice_pos(wave, cur.ok);
-    fetch_data(cur, fetch_order(cur.ok, p), p);
-  }
-
-  const __amdgpu_buffer_rsrc_t out_rs = make_rsrc(out, nd_bytes);
-  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (long)h * N, (uint32_t)N * 4u);
-  const __amdgpu_buffer_rsrc_t fa_rs = make_rsrc(frac_a + (long)h * N, (uint32_t)N * 4u);
-
-  // ---- K and V rows of the pair: slots 0..127 block a, 128..255 block b
-  // (every wave is done with the previous item's rows)
-  if (f != f_beg + lw) lds_barrier();
-  {
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(k, (uint32_t)L * (uint32_t)D * 2u);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(v, (uint32_t)L * (uint32_t)D * 2u);
-    uint4 kr[PER], vr[PER];
+  // this wave's tile of item u (cur), the order entry of its tile of item u
+  // + 1 (nxt: fetched a tile ahead), then its data (during item u)
+  TileIn cur, nxt;
+  stage_order(cur, u0);
+  stage_data(cur);
+  stage_order(nxt, u0 + 1);
+  int kv_h = -1, kv_a = -1, kv_b = -1;  // the (head, pair) whose rows are in LDS
+  for (int u = u0; u < u1; ++u) {
+    const int2 iw = tl_lds[u - u0];
+    const int h = u / n_fit, ba = pair_item_a(iw.y), bb = pair_item_b(iw.y);
+    const int nblk = ba == bb ? 1 : 2;
+    if (h != kv_h || ba != kv_a || bb != kv_b) {
+      // ---- K and V rows of the pair: slots 0..127 block a, 128..255 block
+      // b (every wave is done with the previous pair's rows)
+      if (u != u0) lds_barrier();
+      uint4 kr[PER], vr[PER];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int p = tid + NT * r;
-      const int row = p >> 3, c8 = p & 7;
-      const uint32_t slot = (uint32_t)((row < kPBS ? ba : bb) * kPBS + (row & (kPBS - 1)));
-      const uint32_t off = (slot * (uint32_t)D + (uint32_t)(h * HD + 8 * c8)) * 2u;
-      kr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
-      vr[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+      for (int r = 0; r < PER; ++r) {
+        const int p = tid + NT * r;
+        const int row = p >> 3, c8 = p & 7;
+        const uint32_t slot = (uint32_t)((row < kPBS ? ba : bb) * kPBS + (row & (kPBS - 1)));
+        const uint32_t off = (slot * (uint32_t)D + (uint32_t)(h * HD + 8 * c8)) * 2u;
+        kr[r] = bld128(krs, off);
+        vr[r] = bld128(vrs, off);
+      }
+#pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        const int p = tid + NT * r;
+        const int row = p >> 3, c8 = p & 7;
+        *reinterpret_cast<uint4*>(&k_lds[row * PITCH + 8 * c8]) = kr[r];
+        *reinterpret_cast<uint4*>(&v_lds[row * PITCH + 8 * c8]) = vr[r];
+      }
+      lds_barrier();
+      kv_h = h;
+      kv_a = ba;
+      kv_b = bb;
     }
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int p = tid + NT * r;
-      const int row = p >> 3, c8 = p & 7;
-      *reinterpret_cast<uint4*>(&k_lds[row * PITCH + 8 * c8]) = kr[r];
-      *reinterpret_cast<uint4*>(&v_lds[row * PITCH + 8 * c8]) = vr[r];
-    }
-  }
-  lds_barrier();
+    if (kPairTile * wave < pair_item_tokens(iw.y)) {
+      // (keeps the K fragment reads in the loop: hoisted, the 32 fragments
+      // would take 128 registers for the whole range)
+      asm volatile("" ::: "memory");
+      TileIn n2;  // the order entry of the tile of item u + 2
+      stage_order(n2, u + 2);
 
-  for (int j = wave; j < nsl; j += NW) {
-    // the next slice's order entry, in flight during this slice's block a
-    Slice nxt;
-    const long pn = slice_pos(j + NW, nxt.ok);
-    const long rawn = fetch_order(nxt.ok, pn);
+      bool sa, sb;
+      const float l0 = log2f(fmaxf(cur.g0, 1e-9f)), l1 = log2f(fmaxf(cur.g1, 1e-9f));
+      const float ca = pair_bias(cur.i0, cur.i1, l0, l1, ba, sa);
+      const float cbv = pair_bias(cur.i0, cur.i1, l0, l1, bb, sb);
+      sb = sb && nblk == 2;
 
-    bool sa, sb;
-    const float l0 = log2f(fmaxf(cur.g0, 1e-9f)), l1 = log2f(fmaxf(cur.g1, 1e-9f));
-    const float ca = pair_bias(cur.i0, cur.i1, l0, l1, ba, sa);
-    const float cbb = pair_bias(cur.i0, cur.i1, l0, l1, bb, sb);
-
-    f32x16 o[NO];
+      // ---- S^T chunks (slots 32 c .., tokens): registers 4 j4 .. 4 j4 + 3
+      // are slots 8 j4 + 4 g + 0..3 of the chunk.  Chunk c's products are
+      // issued beside chunk c - 1's maximum (VALU next to MFMA).
+      f32x16 x[NC];
+      float mxa = -INFINITY, mxb = -INFINITY;  // the lane's maxima over blocks a, b (alpha > 0)
 #pragma unroll
-    for (int jj = 0; jj < NO; ++jj) o[jj] = f32x16{};
-    float m_run = kNegBig, l_run = 0.f;
-    float la_run = 0.f;  // the row sum over block a's chunks, rescaled with l_run
-
-    auto qk = [&](int c, f32x16& x) {
-      x = f32x16{};
+      for (int c = 0; c <= NC; ++c) {
+        if (c < NC) {
+          x[c] = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * c + col) * PITCH + 16 * ks + 8 * g]);
-        x = mfma32(a, cur.qf[ks], x);
-      }
-    };
-    // softmax of chunk c's scores (bias cb, selected sl) into bf16 weights,
-    // with the lazy reference of read_fwd.hip: set from one score of the
-    // token's first selected chunk, moved only when a chunk gives some
-    // p > 2^64 (then the chunk is recomputed against its maximum)
-    auto softmax = [&](int c, float cb, bool sl, f32x16& x, bf16x8 (&pk)[2]) {
-      if (__any(sl && m_run == kNegBig)) {
-        const float ref = fmaf(pair_max(x[0]), alpha, cb);
-        if (sl && m_run == kNegBig) m_run = ref;
-      }
-      float add = sl ? cb - m_run : -INFINITY;
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
-      pk[0] = pack8(x, 0);
-      pk[1] = pack8(x, 8);
-      float part = add_bf16x8(pk[1], add_bf16x8(pk[0], 0.f));
-      const bool big = !(pair_max(part) <= 0x1p64f);
-      if (__any(sl && big)) {
-        qk(c, x);
-        const float cand = fmaf(pair_max(max16(x)), alpha, cb);
-        if (sl && big) {
-          const float cr = __builtin_amdgcn_exp2f(m_run - cand);
-#pragma unroll
-          for (int jj = 0; jj < NO; ++jj)
-#pragma unroll
-            for (int vv = 0; vv < 16; ++vv) o[jj][vv] *= cr;
-          l_run *= cr;
-          la_run *= cr;
-          m_run = cand;
+          for (int ks = 0; ks < KS; ++ks) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&k_lds[(32 * c + col) * PITCH + 16 * ks + 8 * g]);
+            x[c] = mfma32(a, cur.qf[ks], x[c]);
+          }
         }
-        add = sl ? cb - m_run : -INFINITY;
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) x[vv] = __builtin_amdgcn_exp2f(fmaf(x[vv], alpha, add));
-        pk[0] = pack8(x, 0);
-        pk[1] = pack8(x, 8);
-        part = add_bf16x8(pk[1], add_bf16x8(pk[0], 0.f));
-      }
-      l_run += part;
-    };
-    auto pv = [&](int c, const bf16x8 (&pk)[2]) {
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int jj = 0; jj < NO; ++jj) {
-          const bf16x8 a = lds_frag_T<true, true>(v_lds, PITCH, 32 * c + 16 * kk, 32 * jj);
-          o[jj] = mfma32(a, pk[kk], o[jj]);
+        if (c > 0) {
+          const float mc = max16(x[c - 1]);
+          if (c - 1 < NC / 2) mxa = fmaxf(mxa, mc);
+          else mxb = fmaxf(mxb, mc);
         }
-    };
-    auto block = [&](int bi) {
-      const float cb = bi ? cbb : ca;
-      const bool sl = bi ? sb : sa;
-#pragma unroll
-      for (int cc = 0; cc < kPBS / 32; ++cc) {
-        const int c = bi * (kPBS / 32) + cc;
-        f32x16 x;
-        bf16x8 pk[2];
-        qk(c, x);
-        softmax(c, cb, sl, x, pk);
-        pv(c, pk);
       }
-    };
+      // the next tile's routing and q, in flight during the weights
+      stage_data(nxt);
 
-    block(0);
-    la_run = l_run;
-    // the next slice's routing and q, in flight during block b and the epilogue
-    fetch_data(nxt, rawn, pn);
-    if (nblk == 2) block(1);
+      // ---- the token's maximum over its selected blocks
+      mxa = pair_max(mxa);
+      mxb = pair_max(mxb);
+      const float m = fmaxf(sa ? fmaf(mxa, alpha, ca) : -INFINITY, sb ? fmaf(mxb, alpha, cbv) : -INFINITY);
+      const float ms = m == -INFINITY ? 0.f : m;  // no selected block: every weight is 0
+      const float adda = sa ? ca - ms : -INFINITY, addb = sb ? cbv - ms : -INFINITY;
 
-    // ---- epilogue: normalise; o, its bf16 remainder, lse and block a's share
-    const float l = pair_sum(l_run);
-    const float la_tot = pair_sum(la_run);
-    {
+      // ---- P (bf16) and its row sums; O^T += V^T P^T, chunk c - 1's
+      // products issued beside chunk c's weights
+      f32x16 o[NO];
+#pragma unroll
+      for (int jj = 0; jj < NO; ++jj) o[jj] = f32x16{};
+      float l_run = 0.f, la_run = 0.f;
+      bf16x8 pk[2][2];
+#pragma unroll
+      for (int c = 0; c <= NC; ++c) {
+        if (c < NC) {
+          const float add = c < NC / 2 ? adda : addb;
+          f32x16 p;
+#pragma unroll
+          for (int vv = 0; vv < 16; ++vv) p[vv] = __builtin_amdgcn_exp2f(fmaf(x[c][vv], alpha, add));
+          pk[c & 1][0] = pack8(p, 0);
+          pk[c & 1][1] = pack8(p, 8);
+          l_run += add_bf16x8(pk[c & 1][1], add_bf16x8(pk[c & 1][0], 0.f));
+          if (c == NC / 2 - 1) la_run = l_run;
+        }
+        if (c > 0) {
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int jj = 0; jj < NO; ++jj) {
+              const bf16x8 a = lds_frag_T<true, true>(v_lds, PITCH, 32 * (c - 1) + 16 * kk, 32 * jj);
+              o[jj] = mfma32(a, pk[(c - 1) & 1][kk], o[jj]);
+            }
+        }
+      }
+
+      // ---- epilogue: o, lse and the row's backward constants
+      const float l = pair_sum(l_run);
+      const float la = pair_sum(la_run);
       const long tok = cur.tok;
       const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
@@ -356,14 +328,26 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
         bst128(out_rs, oo, __builtin_bit_cast(uint4, hi0));
         bst128(out_rs, oo + 16u, __builtin_bit_cast(uint4, hi1));
       }
-      const uint32_t so = (cur.ok && g == 0) ? (uint32_t)tok * 4u : kOob;
-      bst32(lse_rs, so, __float_as_uint(m_run + log2f(l)));
-      // the share of the row's weight on block a (1 for a one-block pair)
-      if (frac_a != nullptr) bst32(fa_rs, so, __float_as_uint(nblk == 1 ? 1.f : (l > 0.f ? la_tot / l : 0.f)));
+      const float lse_v = ms + log2f(l);  // -inf for a row with no selected block
+      const bool rw = cur.ok && g == 0;
+      bst32(lse_rs, rw ? (uint32_t)((long)h * N + tok) * 4u : kOob, __float_as_uint(lse_v));
+      if (rowtab != nullptr) {
+        const float fa = nblk == 1 ? 1.f : (l > 0.f ? la / l : 0.f);
+        const uint32_t sel = (cur.i0 == ba ? 1u : 0u) | (cur.i1 == ba ? 2u : 0u) | (cur.i0 == bb ? 4u : 0u) |
+                             (cur.i1 == bb ? 8u : 0u);
+        const uint4 row = make_uint4(__float_as_uint(sa ? ca - lse_v : -INFINITY),
+                                     __float_as_uint(sb ? cbv - lse_v : -INFINITY), __float_as_uint(fa), sel);
+        bst128(row_rs, rw ? (uint32_t)((long)h * N + tok) * 16u : kOob, row);
+      }
+      cur = nxt;
+      nxt = n2;
+    } else {
+      // no tile of this wave in item u: move the pipeline on
+      cur = nxt;
+      stage_data(cur);
+      stage_order(nxt, u + 2);
     }
-    cur = nxt;
   }
-  }  // items
 }
 
 // ----------------------------------------------------------------- backward
@@ -371,9 +355,7 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
 // 32 w .. 32 w + 31 of the current pair (w < 4: block a, else block b).
 __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const int32_t* __restrict__ top_idx, const float* __restrict__ top_gates, const bf16_t* __restrict__ o,
-    const float* __restrict__ frac_a, const bf16_t* __restrict__ dout,
-    const float* __restrict__ lse,
+    const bf16_t* __restrict__ o, const float* __restrict__ rowtab, const bf16_t* __restrict__ dout,
     const int32_t* __restrict__ plan, bf16_t* __restrict__ dq, float* __restrict__ dlg_part,
     float* __restrict__ dk_part, float* __restrict__ dv_part, long N, int H, int L, int E, float alpha,
     float dq_scale, int R, int n_seg) {
@@ -387,8 +369,8 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   __shared__ int32_t sel_lds[2][TQ];                              // which selections hit a (bit 0,1) / b (bit 2,3)
   __shared__ float fa_lds[2][TQ];                                 // the forward's weight share of block a
   __shared__ __attribute__((aligned(16))) bf16_t kt_lds[kPSlots * PITCH];  // the pair's K rows
-  __shared__ __attribute__((aligned(16))) bf16_t vt_lds[kPSlots * PITCH];  // the pair's V rows
-  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[kPSlots * DSP];    // dS^T of the tile
+  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[kPSlots * DSP];    // dS^T of the tile (bf16)
+  __shared__ __attribute__((aligned(16))) bf16_t dsl_lds[kPSlots * DSP];   // and its bf16 remainder
   __shared__ float dl_lds[4][TQ];  // gate-gradient partials: (block a | b) x (slot half)
   __shared__ int2 tl_lds[kPairBwdMaxRange];  // the range's tile words (first position, count | blocks | pair)
 
@@ -420,10 +402,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   const __amdgpu_buffer_rsrc_t ord_rs = make_rsrc(ord, (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t a_rs = make_rsrc(s_do ? dout : q, nd_bytes);
   const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(o, nd_bytes);
-  const __amdgpu_buffer_rsrc_t idx_rs = make_rsrc(top_idx, (uint32_t)N * 8u);
-  const __amdgpu_buffer_rsrc_t gate_rs = make_rsrc(top_gates, (uint32_t)N * 8u);
-  const __amdgpu_buffer_rsrc_t lse_rs = make_rsrc(lse + (long)h * N, (uint32_t)N * 4u);
-  const __amdgpu_buffer_rsrc_t fa_rs = make_rsrc(frac_a + (long)h * N, (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t row_rs = make_rsrc(rowtab + (long)h * N * 4, (uint32_t)N * 16u);
   const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq, nd_bytes);
   const __amdgpu_buffer_rsrc_t dlg_rs = make_rsrc(dlg_part + (long)h * N * 2, (uint32_t)N * 8u);
   // Staging of one tile: order entries (of the staged piece's row and of row
@@ -434,9 +413,8 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     int nx_pos, nx_raw, nr_pos, nr_raw;
   };
   struct DataSet {
-    uint4 a, o;
-    int tok, i0, i1;
-    float g0, g1, lse, fa;
+    uint4 a, o, row;
+    int tok;
   };
   auto fetch_tokens = [&](TokSet& ts, int t) {
     const int pos0 = t < i1 ? tile_w0(t) : 0, cnt = t < i1 ? pair_tile_count(tile_w1(t)) : 0;
@@ -458,19 +436,13 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     ds.o = bld128(o_rs, s_do ? off : kOob);
     const long tr = token_of(ts.nr_pos, ts.nr_raw);
     ds.tok = (int)tr;
-    const uint32_t ro = tr >= 0 ? (uint32_t)tr * 8u : kOob, rl = tr >= 0 ? (uint32_t)tr * 4u : kOob;
-    ds.i0 = (int)bld32(idx_rs, ro);
-    ds.i1 = (int)bld32(idx_rs, ro + 4u);
-    ds.g0 = __uint_as_float(bld32(gate_rs, ro));
-    ds.g1 = __uint_as_float(bld32(gate_rs, ro + 4u));
-    ds.lse = __uint_as_float(bld32(lse_rs, rl));
-    ds.fa = __uint_as_float(bld32(fa_rs, rl));
+    ds.row = bld128(row_rs, tr >= 0 ? (uint32_t)tr * 16u : kOob);
   };
-  // into buffer `buf`, for the pair (a, b): Q / dO rows, the per-row bias and
-  // delta tables, tokens and selections
-  auto store_tile = [&](int buf, int a, int b, const DataSet& ds) {
+  // into buffer `buf`: Q / dO rows, the per-row bias and delta tables (the
+  // forward's row constants), tokens and selections
+  auto store_tile = [&](int buf, const DataSet& ds) {
     if (s_do) {
-      *reinterpret_cast<uint4*>(&do_lds[buf][srow * PITCH + 8 * sc8]) = bf16x8_to_f16(ds.a);
+      *reinterpret_cast<uint4*>(&do_lds[buf][srow * PITCH + 8 * sc8]) = ds.a;
       // delta = sum_f dO_f o_f over the 8 features of the piece, then over the
       // row's 8 threads (o is the forward's bf16 output; its rounding moves
       // the block sums of dS by (delta' - delta) M_x, which finish_gates
@@ -490,28 +462,25 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       dsum += dpp_f32<0x141>(dsum);
       if (sc8 == 0) ctab[buf][2][srow] = -dsum;
     } else {
-      *reinterpret_cast<uint4*>(&q_lds[buf][srow * PITCH + 8 * sc8]) = bf16x8_to_f16(ds.a);
+      *reinterpret_cast<uint4*>(&q_lds[buf][srow * PITCH + 8 * sc8]) = ds.a;
     }
     if (tid < TQ) {
       const bool ok = ds.tok >= 0;
-      const int i0v = ok ? ds.i0 : -1, i1v = ok ? ds.i1 : -1;
-      const float l0 = log2f(fmaxf(ok ? ds.g0 : 1.f, 1e-9f)), l1 = log2f(fmaxf(ok ? ds.g1 : 1.f, 1e-9f));
-      bool sa, sb;
-      const float ca = pair_bias(i0v, i1v, l0, l1, a, sa);
-      const float cb = pair_bias(i0v, i1v, l0, l1, b, sb);
-      ctab[buf][0][tid] = sa ? ca - ds.lse : -INFINITY;
-      ctab[buf][1][tid] = (sb && b != a) ? cb - ds.lse : -INFINITY;
+      ctab[buf][0][tid] = ok ? __uint_as_float(ds.row.x) : -INFINITY;
+      ctab[buf][1][tid] = ok ? __uint_as_float(ds.row.y) : -INFINITY;
       tok_lds[buf][tid] = ds.tok;
-      fa_lds[buf][tid] = ok ? ds.fa : 1.f;
-      sel_lds[buf][tid] = (i0v == a ? 1 : 0) | (i1v == a ? 2 : 0) | (i0v == b ? 4 : 0) | (i1v == b ? 8 : 0);
+      fa_lds[buf][tid] = ok ? __uint_as_float(ds.row.z) : 1.f;
+      sel_lds[buf][tid] = ok ? (int)ds.row.w : 0;
     }
   };
 
-  // ---- the current pair: its K and V rows in LDS (B operands of S and dP:
-  // lane = slot; and the dQ product's K^T fragments), the dK / dV accumulators
+  // ---- the current pair: its K rows in LDS (the dQ product's K^T
+  // fragments), this lane's K and V slot rows in registers (B operands of S
+  // and dP: lane = slot), the dK / dV accumulators
   int key = -1, pa = 0, pb = 0, nblk = 2;
   bool w_on = true;
   f32x16 acc_dk[NO], acc_dv[NO];
+  bf16x8 kf[KS], vf[KS];  // this lane's slot row of K and V: B operands of S and dP
   const int w_slot = 32 * wave + col;  // this lane's slot in the pair (0..255)
   auto enter_pair = [&](int t) {
     const int w1 = __builtin_amdgcn_readfirstlane(tile_w1(t));
@@ -526,10 +495,16 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       const int p = tid + NT * rr;
       const int row = p >> 3, c8 = p & 7;
       const long off = ((long)(row < kPBS ? pa : pb) * kPBS + (row & (kPBS - 1))) * D + (long)h * HD + 8 * c8;
-      *reinterpret_cast<uint4*>(&kt_lds[row * PITCH + 8 * c8]) =
-          bf16x8_to_f16(*reinterpret_cast<const uint4*>(k + off));
-      *reinterpret_cast<uint4*>(&vt_lds[row * PITCH + 8 * c8]) =
-          bf16x8_to_f16(*reinterpret_cast<const uint4*>(v + off));
+      *reinterpret_cast<uint4*>(&kt_lds[row * PITCH + 8 * c8]) = *reinterpret_cast<const uint4*>(k + off);
+    }
+    {
+      const long srow_g = (long)(w_slot < kPBS ? pa : pb) * kPBS + (w_slot & (kPBS - 1));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const long off = srow_g * D + (long)h * HD + 16 * ks + 8 * g;
+        kf[ks] = *reinterpret_cast<const bf16x8*>(k + off);
+        vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
+      }
     }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
@@ -594,7 +569,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   enter_pair(i0);
   fetch_tokens(tks[0], i0);
   load_tile(dts[0], tks[0]);
-  store_tile(0, pa, pb, dts[0]);
+  store_tile(0, dts[0]);
   fetch_tokens(tks[1], i0 + 1);
   fetch_tokens(tks[0], i0 + 2);
   load_tile(dts[1], tks[1]);
@@ -623,13 +598,10 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int off = col * PITCH + 16 * ks + 8 * g;
-        const int offk = w_slot * PITCH + 16 * ks + 8 * g;
         const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[buf][off]);
         const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[buf][off]);
-        const bf16x8 bk = *reinterpret_cast<const bf16x8*>(&kt_lds[offk]);
-        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&vt_lds[offk]);
-        acc_s = mfma32h(aq, bk, acc_s);
-        acc_p = mfma32h(ad, bv, acc_p);
+        acc_s = mfma32(aq, kf[ks], acc_s);
+        acc_p = mfma32(ad, vf[ks], acc_p);
       }
       // registers 4 j4 .. 4 j4 + 3 are tokens 8 j4 + 4 g + 0..3
 #pragma unroll
@@ -643,22 +615,29 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
           acc_p[vv] = p * acc_p[vv];
         }
       }
-      // ---- dV^T += dO^T P, dK^T += Q^T dS (fp16 P, dS); dS^T to LDS for dQ
+      // ---- dV^T += dO^T P, dK^T += Q^T dS, each weight as bf16 plus its
+      // bf16 remainder (two products: ~2^-16 relative, where bf16 alone
+      // leaves 2^-9 per term in sums over thousands of tokens); dS^T (both
+      // parts) to LDS for dQ and the gate sums
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 bp = pack8h(acc_s, 8 * kk), bd = pack8h(acc_p, 8 * kk);
+        bf16x8 bp, bpl, bd, bdl;
+        pack8_hilo(acc_s, 8 * kk, bp, bpl);
+        pack8_hilo(acc_p, 8 * kk, bd, bdl);
 #pragma unroll
         for (int j = 0; j < NO; ++j) {
           const bf16x8 a_do = lds_frag_T<true, true>(do_lds[buf], PITCH, 16 * kk, 32 * j);
           const bf16x8 a_q = lds_frag_T<true, true>(q_lds[buf], PITCH, 16 * kk, 32 * j);
-          acc_dv[j] = mfma32h(a_do, bp, acc_dv[j]);
-          acc_dk[j] = mfma32h(a_q, bd, acc_dk[j]);
+          acc_dv[j] = mfma32(a_do, bpl, mfma32(a_do, bp, acc_dv[j]));
+          acc_dk[j] = mfma32(a_q, bdl, mfma32(a_q, bd, acc_dk[j]));
         }
         // registers 8 kk .. 8 kk + 7 are tokens 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3
-        const uint4 u = __builtin_bit_cast(uint4, bd);
+        const uint4 u = __builtin_bit_cast(uint4, bd), ul = __builtin_bit_cast(uint4, bdl);
         const int dso = w_slot * DSP + 16 * kk + 4 * g;
         *reinterpret_cast<uint2*>(&ds_lds[dso]) = make_uint2(u.x, u.y);
         *reinterpret_cast<uint2*>(&ds_lds[dso + 8]) = make_uint2(u.z, u.w);
+        *reinterpret_cast<uint2*>(&dsl_lds[dso]) = make_uint2(ul.x, ul.y);
+        *reinterpret_cast<uint2*>(&dsl_lds[dso + 8]) = make_uint2(ul.z, ul.w);
       }
     }
     lds_barrier();  // dS^T of the tile complete
@@ -678,14 +657,15 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
           // A: K^T (features 16 fq .., slots 32 kk ..); B: dS^T (slots, tokens 16 tq ..)
           const bf16x8 akt = frag16_T(kt_lds, PITCH, 32 * kk, 16 * fq);
           const bf16x8 bds = frag16_T(ds_lds, DSP, 32 * kk, 16 * tq);
-          accq = mfma16h(akt, bds, accq);
+          accq = mfma16(akt, bds, accq);
         }
       }
       if (2 * fq < nks) {
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           const int kk = 2 * fq + jj;
-          gsum = add_f16x8(frag16_T(ds_lds, DSP, 32 * kk, 16 * tq), gsum);
+          gsum = add_bf16x8(frag16_T(ds_lds, DSP, 32 * kk, 16 * tq), gsum);
+          gsum = add_bf16x8(frag16_T(dsl_lds, DSP, 32 * kk, 16 * tq), gsum);
         }
       }
       // the four 16-lane groups hold different slots of the same token
@@ -709,7 +689,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
         lds_barrier();
         enter_pair(i + 1);
       }
-      store_tile(buf ^ 1, pa, pb, dts[P ^ 1]);  // tile i + 1
+      store_tile(buf ^ 1, dts[P ^ 1]);  // tile i + 1
       load_tile(dts[P ^ 1], tks[P ^ 1]);         // tile i + 3 (its order entries: fetched by tile i - 1)
     }
     lds_barrier();
@@ -827,8 +807,6 @@ bool read_pair_bwd_shapes(const ReadDims& d, long N) { return read_pair_fwd_shap
 bool read_pair_fwd_ok(const ReadDims& d, long N) { return d.order != nullptr && read_pair_fwd_shapes(d, N); }
 bool read_pair_bwd_ok(const ReadDims& d, long N) { return d.order != nullptr && read_pair_bwd_shapes(d, N); }
 
-static int pair_fwd_max_items(long N, int E) { return pair_plan_layout(N, E).max_tiles; }
-
 int read_pair_ranges(const ReadDims& d) {
   const long N = (long)d.B * d.S;
   const int want = d.H >= 256 ? 1 : 256 / d.H;  // one round of workgroups
@@ -847,8 +825,9 @@ size_t read_pair_part_bytes(const ReadDims& d) {
   return (size_t)d.H * read_pair_segments(d) * kPSlots * kPHD * sizeof(float);
 }
 
-// the side buffer: each row's share of its weight on block a, (H, N) fp32
-size_t read_pair_side_bytes(const ReadDims& d) { return (size_t)d.B * d.S * d.H * 4; }
+// the side buffer: each row's backward constants, (H, N, 4) 32-bit words
+// (c_a - lse, c_b - lse, block a's share of the row weight, selection bits)
+size_t read_pair_side_bytes(const ReadDims& d) { return (size_t)d.B * d.S * d.H * 16; }
 
 // Compute units of the current device (cached per device; 256 on MI355X).
 static int pair_device_cus() {
@@ -866,16 +845,18 @@ hipError_t launch_read_fwd_pair(const void* q, const void* k, const void* v, con
                                 const float* top_gates, void* out, void* side, float* lse, const ReadDims& d,
                                 hipStream_t st) {
   const long N = (long)d.B * d.S;
-  // two workgroups per CU (LDS: 72 KiB each), a multiple of the 8 XCDs, no
-  // more than the items can use
-  const long items = (long)d.H * pair_fwd_max_items(N, d.E);
-  const int mi = (int)std::max<long>(8, std::min<long>(2L * pair_device_cus(), (items + 7) / 8 * 8) / 8 * 8);
-  const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;
-  float* fa = (float*)side;
+  // two workgroups per CU (LDS: 74 KiB each) in 8 equal XCD groups, no more
+  // than the work items can use (at most one per tile), and enough that a
+  // range fits kPairFwdMaxRange
+  const long items = (long)d.H * pair_plan_layout(N, d.E).max_tiles;
+  const long per_xcd = (items + 7) / 8;
+  const long gw = std::max<long>(std::max<long>(1, std::min<long>(2L * pair_device_cus() / 8, per_xcd)),
+                                 (per_xcd + kPairFwdMaxRange - 1) / kPairFwdMaxRange);
+  const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;  // > 0, as the kernel's maximum assumes
   NAYLIS_TIMED("read_fwd", st,
-               hipLaunchKernelGGL(read_fwd_pair_kernel, dim3(mi), dim3(256), 0, st, (const bf16_t*)q,
-                                  (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates, (bf16_t*)out, fa,
-                                  lse, d.order, N, d.H, d.L, d.E, alpha, mi));
+               hipLaunchKernelGGL(read_fwd_pair_kernel, dim3((unsigned)(8 * gw)), dim3(256), 0, st,
+                                  (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates,
+                                  (bf16_t*)out, (float*)side, lse, d.order, N, d.H, d.L, d.E, alpha));
   return hipGetLastError();
 }
 
@@ -890,9 +871,8 @@ hipError_t launch_read_bwd_pair(const void* q, const void* k, const void* v, con
   const float scale = (float)(1.0 / __builtin_sqrt(64.0));
   NAYLIS_TIMED("read_bwd_pair", st,
                hipLaunchKernelGGL(read_bwd_pair_kernel, dim3(d.H * R), dim3(512), 0, st, (const bf16_t*)q,
-                                  (const bf16_t*)k, (const bf16_t*)v, top_idx, top_gates, (const bf16_t*)o,
-                                  (const float*)side, (const bf16_t*)dout, lse,
-                                  d.order, (bf16_t*)dq, dlg_part,
+                                  (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)o, (const float*)side,
+                                  (const bf16_t*)dout, d.order, (bf16_t*)dq, dlg_part,
                                   dk_part, dv_part, N, d.H, d.L, d.E, alpha, scale, R, ns));
   const int kv_blocks = d.H * d.E * 4;
   const int g_blocks = (int)std::min<long>(1024, (N * 2 + 255) / 256);

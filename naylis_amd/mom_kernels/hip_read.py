@@ -98,9 +98,9 @@ class MomReadFunction(torch.autograd.Function):
 
 
 def read_side(lib, out, num_blocks, block_size, top_k):
-    """The side buffer the pair-tiled forward leaves for its backward (o's
-    bf16 remainder, block shares), when the read takes that path both ways
-    (naylis_mom_read_side_bytes > 0), else None."""
+    """The side buffer the pair-tiled forward leaves for its backward (each
+    row's biases minus lse, block-a share and selection bits), when the read
+    takes that path both ways (naylis_mom_read_side_bytes > 0), else None."""
     B, S, H, HD = out.shape
     nbytes = int(lib.naylis_mom_read_side_bytes(B, S, H, HD, num_blocks, block_size, top_k))
     if nbytes > 0:

@@ -102,12 +102,12 @@ def test_read_null_pointers_and_workspace(lib):
 ])
 def test_read_side_bytes_rule(lib, dims, want):
     """naylis_mom_read_side_bytes > 0 exactly where the pair-tiled backward
-    applies: the rows' block-a shares, (H, B, S) fp32."""
+    applies: four 32-bit row constants per (head, token)."""
     nbytes = lib.naylis_mom_read_side_bytes(*dims)
     assert (nbytes > 0) == bool(want)
     if want:
         B, S, H = dims[:3]
-        assert nbytes == B * S * H * 4
+        assert nbytes == B * S * H * 16
 
 
 def test_router_and_bank_reject_bad_arguments(lib):

@@ -151,6 +151,32 @@ def test_read_deterministic(dev):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("case", [(2, 256, 4, 64, 8, 128, 2, "distinct"),   # pair-tiled backward
+                                  (2, 100, 4, 32, 4, 32, 2, "random")])    # two-pass backward
+def test_read_tiny_gradients_keep_their_precision(case, dev):
+    """An upstream gradient of 2^-20 (a layer loss's mean over many
+    elements gives such scales) scales every gradient by 2^-20 and keeps
+    the relative bar: no product may flush it (fp16 operands would, below
+    2^-14).  The bound is the parity bar with atol scaled alike."""
+    from naylis_amd import mom_kernels
+    B, S, H, HD, NB, BS, topk, routing = case
+    q, k, v, top, gates, dout = make_inputs(*case)
+    dout = (dout.float() * 2.0 ** -20).bfloat16()
+    ref = oracle_read(q, k, v, top, gates, dout, NB, BS)
+    qd = q.to(dev).requires_grad_(True)
+    kd = k.to(dev).requires_grad_(True)
+    vd = v.to(dev).requires_grad_(True)
+    gd = gates.to(dev).requires_grad_(True)
+    out = mom_kernels.mom_read(qd, kd, vd, top.to(dev), gd, num_blocks=NB, block_size=BS, mode="hip")
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    atol = 2e-3 * 2.0 ** -20
+    for name, got, want in (("dq", qd.grad, ref[1]), ("dk", kd.grad, ref[2]), ("dv", vd.grad, ref[3]),
+                            ("d_gates", gd.grad, ref[4])):
+        assert float(want.abs().max()) > 0, name
+        assert_close(got, want, name, atol=atol)
+
+
 def test_read_empty_sequence(dev):
     from naylis_amd import mom_kernels
     q = torch.zeros(2, 0, 2, 16, dtype=torch.bfloat16, device=dev, requires_grad=True)

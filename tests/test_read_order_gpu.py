@@ -55,7 +55,7 @@ def check_pair_plan(buf, top_idx, E):
     a CPU statement: the table is the stable sort by sorted block pair (also
     when the mode word keeps sequence order); the keys with tokens ascending,
     each with its blocks, first tile and tile count; each key's run cut into
-    32-position tiles; forward items of up to 256 consecutive positions of a
+    32-position tiles; forward items of up to 128 consecutive positions of a
     key (first position, token count and blocks)."""
     idx = top_idx.reshape(-1, 2).numpy().astype(np.int64)
     N = idx.shape[0]
@@ -81,8 +81,8 @@ def check_pair_plan(buf, top_idx, E):
         for j in range(nt):
             cnt = min(32, c - 32 * j)
             want_tiles.append((pos + 32 * j, cnt | (ka << 6) | (kb << 11) | (kk << 16)))
-        for j in range(0, c, 256):
-            want_fit.append((pos + j, min(256, c - j) | (ka << 16) | (kb << 21)))
+        for j in range(0, c, 128):
+            want_fit.append((pos + j, min(128, c - j) | (ka << 16) | (kb << 21)))
         pos += c
         t += nt
     assert n_tiles == t and n_fit == len(want_fit)
