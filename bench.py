@@ -171,8 +171,39 @@ def executed_tiles(idx, E, tile=128):
     return int(oh.view(n_tiles, tile, E).any(1).sum()), ("grouped" if int(order[0]) == 1 else "sequence")
 
 
+# Every launch of the read path (the north star's kernels): the token order (local histogram
+# and scatter launches), the two-pass path's tile lists, the forward, the backward kernels and
+# the backward's reduction.  Each is bracketed by its own HIP events (KernelTimer).
+READ_LAUNCHES = ("read_order", "read_tile_lists", "read_fwd", "read_bwd_pair", "read_bwd_dq", "read_bwd_dkdv",
+                 "read_bwd_reduce")
+
+
+def pair_executed_tiles(idx, E):
+    """(128-token tile, block) units the pair-tiled kernels execute: every
+    token of a 32-token tile of pair (a, b) runs against both blocks (one
+    for a == b), the pair's runs padded to whole tiles."""
+    import torch
+    K = idx.shape[-1]
+    flat = idx.reshape(-1, K).long().clamp(0, E - 1)
+    lo, hi = flat.min(1).values, flat.max(1).values
+    key = lo * E + hi
+    counts = torch.bincount(key, minlength=E * E)
+    tiles = (counts + 31) // 32
+    nblk = torch.where(torch.arange(E * E, device=idx.device) % (E + 1) == 0, 1, 2)
+    return float((tiles * 32 * nblk).sum()) / 128.0
+
+
 def cpu_model():
-    """The host CPU's model name (what `lscpu` reports), from /proc/cpuinfo."""
+    """The host CPU's model name as `lscpu` reports it (its "Model name"
+    line), else /proc/cpuinfo's "model name"."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -183,17 +214,18 @@ def cpu_model():
 
 
 def cpu_baseline(cfg, sample_b):
-    """Eager fp32 oracle layer on the host cores, as planned for the CPU
-    baseline: config 2 fwd+bwd on `sample_b` of the B sequences at the full T
-    (all of them by default) and config 1 forward (B=2, T=512), each 2 warmup
-    runs then the median of 5."""
+    """Eager fp32 oracle layer on every core of the process's affinity set,
+    as planned for the CPU baseline: config 2 fwd+bwd on `sample_b` of the B
+    sequences at the full T (all of them by default), the bank rescaled to
+    the workload's Frobenius norm, and config 1 forward (B=2, T=512), each 2
+    warmup runs then the median of 5."""
     import torch
 
     import oracle
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
 
-    def make(B, T, D, H, E, BS, K, R):
+    def make(B, T, D, H, E, BS, K, R, bank_fro=None):
         torch.manual_seed(0)
         layer = oracle.OracleMoMLayer(D, H, E * BS, BS, K, R)
         with torch.no_grad():
@@ -201,7 +233,10 @@ def cpu_baseline(cfg, sample_b):
                 lin.weight.normal_(0, 0.02)
             layer.mom_scale.fill_(1.0)
         layer.noise_scale = 0.0
-        M = (torch.randn(E, BS * D) * 0.02).requires_grad_(True)
+        M = torch.randn(E, BS * D) * 0.02
+        if bank_fro:
+            M = M * (bank_fro / float(M.norm()))
+        M.requires_grad_(True)
         x = torch.randn(B, T, D)
         x = (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)).requires_grad_(True)
         return layer, M, x, torch.randn(B, T, D)
@@ -216,7 +251,7 @@ def cpu_baseline(cfg, sample_b):
 
     B, T, D, H, E, BS, K, R = (cfg[k] for k in ("B", "T", "D", "H", "E", "BS", "K", "R"))
     b = min(sample_b, B)
-    layer, M, x, dy = make(b, T, D, H, E, BS, K, R)
+    layer, M, x, dy = make(b, T, D, H, E, BS, K, R, cfg.get("bank_fro"))
 
     def fwd_bwd():
         y = layer(x, M)
@@ -232,8 +267,9 @@ def cpu_baseline(cfg, sample_b):
     with torch.no_grad():
         med1 = median_time(lambda: l1(x1, M1))
     return {"value": round(b * T / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle.OracleMoMLayer fp32 fwd+bwd, {b} of {B} sequences x T={T} "
-                      f"(2 warmup, median of 5 runs: {med:.3f} s), torch {torch.__version__}",
+            "sample": f"oracle.OracleMoMLayer fp32 fwd+bwd, {b} of {B} sequences x T={T}, bank "
+                      f"Frobenius {cfg.get('bank_fro') or 'as drawn'} (2 warmup, median of 5 runs: {med:.3f} s), "
+                      f"torch {torch.__version__}, {threads} threads (the affinity set)",
             "cpu_model": cpu_model(),
             "config1_forward": {"value": round(c1["B"] * c1["T"] / med1, 1), "unit": "tokens/s",
                                 "ms": round(med1 * 1e3, 2),
@@ -472,19 +508,18 @@ def decoder_bench(args, cfg, dev):
         # the routing this forward drew (with its Gumbel noise): the timed steps draw their own,
         # of the same distribution
         A_total += active_tiles(m.last_top_idx.view(B, T, -1), E)
-    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce")
-    read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
+    read_ms = sum(kernels[k][0] for k in READ_LAUNCHES if k in kernels) / args.steps
     read_flop = 14.0 * D * BS * 128 * A_total
     read_tf = read_flop / (read_ms * 1e-3) / 1e12
-    unit_per_layer = 2.0 * D * BS * 128 * A_total / cfg["layers"]
-    alg = {"read_fwd": 2 * unit_per_layer, "read_bwd_dq": 3 * unit_per_layer, "read_bwd_dkdv": 4 * unit_per_layer}
-    dominant = max((k for k in kernels if k in alg), key=lambda k: kernels[k][0])
-    dom_ms = per[dominant][0]
-    ach = alg[dominant] / (dom_ms * 1e-3) / 1e12
-    roof = {"kernel": dominant, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "avg_us": round(dom_ms * 1e3, 2), "alg_flop_per_launch": alg[dominant],
-            "note": "the path's dominant library kernel (the MoM read); trunk GEMMs and attention are torch's"}
+    # the read's launches over all layers against the reference's work on this forward's routing
+    # (A from the Gumbel-noised router of one forward: the timed steps draw their own routing of
+    # the same distribution, so this is an effective rate, not a measured fraction)
+    roof = {"kernel": "read (all layers): " + " + ".join(k for k in READ_LAUNCHES if k in kernels),
+            "bound": "mfma", "achieved": round(read_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(read_tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "avg_us": round(read_ms * 1e3, 2),
+            "alg_flop_per_launch": read_flop,
+            "note": "effective rate: A is one forward's Gumbel-noised routing (A = %d over %d layers), not "
+                    "the timed steps' own; trunk GEMMs and attention are torch's" % (A_total, cfg["layers"])}
     # per-token weights: every matrix but the bank and its K/V projections (the tied
     # embedding counts once, as the LM head); the bank projections run over the L slots
     params_dense = sum(p.numel() for n, p in model.named_parameters()
@@ -514,7 +549,7 @@ def decoder_bench(args, cfg, dev):
         "model": {"flop_per_step": model_flop, "tflops": round(model_tf, 1),
                   "mfma_frac": round(model_tf / PEAK_BF16_TFLOPS, 4), "loss": round(float(loss.detach()), 4)},
         "read": {"active_tile_blocks_all_layers": A_total, "alg_flop": read_flop, "ms": round(read_ms, 4),
-                 "tflops": round(read_tf, 2), "mfma_frac": round(read_tf / PEAK_BF16_TFLOPS, 4)},
+                 "effective_tflops": round(read_tf, 2)},
         "kernels_us": {k: round(v[0] * 1e3, 2) for k, v in sorted(per.items())},
         "kernels_per_step": {k: round(v[1], 2) for k, v in sorted(per.items())},
     }
@@ -591,24 +626,43 @@ def main(argv=None):
            "bank_kv_bwd_dw": 2 * 2.0 * D * D * L, "linear_wgrad": 2.0 * ntok * D * D}
     per = {k: (v[0] / v[1], v[1] / args.steps) for k, v in kernels.items() if v[1]}  # avg ms, launches/step
 
-    # the roofline is the read itself (the north-star path): its kernels, one launch each per step,
-    # priced on the 14-unit basis (forward 2 products, backward 5, 2 flop per multiply-add) over
-    # their summed durations
-    read_names = ("read_fwd", "read_bwd_dq", "read_bwd_dkdv", "read_bwd_reduce")
-    read_ms = sum(kernels[k][0] for k in read_names if k in kernels) / args.steps
+    # the roofline is the read itself (the north-star path): all of its launches per step (the
+    # token order, the forward, the backward and its reduction), priced on the reference's work,
+    # the 14-unit basis (forward 2 products, backward 5, 2 flop per multiply-add) over its active
+    # (128-token tile, block) pairs A, and beside it on the basis of the tile-blocks the path
+    # executed
+    read_launched = [k for k in READ_LAUNCHES if k in kernels]
+    read_ms = sum(kernels[k][0] for k in read_launched) / args.steps
     read_flop = 14.0 * D * BS * 128 * A
     read_tf = read_flop / (read_ms * 1e-3) / 1e12
-    roof = {"kernel": "read: " + " + ".join(k for k in read_names if k in kernels), "bound": "mfma",
+    if "read_bwd_pair" in kernels:
+        A_run, run_basis = pair_executed_tiles(idx, E), "pair tiles: 32 tokens x both blocks of their pair"
+    else:
+        A_run, run_basis = float(A_exec), f"{order_mode}-order 128-token tiles"
+    exec_tf = 14.0 * D * BS * 128 * A_run / (read_ms * 1e-3) / 1e12
+    roof = {"kernel": "read: " + " + ".join(read_launched), "bound": "mfma",
             "achieved": round(read_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(read_tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "avg_us": round(read_ms * 1e3, 2),
-            "alg_flop_per_launch": read_flop}
+            "alg_flop_per_launch": read_flop, "basis": f"active (128-token tile, block) pairs A = {A}",
+            "frac_exec": round(exec_tf / PEAK_BF16_TFLOPS, 4),
+            "exec_basis": f"{run_basis}: {A_run:.1f} tile-block units"}
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             tr = json.load(f)
-        parts = [tr.get(f"{args.workload}:{k}") for k in read_names if k in kernels]
+        parts = [tr.get(f"{args.workload}:{k}") for k in read_launched]
         if parts and all(t is not None for t in parts):
             roof["traffic"] = int(sum(parts))
+            roof["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, " \
+                                     "scaled by a copy kernel's readings)"
+    counters_file = os.path.join(ROOT, "profiles", "read_counters.json")
+    if os.path.exists(counters_file):
+        with open(counters_file) as f:
+            rc = json.load(f).get(args.workload, {})
+        if rc:
+            roof["mfma_busy_counters"] = rc.get("mfma_busy")
+            roof["mfma_busy_source"] = "profiles/read_counters.json (SQ_VALU_MFMA_BUSY_CYCLES over the read's " \
+                                       "launches, per SIMD, over their GRBM_GUI_ACTIVE cycles)"
     # library GEMMs on the MFMA (bank K/V and its gradients, q/o weight gradients)
     gemms = {k: {"us": round(per[k][0] * 1e3, 2), "tflops": round(alg[k] / (per[k][0] * 1e-3) / 1e12, 1),
                  "mfma_frac": round(alg[k] / (per[k][0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}

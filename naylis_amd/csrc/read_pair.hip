@@ -352,7 +352,20 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
 
 // ----------------------------------------------------------------- backward
 // Workgroup (head h, range r of the head's tiles); wave w owns slots
-// 32 w .. 32 w + 31 of the current pair (w < 4: block a, else block b).
+// 32 w .. 32 w + 31 of the current pair (w < 4: block a, else block b).  The
+// tiles run through a software pipeline with one barrier per tile: the step
+// of tile t computes
+//   S3(t - 1): dQ^T of tile t - 1 over all of the pair's slots and its
+//              gate-gradient partials (from the dS^T that S2 left in LDS);
+//   S2(t):     P and dS from tile t's S and dP - delta products, dV^T += dO^T P
+//              and dK^T += Q^T dS, dS^T to LDS;
+//   S1(t + 1): tile t + 1's S and dP - delta products (same pair);
+//   S4(t - 2): tile t - 2's gate gradients from its partials;
+// and stages tile t + 2's rows, so each barrier separates independent
+// product, softmax and staging work of four tiles.  A pair change after
+// tile t drains the pipeline: S3(t), S4(t - 1), the pair's dK / dV sums as a
+// partial, the next pair's rows, S4(t), S1(t + 1).  One-block pairs run the
+// same code: block b's bias is -inf, so its weights are zero.
 __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ o, const float* __restrict__ rowtab, const bf16_t* __restrict__ dout,
@@ -362,16 +375,18 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   constexpr int HD = kPHD, KS = HD / 16, NO = HD / 32, PITCH = kPPitch, TQ = kPairTile, NT = 512;
   constexpr int DSP = kPDsPitch;
 
-  __shared__ __attribute__((aligned(16))) bf16_t q_lds[2][TQ * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16_t do_lds[2][TQ * PITCH];
-  __shared__ __attribute__((aligned(16))) float ctab[2][3][TQ];  // c_a - lse, c_b - lse, -delta
-  __shared__ int32_t tok_lds[2][TQ];                              // token of each row (-1: none)
-  __shared__ int32_t sel_lds[2][TQ];                              // which selections hit a (bit 0,1) / b (bit 2,3)
-  __shared__ float fa_lds[2][TQ];                                 // the forward's weight share of block a
-  __shared__ __attribute__((aligned(16))) bf16_t kt_lds[kPSlots * PITCH];  // the pair's K rows
-  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[kPSlots * DSP];    // dS^T of the tile (bf16)
-  __shared__ __attribute__((aligned(16))) bf16_t dsl_lds[kPSlots * DSP];   // and its bf16 remainder
-  __shared__ float dl_lds[4][TQ];  // gate-gradient partials: (block a | b) x (slot half)
+  // tile t's rows in buffer (t - i0) % 3, its row constants in (t - i0) & 7,
+  // its dS^T and gate partials in (t - i0) & 1
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds[3][TQ * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t do_lds[3][TQ * PITCH];
+  __shared__ __attribute__((aligned(16))) float ctab[3][3][TQ];  // c_a - lse, c_b - lse, -delta
+  __shared__ int32_t tok_lds[8][TQ];                              // token of each row (-1: none)
+  __shared__ int32_t sel_lds[8][TQ];                              // which selections hit a (bit 0,1) / b (bit 2,3)
+  __shared__ float fa_lds[8][TQ];                                 // the forward's weight share of block a
+  __shared__ __attribute__((aligned(16))) bf16_t kt_lds[kPSlots * PITCH];    // the pair's K rows
+  __shared__ __attribute__((aligned(16))) bf16_t ds_lds[2][kPSlots * DSP];   // dS^T (bf16)
+  __shared__ __attribute__((aligned(16))) bf16_t dsl_lds[2][kPSlots * DSP];  // and its bf16 remainder
+  __shared__ float dl_lds[2][4][TQ];  // gate-gradient partials: (block a | b) x (slot half)
   __shared__ int2 tl_lds[kPairBwdMaxRange];  // the range's tile words (first position, count | blocks | pair)
 
   const PairPlanLayout pl = pair_plan_layout(N, E);
@@ -391,10 +406,12 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   __syncthreads();
   auto tile_w0 = [&](int t) { return tl_lds[t - i0].x; };
   auto tile_w1 = [&](int t) { return tl_lds[t - i0].y; };
+  auto qbuf = [&](int t) { return (t - i0) % 3; };
+  auto rbuf = [&](int t) { return (t - i0) & 7; };
 
   // ---- tile staging: waves 0..3 hold dO and o pieces (token row p >> 3,
-  // features 8 (p & 7) ..), waves 4..7 a Q piece; every thread the routing of
-  // row tid % 32 (threads 0..31 keep it)
+  // features 8 (p & 7) ..), waves 4..7 a Q piece; every thread the row
+  // constants of row tid % 32 (threads 0..31 keep them)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int sp = tid & 255, srow = sp >> 3, sc8 = sp & 7, rrow = tid & 31;
   const bool s_do = wave_u < 4;  // wave-uniform
@@ -406,9 +423,10 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   const __amdgpu_buffer_rsrc_t dq_rs = make_rsrc(dq, nd_bytes);
   const __amdgpu_buffer_rsrc_t dlg_rs = make_rsrc(dlg_part + (long)h * N * 2, (uint32_t)N * 8u);
   // Staging of one tile: order entries (of the staged piece's row and of row
-  // tid % 32), then its data: the dO (or Q) / o piece and the routing
-  // of row tid % 32.  Two sets of each rotate, so a tile's order entries are
-  // fetched three tiles and its data two tiles ahead of the tile's use.
+  // tid % 32), then its data: the dO (or Q) / o piece and the row constants
+  // of row tid % 32.  Two sets of each rotate: a tile's order entries are
+  // fetched four steps and its data two steps before it is stored to LDS,
+  // two steps before its S2.
   struct TokSet {
     int nx_pos, nx_raw, nr_pos, nr_raw;
   };
@@ -438,15 +456,16 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     ds.tok = (int)tr;
     ds.row = bld128(row_rs, tr >= 0 ? (uint32_t)tr * 16u : kOob);
   };
-  // into buffer `buf`: Q / dO rows, the per-row bias and delta tables (the
-  // forward's row constants), tokens and selections
-  auto store_tile = [&](int buf, const DataSet& ds) {
+  // tile t's Q / dO rows, the per-row bias and delta tables (the forward's
+  // row constants), tokens and selections
+  auto store_tile = [&](int t, const DataSet& ds) {
+    const int qb = qbuf(t), rb = rbuf(t);
     if (s_do) {
-      *reinterpret_cast<uint4*>(&do_lds[buf][srow * PITCH + 8 * sc8]) = ds.a;
+      *reinterpret_cast<uint4*>(&do_lds[qb][srow * PITCH + 8 * sc8]) = ds.a;
       // delta = sum_f dO_f o_f over the 8 features of the piece, then over the
       // row's 8 threads (o is the forward's bf16 output; its rounding moves
-      // the block sums of dS by (delta' - delta) M_x, which finish_gates
-      // removes, and dQ, dK by far less than their tolerance)
+      // the block sums of dS by (delta' - delta) M_x, which S4 removes, and
+      // dQ, dK by far less than their tolerance)
       const uint32_t dw[4] = {ds.a.x, ds.a.y, ds.a.z, ds.a.w};
       const uint32_t ow[4] = {ds.o.x, ds.o.y, ds.o.z, ds.o.w};
       float dsum = 0.f;
@@ -460,35 +479,31 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       dsum += dpp_f32<0xb1>(dsum);
       dsum += dpp_f32<0x4e>(dsum);
       dsum += dpp_f32<0x141>(dsum);
-      if (sc8 == 0) ctab[buf][2][srow] = -dsum;
+      if (sc8 == 0) ctab[qb][2][srow] = -dsum;
     } else {
-      *reinterpret_cast<uint4*>(&q_lds[buf][srow * PITCH + 8 * sc8]) = ds.a;
+      *reinterpret_cast<uint4*>(&q_lds[qb][srow * PITCH + 8 * sc8]) = ds.a;
     }
     if (tid < TQ) {
       const bool ok = ds.tok >= 0;
-      ctab[buf][0][tid] = ok ? __uint_as_float(ds.row.x) : -INFINITY;
-      ctab[buf][1][tid] = ok ? __uint_as_float(ds.row.y) : -INFINITY;
-      tok_lds[buf][tid] = ds.tok;
-      fa_lds[buf][tid] = ok ? __uint_as_float(ds.row.z) : 1.f;
-      sel_lds[buf][tid] = ok ? (int)ds.row.w : 0;
+      ctab[qb][0][tid] = ok ? __uint_as_float(ds.row.x) : -INFINITY;
+      ctab[qb][1][tid] = ok ? __uint_as_float(ds.row.y) : -INFINITY;
+      tok_lds[rb][tid] = ds.tok;
+      fa_lds[rb][tid] = ok ? __uint_as_float(ds.row.z) : 1.f;
+      sel_lds[rb][tid] = ok ? (int)ds.row.w : 0;
     }
   };
 
-  // ---- the current pair: its K rows in LDS (the dQ product's K^T
-  // fragments), this lane's K and V slot rows in registers (B operands of S
-  // and dP: lane = slot), the dK / dV accumulators
-  int key = -1, pa = 0, pb = 0, nblk = 2;
-  bool w_on = true;
+  // ---- the current pair: its K rows in LDS (B operand of S, K^T fragments
+  // of dQ), this lane's V slot row in registers (B operand of dP: lane =
+  // slot), the dK / dV accumulators
+  int key = -1;
   f32x16 acc_dk[NO], acc_dv[NO];
-  bf16x8 kf[KS], vf[KS];  // this lane's slot row of K and V: B operands of S and dP
+  bf16x8 vf[KS];
   const int w_slot = 32 * wave + col;  // this lane's slot in the pair (0..255)
   auto enter_pair = [&](int t) {
     const int w1 = __builtin_amdgcn_readfirstlane(tile_w1(t));
     key = pair_tile_key(w1);
-    pa = pair_tile_a(w1);
-    pb = pair_tile_b(w1);
-    nblk = pa == pb ? 1 : 2;
-    w_on = wave < 4 * nblk;
+    const int pa = pair_tile_a(w1), pb = pair_tile_b(w1);
     constexpr int PR = kPSlots * HD / 8 / NT;
 #pragma unroll
     for (int rr = 0; rr < PR; ++rr) {
@@ -502,7 +517,6 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const long off = srow_g * D + (long)h * HD + 16 * ks + 8 * g;
-        kf[ks] = *reinterpret_cast<const bf16x8*>(k + off);
         vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
       }
     }
@@ -525,7 +539,6 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   };
   // the pair's sums of this range into segment r + key (rows: the pair's 256 slots)
   auto flush = [&]() {
-    if (!w_on) return;
     const long base = (((long)h * n_seg + (r + key)) * kPSlots + w_slot) * HD;
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
@@ -539,20 +552,120 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       }
     }
   };
-  // gate gradients of the tile in buffer `buf` (partials in dl_lds): threads
-  // 0..31.  With P recomputed from lse (fp32 weights over the bf16 row sum)
-  // and delta from o (the bf16 weights), sum_n dS_n over both blocks, which
-  // is 0 for the exact softmax, keeps a residue (delta' - delta) S; the
-  // block sums are G_x = A_x - delta' M_x, so G_a - (M_a / S)(G_a + G_b) is
-  // the exact A_a - delta M_a.  M_a / S is the forward's share of the row
-  // weight on block a (its error only scales that small residue).
-  auto finish_gates = [&](int buf) {
-    // every thread computes row tid % 32; threads 0..31 store it
-    const int tk = tok_lds[buf][rrow];
-    const int sm = sel_lds[buf][rrow];
-    const float fa = fa_lds[buf][rrow];
-    const float g0 = dl_lds[0][rrow] + dl_lds[1][rrow];
-    const float g1 = dl_lds[2][rrow] + dl_lds[3][rrow];
+
+  // ---- S1(t): S = Q K^T and dP - delta = dO V^T - delta for this wave's 32
+  // slots x the tile's 32 tokens (registers 4 j4 .. 4 j4 + 3 are tokens
+  // 8 j4 + 4 g + 0..3)
+  f32x16 acc_s, acc_p;
+  auto s1 = [&](int t) {
+    const int qb = qbuf(t);
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const f32x4 nd = *reinterpret_cast<const f32x4*>(&ctab[qb][2][8 * j4 + 4 * g]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd[u];
+    }
+    acc_s = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = col * PITCH + 16 * ks + 8 * g;
+      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[qb][off]);
+      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[qb][off]);
+      const bf16x8 bk = *reinterpret_cast<const bf16x8*>(&kt_lds[w_slot * PITCH + 16 * ks + 8 * g]);
+      acc_s = mfma32(aq, bk, acc_s);
+      acc_p = mfma32(ad, vf[ks], acc_p);
+    }
+  };
+  // ---- S2(t): P, dS; dV^T += dO^T P, dK^T += Q^T dS, each weight as bf16
+  // plus its bf16 remainder (two products: ~2^-16 relative, where bf16 alone
+  // leaves 2^-9 per term in sums over thousands of tokens); dS^T (both parts)
+  // to LDS for S3
+  auto s2 = [&](int t, auto par) {
+    constexpr int B2 = decltype(par)::value;
+    const int qb = qbuf(t);
+    const int bsel = wave >> 2;  // 0: block a, 1: block b
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const f32x4 c4 = *reinterpret_cast<const f32x4*>(&ctab[qb][bsel][8 * j4 + 4 * g]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vv = 4 * j4 + u;
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, c4[u]));
+        acc_s[vv] = p;
+        acc_p[vv] = p * acc_p[vv];
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 bp, bpl, bd, bdl;
+      pack8_hilo(acc_s, 8 * kk, bp, bpl);
+      pack8_hilo(acc_p, 8 * kk, bd, bdl);
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const bf16x8 a_do = lds_frag_T<true, true>(do_lds[qb], PITCH, 16 * kk, 32 * j);
+        const bf16x8 a_q = lds_frag_T<true, true>(q_lds[qb], PITCH, 16 * kk, 32 * j);
+        acc_dv[j] = mfma32(a_do, bpl, mfma32(a_do, bp, acc_dv[j]));
+        acc_dk[j] = mfma32(a_q, bdl, mfma32(a_q, bd, acc_dk[j]));
+      }
+      // registers 8 kk .. 8 kk + 7 are tokens 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3
+      const uint4 u = __builtin_bit_cast(uint4, bd), ul = __builtin_bit_cast(uint4, bdl);
+      const int dso = w_slot * DSP + 16 * kk + 4 * g;
+      *reinterpret_cast<uint2*>(&ds_lds[B2][dso]) = make_uint2(u.x, u.y);
+      *reinterpret_cast<uint2*>(&ds_lds[B2][dso + 8]) = make_uint2(u.z, u.w);
+      *reinterpret_cast<uint2*>(&dsl_lds[B2][dso]) = make_uint2(ul.x, ul.y);
+      *reinterpret_cast<uint2*>(&dsl_lds[B2][dso + 8]) = make_uint2(ul.z, ul.w);
+    }
+  };
+  // ---- S3(t): dQ^T tile (features 16 (w & 3) .., tokens 16 (w >> 2) ..)
+  // over the pair's slots, and the gate-gradient partials: wave with
+  // w & 3 == c sums dS over K-steps 2c, 2c + 1 (block a for c < 2, b
+  // otherwise)
+  auto s3 = [&](int t, auto par) {
+    constexpr int B3 = decltype(par)::value;
+    const int tq = wave >> 2, fq = wave & 3;
+    const int q4 = (lane >> 4) & 3, j = lane & 15;
+    f32x4v accq0 = f32x4v{0.f, 0.f, 0.f, 0.f}, accq1 = accq0;
+#pragma unroll
+    for (int kk = 0; kk < 8; kk += 2) {
+      // A: K^T (features 16 fq .., slots 32 kk ..); B: dS^T (slots, tokens 16 tq ..)
+      accq0 = mfma16(frag16_T(kt_lds, PITCH, 32 * kk, 16 * fq), frag16_T(ds_lds[B3], DSP, 32 * kk, 16 * tq), accq0);
+      accq1 = mfma16(frag16_T(kt_lds, PITCH, 32 * kk + 32, 16 * fq),
+                     frag16_T(ds_lds[B3], DSP, 32 * kk + 32, 16 * tq), accq1);
+    }
+    float gsum = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int kk = 2 * fq + jj;
+      gsum = add_bf16x8(frag16_T(ds_lds[B3], DSP, 32 * kk, 16 * tq), gsum);
+      gsum = add_bf16x8(frag16_T(dsl_lds[B3], DSP, 32 * kk, 16 * tq), gsum);
+    }
+    // the four 16-lane groups hold different slots of the same token
+    gsum = xor16_f32(gsum, [](float a, float b) { return a + b; });
+    gsum = xor32_f32(gsum, [](float a, float b) { return a + b; });
+    if (lane < 16) dl_lds[B3][fq][16 * tq + lane] = gsum;
+    // dQ rows: lane holds features 16 fq + 4 (l / 16) + 0..3 of token row 16 tq + l % 16
+    const f32x4v accq = accq0 + accq1;
+    const int tk = tok_lds[rbuf(t)][16 * tq + j];
+    const uint32_t px = (uint32_t)f32_to_bf16(accq[0] * dq_scale) | ((uint32_t)f32_to_bf16(accq[1] * dq_scale) << 16);
+    const uint32_t py = (uint32_t)f32_to_bf16(accq[2] * dq_scale) | ((uint32_t)f32_to_bf16(accq[3] * dq_scale) << 16);
+    bst64(dq_rs, tk >= 0 ? (uint32_t)(((long)tk * D + (long)h * HD + 16 * fq + 4 * q4) * 2) : kOob, px, py);
+  };
+  // ---- S4(t): gate gradients of tile t (partials of S3(t)): every thread
+  // computes row tid % 32, threads 0..31 store it.  With P recomputed from
+  // lse (fp32 weights over the bf16 row sum) and delta from o (the bf16
+  // weights), sum_n dS_n over both blocks, which is 0 for the exact softmax,
+  // keeps a residue (delta' - delta) S; the block sums are G_x = A_x - delta'
+  // M_x, so G_a - (M_a / S)(G_a + G_b) is the exact A_a - delta M_a.  M_a / S
+  // is the forward's share of the row weight on block a (its error only
+  // scales that small residue).
+  auto s4 = [&](int t, auto par) {
+    constexpr int B4 = decltype(par)::value;
+    const int rb = rbuf(t);
+    const int tk = tok_lds[rb][rrow];
+    const int sm = sel_lds[rb][rrow];
+    const float fa = fa_lds[rb][rrow];
+    const float g0 = dl_lds[B4][0][rrow] + dl_lds[B4][1][rrow];
+    const float g1 = dl_lds[B4][2][rrow] + dl_lds[B4][3][rrow];
     const float tot = g0 + g1;
     const float ga = g0 - fa * tot;
     const float gb = g1 - (1.f - fa) * tot;
@@ -561,145 +674,67 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     bst64(dlg_rs, (tid < TQ && tk >= 0) ? (uint32_t)tk * 8u : kOob, __float_as_uint(d0), __float_as_uint(d1));
   };
 
-  // ---- prologue: tile i0 staged and its pair entered; the data of tiles
-  // i0 + 1, i0 + 2 and the order entries of tile i0 + 3 in flight.  Tile i
-  // uses LDS buffer (i - i0) & 1 and staging sets of that parity.
+  // ---- prologue: the first pair entered; tiles i0, i0 + 1 staged, the data
+  // of i0 + 2, i0 + 3 and the order entries of i0 + 4, i0 + 5 in flight;
+  // S1(i0).  Staging sets of parity (t - i0) & 1 serve tile t.
   TokSet tks[2];
   DataSet dts[2];
   enter_pair(i0);
   fetch_tokens(tks[0], i0);
-  load_tile(dts[0], tks[0]);
-  store_tile(0, dts[0]);
   fetch_tokens(tks[1], i0 + 1);
-  fetch_tokens(tks[0], i0 + 2);
-  load_tile(dts[1], tks[1]);
   load_tile(dts[0], tks[0]);
+  load_tile(dts[1], tks[1]);
+  fetch_tokens(tks[0], i0 + 2);
   fetch_tokens(tks[1], i0 + 3);
+  store_tile(i0, dts[0]);
+  store_tile(i0 + 1, dts[1]);
+  load_tile(dts[0], tks[0]);
+  load_tile(dts[1], tks[1]);
+  fetch_tokens(tks[0], i0 + 4);
+  fetch_tokens(tks[1], i0 + 5);
   lds_barrier();
+  s1(i0);
+  int s3_done = i0 - 1, s4_done = i0 - 1;  // the last tiles whose S3 / S4 ran (uniform)
 
-  // one tile; P = (i - i0) & 1 as a compile-time constant (the loop below is
-  // unrolled by two), so the staging sets stay in registers
-  auto tile_step = [&](auto par, int i) {
+  // one step of the pipeline; P = (t - i0) & 1 as a compile-time constant
+  // (the loop below is unrolled by two), so the staging sets stay in registers
+  auto step = [&](auto par, int t) {
     constexpr int P = decltype(par)::value;
-    const int buf = P;
-    fetch_tokens(tks[P], i + 4);        // tks[P] was last read by tile i + 2's load
-    if (i > i0) finish_gates(buf ^ 1);  // the previous tile's gate gradients (its partials are complete)
-
-    // ---- S, dP - delta, P, dS for this wave's 32 slots x the tile's 32 tokens
-    f32x16 acc_s = f32x16{}, acc_p;
-    if (w_on) {
-      const int bsel = wave >> 2;  // 0: block a, 1: block b
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const f32x4 nd = *reinterpret_cast<const f32x4*>(&ctab[buf][2][8 * j4 + 4 * g]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc_p[4 * j4 + u] = nd[u];
-      }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int off = col * PITCH + 16 * ks + 8 * g;
-        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&q_lds[buf][off]);
-        const bf16x8 ad = *reinterpret_cast<const bf16x8*>(&do_lds[buf][off]);
-        acc_s = mfma32(aq, kf[ks], acc_s);
-        acc_p = mfma32(ad, vf[ks], acc_p);
-      }
-      // registers 4 j4 .. 4 j4 + 3 are tokens 8 j4 + 4 g + 0..3
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&ctab[buf][bsel][8 * j4 + 4 * g]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int vv = 4 * j4 + u;
-          const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[vv], alpha, c4[u]));
-          acc_s[vv] = p;
-          acc_p[vv] = p * acc_p[vv];
-        }
-      }
-      // ---- dV^T += dO^T P, dK^T += Q^T dS, each weight as bf16 plus its
-      // bf16 remainder (two products: ~2^-16 relative, where bf16 alone
-      // leaves 2^-9 per term in sums over thousands of tokens); dS^T (both
-      // parts) to LDS for dQ and the gate sums
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        bf16x8 bp, bpl, bd, bdl;
-        pack8_hilo(acc_s, 8 * kk, bp, bpl);
-        pack8_hilo(acc_p, 8 * kk, bd, bdl);
-#pragma unroll
-        for (int j = 0; j < NO; ++j) {
-          const bf16x8 a_do = lds_frag_T<true, true>(do_lds[buf], PITCH, 16 * kk, 32 * j);
-          const bf16x8 a_q = lds_frag_T<true, true>(q_lds[buf], PITCH, 16 * kk, 32 * j);
-          acc_dv[j] = mfma32(a_do, bpl, mfma32(a_do, bp, acc_dv[j]));
-          acc_dk[j] = mfma32(a_q, bdl, mfma32(a_q, bd, acc_dk[j]));
-        }
-        // registers 8 kk .. 8 kk + 7 are tokens 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3
-        const uint4 u = __builtin_bit_cast(uint4, bd), ul = __builtin_bit_cast(uint4, bdl);
-        const int dso = w_slot * DSP + 16 * kk + 4 * g;
-        *reinterpret_cast<uint2*>(&ds_lds[dso]) = make_uint2(u.x, u.y);
-        *reinterpret_cast<uint2*>(&ds_lds[dso + 8]) = make_uint2(u.z, u.w);
-        *reinterpret_cast<uint2*>(&dsl_lds[dso]) = make_uint2(ul.x, ul.y);
-        *reinterpret_cast<uint2*>(&dsl_lds[dso + 8]) = make_uint2(ul.z, ul.w);
-      }
-    }
-    lds_barrier();  // dS^T of the tile complete
-
-    // ---- dQ^T tile (features 16 (w & 3) .., tokens 16 (w >> 2) ..) over the
-    // pair's slots, and the gate-gradient partials: wave with w & 3 == c sums
-    // dS over K-steps 2c, 2c + 1 (block a for c < 2, b otherwise)
-    {
-      const int tq = wave >> 2, fq = wave & 3;
-      const int q4 = (lane >> 4) & 3, j = lane & 15;
-      f32x4v accq = f32x4v{0.f, 0.f, 0.f, 0.f};
-      float gsum = 0.f;
-      const int nks = 4 * nblk;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        if (kk < nks) {
-          // A: K^T (features 16 fq .., slots 32 kk ..); B: dS^T (slots, tokens 16 tq ..)
-          const bf16x8 akt = frag16_T(kt_lds, PITCH, 32 * kk, 16 * fq);
-          const bf16x8 bds = frag16_T(ds_lds, DSP, 32 * kk, 16 * tq);
-          accq = mfma16(akt, bds, accq);
-        }
-      }
-      if (2 * fq < nks) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int kk = 2 * fq + jj;
-          gsum = add_bf16x8(frag16_T(ds_lds, DSP, 32 * kk, 16 * tq), gsum);
-          gsum = add_bf16x8(frag16_T(dsl_lds, DSP, 32 * kk, 16 * tq), gsum);
-        }
-      }
-      // the four 16-lane groups hold different slots of the same token
-      gsum = xor16_f32(gsum, [](float a, float b) { return a + b; });
-      gsum = xor32_f32(gsum, [](float a, float b) { return a + b; });
-      if (lane < 16) dl_lds[fq][16 * tq + lane] = gsum;
-      // dQ rows: lane holds features 16 fq + 4 (l / 16) + 0..3 of token row 16 tq + l % 16
-      const int tk = tok_lds[buf][16 * tq + j];
-      const uint32_t px = (uint32_t)f32_to_bf16(accq[0] * dq_scale) | ((uint32_t)f32_to_bf16(accq[1] * dq_scale) << 16);
-      const uint32_t py = (uint32_t)f32_to_bf16(accq[2] * dq_scale) | ((uint32_t)f32_to_bf16(accq[3] * dq_scale) << 16);
-      bst64(dq_rs, tk >= 0 ? (uint32_t)(((long)tk * D + (long)h * HD + 16 * fq + 4 * q4) * 2) : kOob, px, py);
-    }
-
-    // ---- next tile: its pair (flush and reload on a change), staging, barrier
-    if (i + 1 < i1) {
-      const int nkey = __builtin_amdgcn_readfirstlane(pair_tile_key(tile_w1(i + 1)));
-      if (nkey != key) {
-        // other waves may still read kt_lds in their dQ products: wait for
-        // them before the next pair's rows overwrite it
-        flush();
-        lds_barrier();
-        enter_pair(i + 1);
-      }
-      store_tile(buf ^ 1, dts[P ^ 1]);  // tile i + 1
-      load_tile(dts[P ^ 1], tks[P ^ 1]);         // tile i + 3 (its order entries: fetched by tile i - 1)
-    }
+    using Pc = std::integral_constant<int, P>;
+    using Qc = std::integral_constant<int, P ^ 1>;
+    const int nkey = t + 1 < i1 ? (int)__builtin_amdgcn_readfirstlane(pair_tile_key(tile_w1(t + 1))) : -1;
+    const bool cont = nkey == key;  // tile t + 1 in the current pair
+    if (t - 1 > s3_done) s3(t - 1, Qc{});
+    s2(t, Pc{});
+    if (cont) s1(t + 1);
+    if (t - 2 > s4_done) s4(t - 2, Pc{});
+    store_tile(t + 2, dts[P]);
+    load_tile(dts[P], tks[P]);     // tile t + 4
+    fetch_tokens(tks[P], t + 6);
     lds_barrier();
+    s3_done = max(s3_done, t - 1);
+    s4_done = max(s4_done, t - 2);
+    if (!cont) {
+      // drain: tile t's dQ and gates (S4(t - 1) beside S3(t): other
+      // partial buffers), the pair's sums, then the next pair
+      s3(t, Pc{});
+      if (t - 1 > s4_done) s4(t - 1, Qc{});
+      flush();
+      lds_barrier();  // S3(t) is done with kt_lds and has written tile t's partials
+      s4(t, Pc{});
+      if (t + 1 < i1) {
+        enter_pair(t + 1);
+        lds_barrier();  // the next pair's K rows complete (S1 reads other waves' rows)
+        s1(t + 1);
+      }
+      s3_done = t;
+      s4_done = t;
+    }
   };
-  for (int i = i0; i < i1; i += 2) {
-    tile_step(std::integral_constant<int, 0>{}, i);
-    if (i + 1 < i1) tile_step(std::integral_constant<int, 1>{}, i + 1);
+  for (int t = i0; t < i1; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < i1) step(std::integral_constant<int, 1>{}, t + 1);
   }
-  finish_gates((i1 - 1 - i0) & 1);
-  flush();
 }
 
 // ------------------------------------------------------------------- reduce
