@@ -48,7 +48,7 @@ constexpr int kPHD = 64;              // head_dim of the pair kernels
 constexpr int kPBS = 128;             // block size of the pair kernels
 constexpr int kPPitch = kPHD + 8;     // LDS row pitch (bf16) of K / V / Q / dO rows
 constexpr int kPSlots = 2 * kPBS;     // slots of a pair
-constexpr int kPDsPitch = kPairTile + 8;  // LDS row pitch of dS^T (slot rows, token columns)
+constexpr int kPDsPitch = kPairTile + 4;  // LDS row pitch of dS^T (slot rows, token columns; 72 B)
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
