@@ -363,15 +363,18 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
 //   S4(t - 2): tile t - 2's gate gradients from its partials;
 // and stages tile t + 2's rows, so each barrier separates independent
 // product, softmax and staging work of four tiles.  A pair change after
-// tile t drains the pipeline: S3(t), S4(t - 1), the pair's dK / dV sums as a
-// partial, the next pair's rows, S4(t), S1(t + 1).  One-block pairs run the
-// same code: block b's bias is -inf, so its weights are zero.
+// tile t drains the pipeline: S3(t), S4(t - 1), the finished dK / dV sums as
+// partials, the next pair's rows, S4(t), S1(t + 1).  Block b's half (waves 4..7)
+// writes its sums per (range, pair), block a's half only when block a changes:
+// pairs are sorted by (a, b), so consecutive pairs mostly share block a and a
+// range writes one block-a partial per run of equal a.  One-block pairs run
+// the same code: block b's bias is -inf, so its weights are zero.
 __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ o, const float* __restrict__ rowtab, const bf16_t* __restrict__ dout,
     const int32_t* __restrict__ plan, bf16_t* __restrict__ dq, float* __restrict__ dlg_part,
     float* __restrict__ dk_part, float* __restrict__ dv_part, long N, int H, int L, int E, float alpha,
-    float dq_scale, int R, int n_seg) {
+    float dq_scale, int R, int n_seg_a, int n_seg_b) {
   constexpr int HD = kPHD, KS = HD / 16, NO = HD / 32, PITCH = kPPitch, TQ = kPairTile, NT = 512;
   constexpr int DSP = kPDsPitch;
 
@@ -496,14 +499,19 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
   // ---- the current pair: its K rows in LDS (B operand of S, K^T fragments
   // of dQ), this lane's V slot row in registers (B operand of dP: lane =
   // slot), the dK / dV accumulators
-  int key = -1;
+  int key = -1, pa = -1, pb = -1;
   f32x16 acc_dk[NO], acc_dv[NO];
   bf16x8 vf[KS];
   const int w_slot = 32 * wave + col;  // this lane's slot in the pair (0..255)
   auto enter_pair = [&](int t) {
     const int w1 = __builtin_amdgcn_readfirstlane(tile_w1(t));
     key = pair_tile_key(w1);
-    const int pa = pair_tile_a(w1), pb = pair_tile_b(w1);
+    const int na = pair_tile_a(w1);
+    // block a's half keeps its sums while block a stays (the previous pair's
+    // were written by flush otherwise); block b's half starts over
+    const bool zero = wave >= 4 || na != pa;
+    pa = na;
+    pb = pair_tile_b(w1);
     constexpr int PR = kPSlots * HD / 8 / NT;
 #pragma unroll
     for (int rr = 0; rr < PR; ++rr) {
@@ -520,10 +528,12 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
         vf[ks] = *reinterpret_cast<const bf16x8*>(v + off);
       }
     }
+    if (zero) {
 #pragma unroll
-    for (int j = 0; j < NO; ++j) {
-      acc_dk[j] = f32x16{};
-      acc_dv[j] = f32x16{};
+      for (int j = 0; j < NO; ++j) {
+        acc_dk[j] = f32x16{};
+        acc_dv[j] = f32x16{};
+      }
     }
   };
   // Transposed 16x16x32 operand from natural LDS rows: lane l gets
@@ -537,9 +547,20 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
     const v4i16 hi = lds_read_tr16(base + 4 * pitch);
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
-  // the pair's sums of this range into segment r + key (rows: the pair's 256 slots)
-  auto flush = [&]() {
-    const long base = (((long)h * n_seg + (r + key)) * kPSlots + w_slot) * HD;
+  // the finished sums before the pair `next` (-1: the range's end): block b's
+  // half as the (range, pair) partial, segment r + key of the B partials;
+  // block a's half, when block a changes, as the (range, block-a run)
+  // partial, segment r + a of the A partials (both unique: ranges and pairs
+  // are contiguous and sorted).  Rows: the block's 128 slots.
+  auto flush = [&](int next_a) {
+    long base;
+    if (wave < 4) {
+      if (next_a == pa) return;
+      base = (((long)h * n_seg_a + (r + pa)) * kPBS + w_slot) * HD;
+    } else {
+      if (pa == pb) return;  // a one-block pair: block b's half is zeros
+      base = ((long)H * n_seg_a * kPBS + ((long)h * n_seg_b + (r + key)) * kPBS + (w_slot - kPBS)) * HD;
+    }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
       const int f0 = 32 * j + 16 * g;
@@ -719,7 +740,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       // partial buffers), the pair's sums, then the next pair
       s3(t, Pc{});
       if (t - 1 > s4_done) s4(t - 1, Qc{});
-      flush();
+      flush(t + 1 < i1 ? (int)__builtin_amdgcn_readfirstlane(pair_tile_a(tile_w1(t + 1))) : -1);
       lds_barrier();  // S3(t) is done with kt_lds and has written tile t's partials
       s4(t, Pc{});
       if (t + 1 < i1) {
@@ -739,18 +760,21 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
 
 // ------------------------------------------------------------------- reduce
 // dK / dV of block e (rows e * 128 ..), head h, a quarter of its slots: the
-// sum over the pairs holding e (ascending pair index) and, within a pair,
-// over its ranges (ascending), of the pair's partial half for e; dK scaled.
+// A partials of the run of pairs (e, *) over its ranges (ascending), then
+// for each pair (a, e) with a != e (ascending) the B partials over its
+// ranges (ascending); dK scaled.
 // Workgroups past the dK / dV ones sum the per-head gate-gradient partials
 // (head order) into d(top_gates) through log(max(g, 1e-9)).
 __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
     const float* __restrict__ dk_part, const float* __restrict__ dv_part, const int32_t* __restrict__ plan,
-    bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long N, int H, int E, int R, int n_seg, float dk_scale,
+    bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long N, int H, int E, int R, int n_seg_a, int n_seg_b,
+    float dk_scale,
     int kv_blocks, const float* __restrict__ dlg_part, const float* __restrict__ top_gates,
     float* __restrict__ dgates) {
   constexpr int HD = kPHD, QS = kPBS / 4;  // slots per workgroup
-  __shared__ int seg[1024];
-  __shared__ int half[1024];
+  constexpr int MK = kPairBwdMaxE * (kPairBwdMaxE + 1) / 2;
+  __shared__ long seg_off[1024];  // first float of each partial's block rows
+  __shared__ int4 key_lds[MK];    // the pair table (block a, block b, first tile, tiles)
   __shared__ int n_s;
   if ((int)blockIdx.x >= kv_blocks) {
     const long n = N * 2;
@@ -776,56 +800,89 @@ __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
   const int qtr = b & 3, e = (b >> 2) % E, h = (b >> 2) / E;
   const int n_tiles = plan[pl.hdr], n_keys = plan[pl.hdr + 1];
   const int per = (n_tiles + R - 1) / R;
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int kk = 0; kk < n_keys; ++kk) {
-      const int* kr = plan + pl.keys + 4 * kk;
-      const int a = kr[0], bb = kr[1], ts = kr[2], nt = kr[3];
-      if ((a != e && bb != e) || nt <= 0) continue;
-      const int hf = a == e ? 0 : 1;
-      for (int rr = ts / per; rr <= (ts + nt - 1) / per && n < 1024; ++rr) {
-        seg[n] = rr + kk;
-        half[n] = hf;
-        ++n;
-      }
+  const int nk = min(n_keys, MK);  // (the backward's pair path takes E <= kPairBwdMaxE)
+  for (int i = threadIdx.x; i < nk; i += blockDim.x)
+    key_lds[i] = make_int4(plan[pl.keys + 4 * i], plan[pl.keys + 4 * i + 1], plan[pl.keys + 4 * i + 2],
+                           plan[pl.keys + 4 * i + 3]);
+  __syncthreads();
+  static_assert(MK <= 64, "one pair per lane of wave 0");
+  if (threadIdx.x < 64) {
+    // wave 0, lane k = pair k: the run (e, *)'s tile span (its A partials),
+    // then pair k's B partials when it is (a, e) with a != e, placed by a
+    // prefix count over the lanes
+    const int k = threadIdx.x;
+    const long rows = (long)kPBS * HD;
+    const int4 kr = k < nk ? key_lds[k] : make_int4(-1, -1, 0, 0);
+    const bool in_run = kr.x == e && kr.w > 0;
+    int t_first = in_run ? kr.z : 0x7fffffff, t_last = in_run ? kr.z + kr.w - 1 : -1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      t_first = min(t_first, __shfl_xor(t_first, o));
+      t_last = max(t_last, __shfl_xor(t_last, o));
     }
-    n_s = n;
+    const int na = t_last >= 0 ? t_last / per - t_first / per + 1 : 0;
+    const bool is_b = kr.y == e && kr.x != e && kr.w > 0;
+    const int nb = is_b ? (kr.z + kr.w - 1) / per - kr.z / per + 1 : 0;
+    int incl = nb;  // inclusive prefix of nb over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (k >= o) incl += y;
+    }
+    const int total = na + __shfl(incl, 63);
+    for (int i = k; i < na; i += 64)
+      if (i < 1024) seg_off[i] = ((long)h * n_seg_a + t_first / per + i + e) * rows;
+    for (int i = 0, at = na + incl - nb; i < nb; ++i)
+      if (at + i < 1024) seg_off[at + i] = (long)H * n_seg_a * rows + ((long)h * n_seg_b + kr.z / per + i + k) * rows;
+    if (k == 0) n_s = min(total, 1024);
   }
   __syncthreads();
   const int ns = n_s;
   const int D = H * HD;
-  // 32 slots x 64 features = 512 float4 per tensor: two per thread
-  for (int c = threadIdx.x; c < QS * HD / 4; c += blockDim.x) {
-    const int sl = c / (HD / 4), f4 = c % (HD / 4);
-    const int s_in = qtr * QS + sl;  // slot within the block
-    f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
-    int i = 0;
-    for (; i + 4 <= ns; i += 4) {
-      f32x4 pk[4], pv[4];
+  // 32 slots x 64 features = 512 float4 per tensor: two per thread, all of a
+  // batch of 8 partials' loads in flight before the (ascending) sums
+  static_assert(QS * HD / 4 == 2 * 256, "two float4 per thread and tensor");
+  int s_in[2], f4[2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const long off = (((long)h * n_seg + seg[i + u]) * kPSlots + half[i + u] * kPBS + s_in) * HD + 4 * f4;
-        pk[u] = *reinterpret_cast<const f32x4*>(dk_part + off);
-        pv[u] = *reinterpret_cast<const f32x4*>(dv_part + off);
+  for (int cc = 0; cc < 2; ++cc) {
+    const int c = threadIdx.x + 256 * cc;
+    s_in[cc] = qtr * QS + c / (HD / 4);  // slot within the block
+    f4[cc] = c % (HD / 4);
+  }
+  f32x4 sk[2], sv[2];
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) sk[cc] = sv[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < ns; i += 8) {
+    f32x4 pk[8][2], pv[8][2];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i + u < ns) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const long off = seg_off[i + u] + (long)s_in[cc] * HD + 4 * f4[cc];
+          pk[u][cc] = *reinterpret_cast<const f32x4*>(dk_part + off);
+          pv[u][cc] = *reinterpret_cast<const f32x4*>(dv_part + off);
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sk += pk[u];
-        sv += pv[u];
+    for (int u = 0; u < 8; ++u)
+      if (i + u < ns) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          sk[cc] += pk[u][cc];
+          sv[cc] += pv[u][cc];
+        }
       }
-    }
-    for (; i < ns; ++i) {
-      const long off = (((long)h * n_seg + seg[i]) * kPSlots + half[i] * kPBS + s_in) * HD + 4 * f4;
-      sk += *reinterpret_cast<const f32x4*>(dk_part + off);
-      sv += *reinterpret_cast<const f32x4*>(dv_part + off);
-    }
+  }
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
     bf16x4 ok, ov;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      ok[u] = (__bf16)(sk[u] * dk_scale);
-      ov[u] = (__bf16)sv[u];
+      ok[u] = (__bf16)(sk[cc][u] * dk_scale);
+      ov[u] = (__bf16)sv[cc][u];
     }
-    const long dst = ((long)e * kPBS + s_in) * D + (long)h * HD + 4 * f4;
+    const long dst = ((long)e * kPBS + s_in[cc]) * D + (long)h * HD + 4 * f4[cc];
     *reinterpret_cast<bf16x4*>(dk + dst) = ok;
     *reinterpret_cast<bf16x4*>(dv + dst) = ov;
   }
@@ -851,13 +908,16 @@ int read_pair_ranges(const ReadDims& d) {
   return std::max(r, (tiles + kPairBwdMaxRange - 1) / kPairBwdMaxRange);
 }
 
+// partial segments: A (per range and block-a run: r + a) and B (per range
+// and pair: r + pair index)
+int read_pair_segments_a(const ReadDims& d) { return read_pair_ranges(d) + d.E - 1; }
 int read_pair_segments(const ReadDims& d) {
   const long N = (long)d.B * d.S;
   return read_pair_ranges(d) + pair_plan_layout(N, d.E).max_keys - 1;
 }
 
 size_t read_pair_part_bytes(const ReadDims& d) {
-  return (size_t)d.H * read_pair_segments(d) * kPSlots * kPHD * sizeof(float);
+  return (size_t)d.H * (read_pair_segments_a(d) + read_pair_segments(d)) * kPBS * kPHD * sizeof(float);
 }
 
 // the side buffer: each row's backward constants, (H, N, 4) 32-bit words
@@ -901,19 +961,20 @@ hipError_t launch_read_bwd_pair(const void* q, const void* k, const void* v, con
                                 float* dk_part, float* dv_part, const ReadDims& d, hipStream_t st) {
   const long N = (long)d.B * d.S;
   const int R = read_pair_ranges(d);
-  const int ns = read_pair_segments(d);
+  const int nsa = read_pair_segments_a(d), ns = read_pair_segments(d);
   const float alpha = (float)(1.0 / __builtin_sqrt(64.0)) * kLog2e;
   const float scale = (float)(1.0 / __builtin_sqrt(64.0));
   NAYLIS_TIMED("read_bwd_pair", st,
                hipLaunchKernelGGL(read_bwd_pair_kernel, dim3(d.H * R), dim3(512), 0, st, (const bf16_t*)q,
                                   (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)o, (const float*)side,
                                   (const bf16_t*)dout, d.order, (bf16_t*)dq, dlg_part,
-                                  dk_part, dv_part, N, d.H, d.L, d.E, alpha, scale, R, ns));
+                                  dk_part, dv_part, N, d.H, d.L, d.E, alpha, scale, R, nsa, ns));
   const int kv_blocks = d.H * d.E * 4;
   const int g_blocks = (int)std::min<long>(1024, (N * 2 + 255) / 256);
   NAYLIS_TIMED("read_bwd_reduce", st,
                hipLaunchKernelGGL(read_pair_reduce_kernel, dim3(kv_blocks + g_blocks), dim3(256), 0, st, dk_part,
-                                  dv_part, d.order, (bf16_t*)dk, (bf16_t*)dv, N, d.H, d.E, R, ns, scale, kv_blocks,
+                                  dv_part, d.order, (bf16_t*)dk, (bf16_t*)dv, N, d.H, d.E, R, nsa, ns, scale,
+                                  kv_blocks,
                                   dlg_part, top_gates, dgates));
   return hipGetLastError();
 }

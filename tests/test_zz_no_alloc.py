@@ -73,14 +73,14 @@ def test_read_bwd_noalloc_matches_workspace_entry_point(dev):
     lib = _lib.load()
     st = _lib.stream_of(dev)
     with _lib.on_device(dev):
-        # a config-2-like read (16 heads of 64, 8 blocks of 128 slots, grouped token order: the
-        # pair-tiled backward), then the config-4 read (24 heads, 32 blocks, 16384 tokens, top-2,
-        # sequence order: the two-pass backward), then a smaller, ragged one (4 heads of 32, 4
-        # blocks of 64 slots, 300 tokens): each call needs less scratch than the one before
-        cases = [_case(dev, 4, 2048, 16, 64, 8, 128, 2, seed=1, grouped=True),
-                 _case(dev, 4, 4096, 24, 64, 32, 128, 2, seed=4, grouped=False),
+        # the config-4 read (24 heads, 32 blocks, 16384 tokens, top-2, sequence order: the
+        # two-pass backward), then a config-2-like read (16 heads of 64, 8 blocks of 128 slots,
+        # grouped token order: the pair-tiled backward), then a smaller, ragged one (4 heads of
+        # 32, 4 blocks of 64 slots, 300 tokens): each call needs less scratch than the one before
+        cases = [_case(dev, 4, 4096, 24, 64, 32, 128, 2, seed=4, grouped=False),
+                 _case(dev, 4, 2048, 16, 64, 8, 128, 2, seed=1, grouped=True),
                  _case(dev, 1, 300, 4, 32, 4, 64, 2, seed=2, grouped=False)]
-        assert cases[0]["side"] is not None and cases[1]["side"] is None
+        assert cases[0]["side"] is None and cases[1]["side"] is not None
         needs = [lib.naylis_mom_read_workspace_bytes(*c["dims"]) for c in cases]
         assert 0 < needs[2] < needs[1] < needs[0] <= _max_bytes(), needs
         got = []
