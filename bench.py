@@ -134,6 +134,46 @@ def _forward_with_bias(layer, x, M, bias):
     return mom_kernels.mom_rezero(layer._read(x, idx, gates, M), layer.mom_scale)
 
 
+def torch_projection_gemms(layer, x, steps):
+    """The layer's q / o projection GEMMs that run on torch (hipBLASLt): the
+    q projection forward (model.py:251), the o projection forward with the
+    ReZero gate folded into the weight and an fp32 result (model.py:276) and
+    the two input gradients, each called as the layer calls it, on the layer's
+    own shapes and weights, timed standalone with events on the current
+    stream (the library's KernelTimer does not see torch's launches).  2 N d^2
+    FLOP each."""
+    import torch
+    import torch.nn.functional as F
+    B, T, D = x.shape
+    N = B * T
+    x2 = x.detach().reshape(N, D).to(torch.bfloat16).contiguous()
+    w_q = layer.q_proj.weight.detach()
+    w_os = (layer.o_proj.weight.detach().float() * float(layer.mom_scale.detach())).to(w_q.dtype)
+    g = torch.Generator(device=x.device).manual_seed(1)
+    a2 = torch.randn((N, D), generator=g, device=x.device).to(torch.bfloat16)
+    calls = {"q_proj_fwd": lambda: F.linear(x2, w_q),
+             "o_proj_fwd": lambda: torch.mm(a2, w_os.t(), out_dtype=torch.float32),
+             "o_proj_dgrad": lambda: torch.mm(a2, w_os),
+             "q_proj_dgrad": lambda: torch.mm(a2, w_q)}
+    out = {}
+    flop = 2.0 * N * D * D
+    for name, fn in calls.items():
+        for _ in range(3):
+            fn()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps
+        tf = flop / (us * 1e-6) / 1e12
+        out["hipblaslt_" + name] = {"us": round(us, 2), "tflops": round(tf, 1),
+                                    "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                                    "timing": "standalone, back to back, events on the current stream"}
+    return out
+
+
 def routing(layer, M, x):
     import torch
 
@@ -667,6 +707,7 @@ def main(argv=None):
     gemms = {k: {"us": round(per[k][0] * 1e3, 2), "tflops": round(alg[k] / (per[k][0] * 1e-3) / 1e12, 1),
                  "mfma_frac": round(alg[k] / (per[k][0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
              for k in ("bank_kv_fwd", "bank_kv_bwd_dslots", "bank_kv_bwd_dw", "linear_wgrad") if k in per}
+    gemms.update(torch_projection_gemms(layer, x, args.steps))
     # the prefix-mean router against HBM: forward reads x once and writes logits / probs / top-k /
     # gates / activations (plus the (N, R) projection written and read back); the backward reads x,
     # the incoming dx and writes dx (the accumulating input gradient), plus the (N, R) and (N, E)

@@ -25,7 +25,7 @@
 // histograms), the decision, and the placement of the chunk's tokens.  The
 // second launch also writes the pair plan (read_common.h): the grouped table
 // (always, whatever the decision), the keys with tokens, their 32-token tiles
-// and the forward's work items; its first workgroup writes the lists.
+// and the forward's work items; one extra workgroup writes the lists.
 #include "launch.h"
 #include "read_common.h"
 #include "timing.h"
@@ -66,10 +66,10 @@ static OrderWs plan_order_ws(long N, int E) {
 }
 
 // (1) per chunk of 1024 tokens: key = sorted block pair, rank among the
-// chunk's earlier tokens of the same key (inside a wave one ballot per
-// distinct key of the wave, per-wave key counts across waves), the chunk's
-// key histogram, and the distinct-block count of each 128-token tile in
-// sequence order.
+// chunk's earlier tokens of the same key (inside a wave the lanes with the
+// same key from one ballot per key bit, per-wave key counts across waves),
+// the chunk's key histogram, and the distinct-block count of each 128-token
+// tile in sequence order.
 __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* __restrict__ top_idx,
                                                                 uint16_t* __restrict__ keys, int32_t* __restrict__ rank,
                                                                 int32_t* __restrict__ hist,
@@ -90,20 +90,23 @@ __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* _
     if (b0 >= 0 && b0 < E) mask |= 1u << b0;
   }
   for (int i = tid; i < kOrdWaves * nkeys; i += kOrdChunk) wcnt[i / nkeys][i % nkeys] = 0;
-  // lanes of this wave with the same key, below and above this lane: one
-  // round per distinct key, led by the lowest lane not yet matched
+  // lanes of this wave with the same key, below and above this lane: the
+  // real lanes that agree with this lane's key on every bit (one ballot per
+  // bit of a key)
   int before = 0, after = 0;
-  const uint64_t below = (1ull << lane) - 1;
-  uint64_t rem = __ballot(real);
-  while (rem) {
-    const int lead = __builtin_ctzll(rem);
-    const int k = __builtin_amdgcn_readlane(key, lead);
-    const uint64_t m = __ballot(real && key == k);
-    if (real && key == k) {
+  {
+    const uint64_t below = (1ull << lane) - 1;
+    uint64_t m = __ballot(real);
+    const int nb = 32 - __clz(max(nkeys - 1, 1));
+    for (int bit = 0; bit < nb; ++bit) {
+      const bool on = real && ((key >> bit) & 1);
+      const uint64_t bm = __ballot(on);
+      m &= on ? bm : ~bm;
+    }
+    if (real) {
       before = __popcll(m & below);
       after = __popcll(m & ~below) - 1;
     }
-    rem &= ~m;
   }
   for (int o = 32; o > 0; o >>= 1) mask |= __shfl_xor(mask, o, 64);
   if (lane == 0) wmask[wave] = mask;
@@ -130,18 +133,36 @@ __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* _
   }
 }
 
-// Inclusive scan of x over the first n threads of the workgroup (n <= 1024),
-// in LDS array a; every thread of the workgroup must call it.
-__device__ __forceinline__ void block_scan_incl(int32_t* a, int n, int x) {
-  const int tid = threadIdx.x;
-  if (tid < n) a[tid] = x;
-  __syncthreads();
-  for (int st = 1; st < n; st <<= 1) {
-    const int add = (tid < n && tid >= st) ? a[tid - st] : 0;
-    __syncthreads();
-    if (tid < n) a[tid] += add;
-    __syncthreads();
+// Inclusive scans of two values over threads 0..n-1 of the workgroup (n <=
+// 1024; threads from n on add 0): a scan inside each wave, then the wave
+// totals through LDS (two barriers).  Every thread of the workgroup must call
+// it; `tot` gets the two totals.
+__device__ __forceinline__ int2 block_scan2(int x, int y, int n, int2* wsum, int2& tot) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (int)(blockDim.x >> 6);
+  int a = tid < n ? x : 0, b = tid < n ? y : 0;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ua = __shfl_up(a, o, 64), ub = __shfl_up(b, o, 64);
+    if (lane >= o) {
+      a += ua;
+      b += ub;
+    }
   }
+  if (lane == 63) wsum[wave] = make_int2(a, b);
+  __syncthreads();
+  int2 add = make_int2(0, 0), t = make_int2(0, 0);
+  for (int w = 0; w < nw; ++w) {
+    const int2 s = wsum[w];
+    if (w < wave) {
+      add.x += s.x;
+      add.y += s.y;
+    }
+    t.x += s.x;
+    t.y += s.y;
+  }
+  __syncthreads();  // (wsum free for the next scan)
+  tot = t;
+  return make_int2(a + add.x, b + add.y);
 }
 
 // Largest i in [0, n) with a[i] <= x (a ascending, a[0] <= x).
@@ -154,12 +175,13 @@ __device__ __forceinline__ int last_le(const int32_t* a, int n, int x) {
   return lo;
 }
 
-// The pair plan (layout in read_common.h), written by one workgroup of the
-// scatter launch from the key totals (`all` of thread t = tokens of key t,
-// ends / nzs the inclusive scans of the totals and of "key has tokens").
-__device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int nkeys, int all,
-                                const int32_t* ends, const int32_t* nzs, int32_t* tsc, int32_t* fsc, int32_t* ktile,
-                                int32_t* kfit, int32_t* kpos, int32_t* kcnt, int32_t* kab) {
+// The pair plan (layout in read_common.h), written by the scatter launch's
+// last workgroup from the key totals: thread t holds key t's token count
+// `all`, the inclusive scans `end` (of the counts) and `nz` (of "key has
+// tokens") at key t, and nnz (keys with tokens).
+__device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int nkeys, int all, int end, int nz,
+                                int nnz, int2* wsum, int32_t* ktile, int32_t* kfit, int32_t* kpos, int32_t* kcnt,
+                                int32_t* kab) {
   const PairPlanLayout pl = pair_plan_layout(N, E);
   int32_t* hdr = order + pl.hdr;
   int32_t* kl = order + pl.keys;
@@ -168,24 +190,23 @@ __device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int 
   const int tid = threadIdx.x;
   const int nt = tid < nkeys ? (all + kPairTile - 1) / kPairTile : 0;
   const int nf = (nt + kPairFwdItem - 1) / kPairFwdItem;
-  block_scan_incl(tsc, nkeys, nt);
-  block_scan_incl(fsc, nkeys, nf);
+  int2 tot;
+  const int2 sc = block_scan2(nt, nf, nkeys, wsum, tot);  // tiles, forward items
   if (tid < nkeys && all > 0) {
-    const int k = nzs[tid] - 1;
+    const int k = nz - 1;
     const int a = tid / E, b = tid % E;
-    ktile[k] = tsc[tid] - nt;
-    kfit[k] = fsc[tid] - nf;
-    kpos[k] = ends[tid] - all;
+    ktile[k] = sc.x - nt;
+    kfit[k] = sc.y - nf;
+    kpos[k] = end - all;
     kcnt[k] = all;
     kab[k] = a | (b << 5);
     kl[4 * k + 0] = a;
     kl[4 * k + 1] = b;
-    kl[4 * k + 2] = tsc[tid] - nt;
+    kl[4 * k + 2] = sc.x - nt;
     kl[4 * k + 3] = nt;
   }
   __syncthreads();
-  const int nnz = nzs[nkeys - 1];
-  const int n_tiles = tsc[nkeys - 1], n_fit = fsc[nkeys - 1];
+  const int n_tiles = tot.x, n_fit = tot.y;
   if (tid == 0) {
     hdr[0] = n_tiles;
     hdr[1] = nnz;
@@ -216,29 +237,35 @@ __device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int 
 // block pairs of the keys whose segments overlap it, which the offsets give
 // exactly.  Grouping is kept when it lowers the (tile, block) pairs by at
 // least 10 %: then the mode word order[0] = 1, otherwise 0.  The table
-// order[1 + offset + rank] = token is written when grouping is kept or when
-// the pair plan is (write_plan), which the first workgroup adds.
+// order[1 + offset + rank] = token is written either way (the pair plan
+// indexes it).  One workgroup more than the chunks writes the pair plan, in
+// parallel with them.
 __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t* __restrict__ keys,
                                                                   const int32_t* __restrict__ rank,
                                                                   const int32_t* __restrict__ hist,
                                                                   const int32_t* __restrict__ seqcnt,
                                                                   int32_t* __restrict__ order, long N, int E,
-                                                                  int nchunks, bool write_plan) {
+                                                                  int nchunks) {
   __shared__ int32_t off[kOrdMaxE * kOrdMaxE];
-  __shared__ int32_t ends[kOrdMaxE * kOrdMaxE];  // inclusive scan of the key totals
-  __shared__ int32_t nzs[kOrdMaxE * kOrdMaxE];   // inclusive scan of "key has tokens"
   __shared__ int32_t cend[kOrdMaxE * kOrdMaxE];  // the keys with tokens, ascending: segment end
   __shared__ uint32_t cmask[kOrdMaxE * kOrdMaxE];  // and block pair mask
+  __shared__ int2 wsum[kOrdWaves];
   __shared__ long red[2][kOrdWaves];
-  // pair plan (first workgroup): inclusive scans over keys of their tiles and
-  // forward items, and per key with tokens (ascending) its first tile, first
-  // item, first position, token count and blocks
-  __shared__ int32_t tsc[kOrdMaxE * kOrdMaxE], fsc[kOrdMaxE * kOrdMaxE];
+  // pair plan (last workgroup): per key with tokens (ascending) its first
+  // tile, first item, first position, token count and blocks
   __shared__ int32_t ktile[kOrdMaxE * kOrdMaxE], kfit[kOrdMaxE * kOrdMaxE], kpos[kOrdMaxE * kOrdMaxE];
   __shared__ int32_t kcnt[kOrdMaxE * kOrdMaxE], kab[kOrdMaxE * kOrdMaxE];
   const int nkeys = E * E;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x;
+  // this thread's token and the first tile count of the decision, loaded
+  // before the scans so their latency is hidden
+  const long ntiles = (N + kOrdTile - 1) / kOrdTile;
+  const long tok = (long)c * kOrdChunk + tid;
+  const bool tok_ok = c < nchunks && tok < N;
+  const int my_key = tok_ok ? (int)keys[tok] : 0;
+  const int my_rank = tok_ok ? rank[tok] : 0;
+  const int seq0 = (c < nchunks && tid < ntiles) ? seqcnt[tid] : 0;
   int before = 0, all = 0;
   if (tid < nkeys) {
     for (int c0 = 0; c0 < nchunks; c0 += 16) {  // 16 independent loads in flight
@@ -251,37 +278,27 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
         before += (c0 + u < c) ? h[u] : 0;
       }
     }
-    ends[tid] = all;
-    nzs[tid] = all > 0;
   }
-  __syncthreads();
-  for (int st = 1; st < nkeys; st <<= 1) {  // inclusive scans over keys
-    int add = 0, addn = 0;
-    if (tid < nkeys && tid >= st) {
-      add = ends[tid - st];
-      addn = nzs[tid - st];
-    }
-    __syncthreads();
-    if (tid < nkeys) {
-      ends[tid] += add;
-      nzs[tid] += addn;
-    }
-    __syncthreads();
+  // inclusive scans over keys of the totals and of "key has tokens"
+  int2 tot;
+  const int2 sc = block_scan2(all, all > 0 ? 1 : 0, nkeys, wsum, tot);
+  const int nnz = tot.y;
+  if (c == nchunks) {
+    write_pair_plan(order, N, E, nkeys, all, sc.x, sc.y, nnz, wsum, ktile, kfit, kpos, kcnt, kab);
+    return;
   }
   if (tid < nkeys) {
-    off[tid] = ends[tid] - all + before;
+    off[tid] = sc.x - all + before;
     if (all > 0) {
-      cend[nzs[tid] - 1] = ends[tid];
-      cmask[nzs[tid] - 1] = (1u << (tid / E)) | (1u << (tid % E));
+      cend[sc.y - 1] = sc.x;
+      cmask[sc.y - 1] = (1u << (tid / E)) | (1u << (tid % E));
     }
   }
   __syncthreads();
-  const int nnz = nzs[nkeys - 1];
   // (tile, block) pairs of both orders
-  const long ntiles = (N + kOrdTile - 1) / kOrdTile;
   long seq = 0, grp = 0;
   for (long t = tid; t < ntiles; t += kOrdChunk) {
-    seq += seqcnt[t];
+    seq += t == tid ? seq0 : seqcnt[t];
     const long p0 = t * kOrdTile, p1 = min(N, p0 + kOrdTile);
     // the keys with tokens tile [0, N) in order: from the first whose
     // segment ends after p0, those that start before p1
@@ -310,10 +327,8 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
   }
   const bool grouped = g_all * 10 <= s_all * 9;
   if (c == 0 && tid == 0) order[0] = grouped ? 1 : 0;  // the mode word
-  if (write_plan && c == 0) write_pair_plan(order, N, E, nkeys, all, ends, nzs, tsc, fsc, ktile, kfit, kpos, kcnt, kab);
-  const long tok = (long)c * kOrdChunk + tid;
-  if (tok >= N || !(grouped || write_plan)) return;
-  const long dst = (long)off[keys[tok]] + rank[tok];
+  if (!tok_ok) return;
+  const long dst = (long)off[my_key] + my_rank;
   if (dst >= 0 && dst < N) order[1 + dst] = (int32_t)tok;
 }
 
@@ -350,8 +365,8 @@ hipError_t launch_read_order(const int32_t* top_idx, long N, int E, int topk, in
                hipLaunchKernelGGL(order_local_kernel, dim3(nchunks), dim3(kOrdChunk), 0, st, top_idx, keys, rank, hist,
                                   seqcnt, N, E));
   NAYLIS_TIMED("read_order", st,
-               hipLaunchKernelGGL(order_scatter_kernel, dim3(nchunks), dim3(kOrdChunk), 0, st, keys, rank, hist,
-                                  seqcnt, order, N, E, nchunks, true));
+               hipLaunchKernelGGL(order_scatter_kernel, dim3(nchunks + 1), dim3(kOrdChunk), 0, st, keys, rank,
+                                  hist, seqcnt, order, N, E, nchunks));
   return hipGetLastError();
 }
 

@@ -597,10 +597,11 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
       acc_p = mfma32(ad, vf[ks], acc_p);
     }
   };
-  // ---- S2(t): P, dS; dV^T += dO^T P, dK^T += Q^T dS, each weight as bf16
-  // plus its bf16 remainder (two products: ~2^-16 relative, where bf16 alone
-  // leaves 2^-9 per term in sums over thousands of tokens); dS^T (both parts)
-  // to LDS for S3
+  // ---- S2(t): P, dS; dV^T += dO^T P with P as bf16 plus its bf16 remainder
+  // (two products: ~2^-16 relative; bf16 P alone, all terms of one sign,
+  // leaves 2^-9 per term in sums over thousands of tokens), dK^T += Q^T dS
+  // with bf16 dS (terms of both signs); dS^T and its remainder to LDS for S3
+  // (dQ takes the bf16 part, the gate sums both)
   auto s2 = [&](int t, auto par) {
     constexpr int B2 = decltype(par)::value;
     const int qb = qbuf(t);
@@ -626,7 +627,7 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
         const bf16x8 a_do = lds_frag_T<true, true>(do_lds[qb], PITCH, 16 * kk, 32 * j);
         const bf16x8 a_q = lds_frag_T<true, true>(q_lds[qb], PITCH, 16 * kk, 32 * j);
         acc_dv[j] = mfma32(a_do, bpl, mfma32(a_do, bp, acc_dv[j]));
-        acc_dk[j] = mfma32(a_q, bdl, mfma32(a_q, bd, acc_dk[j]));
+        acc_dk[j] = mfma32(a_q, bd, acc_dk[j]);
       }
       // registers 8 kk .. 8 kk + 7 are tokens 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3
       const uint4 u = __builtin_bit_cast(uint4, bd), ul = __builtin_bit_cast(uint4, bdl);
