@@ -65,6 +65,32 @@ static OrderWs plan_order_ws(long N, int E) {
   return w;
 }
 
+// Key of a top-2 selection (the sorted block pair of the clamped ids) and
+// the mask of its valid ids.
+__device__ __forceinline__ int pair_key(int a0, int b0, int E, uint32_t& mask) {
+  const int a = min(max(a0, 0), E - 1), b = min(max(b0, 0), E - 1);
+  mask = 0;
+  if (a0 >= 0 && a0 < E) mask |= 1u << a0;
+  if (b0 >= 0 && b0 < E) mask |= 1u << b0;
+  return a < b ? a * E + b : b * E + a;
+}
+
+// Lanes of this wave with this lane's key, below and above this lane: the
+// real lanes that agree with it on every key bit (one ballot per bit).
+__device__ __forceinline__ void same_key_lanes(bool real, int key, int nkeys, int& before, int& after) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = (1ull << lane) - 1;
+  uint64_t m = __ballot(real);
+  const int nb = 32 - __clz(max(nkeys - 1, 1));
+  for (int bit = 0; bit < nb; ++bit) {
+    const bool on = real && ((key >> bit) & 1);
+    const uint64_t bm = __ballot(on);
+    m &= on ? bm : ~bm;
+  }
+  before = real ? __popcll(m & below) : 0;
+  after = real ? __popcll(m & ~below) - 1 : 0;
+}
+
 // (1) per chunk of 1024 tokens: key = sorted block pair, rank among the
 // chunk's earlier tokens of the same key (inside a wave the lanes with the
 // same key from one ballot per key bit, per-wave key counts across waves),
@@ -82,32 +108,10 @@ __global__ __launch_bounds__(kOrdChunk) void order_local_kernel(const int32_t* _
   const bool real = tok < N;
   int key = -1;
   uint32_t mask = 0;
-  if (real) {
-    const int a0 = top_idx[tok * 2], b0 = top_idx[tok * 2 + 1];
-    const int a = min(max(a0, 0), E - 1), b = min(max(b0, 0), E - 1);
-    key = a < b ? a * E + b : b * E + a;
-    if (a0 >= 0 && a0 < E) mask |= 1u << a0;
-    if (b0 >= 0 && b0 < E) mask |= 1u << b0;
-  }
+  if (real) key = pair_key(top_idx[tok * 2], top_idx[tok * 2 + 1], E, mask);
   for (int i = tid; i < kOrdWaves * nkeys; i += kOrdChunk) wcnt[i / nkeys][i % nkeys] = 0;
-  // lanes of this wave with the same key, below and above this lane: the
-  // real lanes that agree with this lane's key on every bit (one ballot per
-  // bit of a key)
-  int before = 0, after = 0;
-  {
-    const uint64_t below = (1ull << lane) - 1;
-    uint64_t m = __ballot(real);
-    const int nb = 32 - __clz(max(nkeys - 1, 1));
-    for (int bit = 0; bit < nb; ++bit) {
-      const bool on = real && ((key >> bit) & 1);
-      const uint64_t bm = __ballot(on);
-      m &= on ? bm : ~bm;
-    }
-    if (real) {
-      before = __popcll(m & below);
-      after = __popcll(m & ~below) - 1;
-    }
-  }
+  int before, after;
+  same_key_lanes(real, key, nkeys, before, after);
   for (int o = 32; o > 0; o >>= 1) mask |= __shfl_xor(mask, o, 64);
   if (lane == 0) wmask[wave] = mask;
   __syncthreads();
@@ -231,6 +235,50 @@ __device__ void write_pair_plan(int32_t* __restrict__ order, long N, int E, int 
   }
 }
 
+// (tile, block) pairs of this thread's 128-token tiles in the grouped order:
+// the keys with tokens tile [0, N) in ascending order (segment ends cend,
+// block pair masks cmask); a tile's blocks are those of the keys whose
+// segments overlap it.
+__device__ __forceinline__ long grouped_pairs(long N, int nnz, const int32_t* cend, const uint32_t* cmask) {
+  const long ntiles = (N + kOrdTile - 1) / kOrdTile;
+  long grp = 0;
+  for (long t = threadIdx.x; t < ntiles; t += blockDim.x) {
+    const long p0 = t * kOrdTile, p1 = min(N, p0 + kOrdTile);
+    // from the first key whose segment ends after p0, those that start before p1
+    int lo = 0, hi = nnz - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (cend[mid] > p0) hi = mid; else lo = mid + 1;
+    }
+    uint32_t mask = 0;
+    for (int i = lo; i < nnz && (i == 0 ? 0 : cend[i - 1]) < p1; ++i) mask |= cmask[i];
+    grp += __popc(mask);
+  }
+  return grp;
+}
+
+// The decision from every thread's sequence-order and grouped-order pair
+// counts (summed over the workgroup): grouping is kept when it lowers the
+// pairs by at least 10 %.  Every thread of the workgroup must call it.
+__device__ __forceinline__ bool keep_grouping(long seq, long grp, long (*red)[kOrdWaves]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
+  for (int o = 32; o > 0; o >>= 1) {
+    seq += __shfl_xor(seq, o, 64);
+    grp += __shfl_xor(grp, o, 64);
+  }
+  if (lane == 0) {
+    red[0][wave] = seq;
+    red[1][wave] = grp;
+  }
+  __syncthreads();
+  long s_all = 0, g_all = 0;
+  for (int w = 0; w < nw; ++w) {
+    s_all += red[0][w];
+    g_all += red[1][w];
+  }
+  return g_all * 10 <= s_all * 9;
+}
+
 // (2) per chunk: key offsets = (tokens of smaller keys) + (tokens of the same
 // key in earlier chunks).  Every workgroup also evaluates the decision from
 // the same data: in the grouped order a tile's blocks are the union of the
@@ -256,7 +304,7 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
   __shared__ int32_t ktile[kOrdMaxE * kOrdMaxE], kfit[kOrdMaxE * kOrdMaxE], kpos[kOrdMaxE * kOrdMaxE];
   __shared__ int32_t kcnt[kOrdMaxE * kOrdMaxE], kab[kOrdMaxE * kOrdMaxE];
   const int nkeys = E * E;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int c = blockIdx.x;
   // this thread's token and the first tile count of the decision, loaded
   // before the scans so their latency is hidden
@@ -296,36 +344,9 @@ __global__ __launch_bounds__(kOrdChunk) void order_scatter_kernel(const uint16_t
   }
   __syncthreads();
   // (tile, block) pairs of both orders
-  long seq = 0, grp = 0;
-  for (long t = tid; t < ntiles; t += kOrdChunk) {
-    seq += t == tid ? seq0 : seqcnt[t];
-    const long p0 = t * kOrdTile, p1 = min(N, p0 + kOrdTile);
-    // the keys with tokens tile [0, N) in order: from the first whose
-    // segment ends after p0, those that start before p1
-    int lo = 0, hi = nnz - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (cend[mid] > p0) hi = mid; else lo = mid + 1;
-    }
-    uint32_t mask = 0;
-    for (int i = lo; i < nnz && (i == 0 ? 0 : cend[i - 1]) < p1; ++i) mask |= cmask[i];
-    grp += __popc(mask);
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    seq += __shfl_xor(seq, o, 64);
-    grp += __shfl_xor(grp, o, 64);
-  }
-  if (lane == 0) {
-    red[0][wave] = seq;
-    red[1][wave] = grp;
-  }
-  __syncthreads();
-  long s_all = 0, g_all = 0;
-  for (int w = 0; w < kOrdWaves; ++w) {
-    s_all += red[0][w];
-    g_all += red[1][w];
-  }
-  const bool grouped = g_all * 10 <= s_all * 9;
+  long seq = 0;
+  for (long t = tid; t < ntiles; t += kOrdChunk) seq += t == tid ? seq0 : seqcnt[t];
+  const bool grouped = keep_grouping(seq, grouped_pairs(N, nnz, cend, cmask), red);
   if (c == 0 && tid == 0) order[0] = grouped ? 1 : 0;  // the mode word
   if (!tok_ok) return;
   const long dst = (long)off[my_key] + my_rank;

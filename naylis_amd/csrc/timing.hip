@@ -67,13 +67,17 @@ ScopedKernelTimer::ScopedKernelTimer(const char* name, hipStream_t st) : name_(n
   std::lock_guard<std::mutex> lk(g_mu);
   start_ = take_event();
   stop_ = take_event();
-  if (start_ && stop_) (void)hipEventRecord(start_, st_);
+  if (!start_ || !stop_) {  // timing off for this launch; return what was taken
+    if (start_) g_pool.push_back(start_);
+    if (stop_) g_pool.push_back(stop_);
+    start_ = stop_ = nullptr;
+  }
 }
 
+// (the launch inside NAYLIS_TIMED recorded both events with the kernel)
 ScopedKernelTimer::~ScopedKernelTimer() {
   if (!start_ || !stop_) return;
   std::lock_guard<std::mutex> lk(g_mu);
-  (void)hipEventRecord(stop_, st_);
   g_pending.push_back({name_, start_, stop_});
 }
 

@@ -96,6 +96,9 @@ def check_pair_plan(buf, top_idx, E):
     (8, 2048, 8, 2, False),    # config 2 geometry, incoherent routing: grouping pays
     (4, 4096, 32, 2, True),    # config 4 style: one block set per 128-token tile, sequence order kept
     (4, 4096, 32, 2, False),   # 32 blocks, incoherent: hundreds of keys, many of them empty
+    (2, 16384, 8, 2, False),   # 32 chunks of 1024 tokens
+    (1, 20000, 32, 2, False),  # 32 blocks, a ragged last chunk
+    (3, 4096, 32, 2, True),    # coherent, three sequences: sequence order kept
     (2, 300, 8, 2, False),     # ragged token count
     (2, 300, 8, 3, False),     # top-3: sequence order
     (1, 1000, 64, 2, False),   # more than 32 blocks: sequence order
