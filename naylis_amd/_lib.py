@@ -108,7 +108,9 @@ def load():
                 f"naylis_amd: HIP library not built ({LIB_PATH} missing). "
                 "Run `python -c 'import __graft_entry__ as g; g.build()'` or "
                 "`python -m naylis_amd.build` first.")
-        lib = ctypes.CDLL(LIB_PATH)
+        # global visibility: the torch extension of the fused layer node
+        # (naylis_amd/_torch_ext.py) binds its calls to this instance
+        lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = res

@@ -1,4 +1,5 @@
-"""Build libnaylis_mom.so (gfx950) in-tree with hipcc.
+"""Build libnaylis_mom.so (gfx950) in-tree with hipcc, then the torch
+extension of the fused layer node over it.
 
     python -m naylis_amd.build [--jobs N]
 
@@ -6,7 +7,10 @@ Each .hip source is compiled to an object in parallel, then linked into
 ``naylis_amd/_lib/libnaylis_mom.so``.  Flags: -O3, gfx950 only, packed fp32
 instructions disabled (``-Xclang -target-feature -Xclang -packed-fp32-ops``),
 correctly rounded fp32 division (the router's prefix mean divides in fp32
-exactly as the reference does).
+exactly as the reference does).  ``csrc/torch_layer.cpp`` becomes
+``naylis_amd/_lib/ext/naylis_torch.so`` (torch.utils.cpp_extension, host
+code only); it calls the library's C ABI, whose symbols it takes from the
+library loaded first with global visibility.
 """
 from __future__ import annotations
 
@@ -22,6 +26,10 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 OBJ_DIR = os.path.join(OUT_DIR, "obj")
 LIB = os.path.join(OUT_DIR, "libnaylis_mom.so")
+EXT_DIR = os.path.join(OUT_DIR, "ext")
+EXT_NAME = "naylis_torch"
+EXT = os.path.join(EXT_DIR, EXT_NAME + ".so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -41,6 +49,26 @@ def hipcc():
 
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build_torch_ext(verbose=False):
+    """Compile csrc/torch_layer.cpp into the torch extension (every time: the
+    previous outputs are removed first)."""
+    import ctypes
+
+    import torch.utils.cpp_extension as ce
+    os.makedirs(EXT_DIR, exist_ok=True)
+    for f in os.listdir(EXT_DIR):
+        if f.endswith((".o", ".so")):
+            os.remove(os.path.join(EXT_DIR, f))
+    # cpp_extension imports the module it built: its C-ABI symbols come from
+    # the library, loaded here with global visibility as naylis_amd._lib does
+    ctypes.CDLL(LIB, mode=ctypes.RTLD_GLOBAL)
+    ce.load(name=EXT_NAME, sources=[os.path.join(CSRC, "torch_layer.cpp")], build_directory=EXT_DIR,
+            extra_include_paths=[INCLUDE], extra_cflags=["-O2"], verbose=verbose)
+    if not os.path.exists(EXT):
+        raise RuntimeError(f"torch extension build produced no {EXT}")
+    return EXT
 
 
 def _compile(src):
@@ -72,6 +100,7 @@ def build(jobs=None, verbose=False):
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_torch_ext(verbose)
     return LIB
 
 

@@ -16,19 +16,28 @@ in fp32 and gets dW_o = s dW' and ds = sum(dW' W_o) from one pass over the
 weight.  Results equal the modular path's to bf16 rounding (W' is rounded
 where the modular path rounds o W_o^T); the modular Functions stay the
 public drop-in API (mom_read etc.) and serve gradient checkpointing.
+
+The node's host work -- about fifteen library and torch calls each way --
+runs in C++ (the torch extension of csrc/torch_layer.cpp, one call per
+direction) when ``USE_TORCH_EXT`` is set, as it is by default; the Python
+statement of the same calls below stays as its specification and for the
+tests that compare the two bitwise.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
 
-from .. import _lib
+from .. import _lib, _torch_ext
 from .hip_linear import library_wgrad as _wgrad
 from .hip_read import _ptr, read_order, read_side
 from .hip_rezero import gated_linear_backward, gated_linear_forward
 from .hip_router import d_probs_arg
 
 _F32, _BF16 = 0, 1
+
+# run the node's host side in the torch extension (one C++ call per direction)
+USE_TORCH_EXT = True
 
 
 def _ws(nbytes, dev):
@@ -75,6 +84,18 @@ class MomLayerFunction(torch.autograd.Function):
         dev = x.device
         st = _lib.stream_of(dev)
         x = x.contiguous()
+        if USE_TORCH_EXT:
+            (y, probs, top_idx, act, gates, slots, k, v, q, order, out, side, lse, w_os) = _torch_ext.load().layer_fwd(
+                x, M_blocks if k_ext is None else None, w_down, w_up, w_q, w_k, w_v, w_o, scale, noise,
+                float(noise_scale), n_heads, num_blocks, block_size, top_k, int(noise_kind), k_ext, v_ext, st)
+            ctx.save_for_backward(x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v,
+                                  q, order, out, side, lse, w_os)
+            ctx.geom = geom
+            ctx.external_bank = k_ext is not None
+            ctx.m_shape = None if k_ext is not None else (tuple(M_blocks.shape), M_blocks.dtype)
+            ctx.mark_non_differentiable(top_idx)
+            ctx.set_materialize_grads(False)
+            return y, probs, top_idx
         f32 = dict(device=dev, dtype=torch.float32)
         with _lib.on_device(dev):
             # ---- router (model.py:169-220)
@@ -140,6 +161,14 @@ class MomLayerFunction(torch.autograd.Function):
         st = _lib.stream_of(dev)
         f32 = dict(device=dev, dtype=torch.float32)
         N = B * T
+        if USE_TORCH_EXT:
+            m_shape, m_dtype = ctx.m_shape if ctx.m_shape is not None else ((), None)
+            (dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds, dk_ext, dv_ext) = _torch_ext.load().layer_bwd(
+                dy, d_probs, x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q,
+                order, out, side, lse, w_os, n_heads, num_blocks, block_size, top_k, ctx.external_bank,
+                list(m_shape), m_dtype == torch.bfloat16, st)
+            return (dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds.view(scale.shape), None, None, None, dk_ext,
+                    dv_ext)
         with _lib.on_device(dev):
             # ---- o projection with the folded gate (d out, dW_o, ds)
             if dy is None:

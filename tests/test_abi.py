@@ -38,6 +38,14 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
 
 
+def test_torch_extension_loads(lib):
+    """The fused layer node's torch extension (csrc/torch_layer.cpp) loads
+    against the library and exports its two calls (no device work)."""
+    from naylis_amd import _torch_ext
+    ext = _torch_ext.load()
+    assert callable(ext.layer_fwd) and callable(ext.layer_bwd)
+
+
 def test_abi_version(lib):
     assert lib.naylis_mom_abi_version() == _lib.ABI_VERSION
 

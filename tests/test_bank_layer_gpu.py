@@ -179,6 +179,60 @@ def test_layer_fused_node_matches_modular(dev, monkeypatch):
     assert float(err.max()) <= 2.0 ** -7 * scale, (float(err.max()), scale)
 
 
+EXT_CASES = [
+    # B, S, D, H, NB, BS, K, R, bank dtype, external bank, router noise
+    (2, 256, 256, 4, 8, 128, 2, 32, torch.bfloat16, False, False),  # pair-tiled read, bf16 bank
+    (2, 256, 256, 4, 8, 128, 2, 32, torch.float32, False, True),    # fp32 bank gradient, uniform noise (Gumbel)
+    (2, 256, 256, 4, 8, 128, 2, 32, torch.bfloat16, True, False),   # bank K/V from the caller
+    (1, 131, 256, 2, 4, 64, 2, 16, torch.bfloat16, False, False),   # 131 tokens: the unsplit weight gradients
+]
+
+
+@pytest.mark.parametrize("case", EXT_CASES, ids=[f"case{i}" for i in range(len(EXT_CASES))])
+def test_layer_torch_ext_matches_python_node(case, dev, monkeypatch):
+    """The fused node's host side in C++ (csrc/torch_layer.cpp, one extension
+    call per direction) against its Python statement (the same library and
+    torch calls through ctypes): output, probs, routing and every gradient
+    bitwise equal, with the aux loss reaching the router through the probs."""
+    import naylis_amd.layer as layer_mod
+    from naylis_amd import mom_kernels
+    from naylis_amd.mom_kernels import hip_layer
+    B, S, D, H, NB, BS, K, R, m_dtype, external, noise = case
+    res = []
+    for use_ext in (True, False):
+        monkeypatch.setattr(hip_layer, "USE_TORCH_EXT", use_ext)
+        layer, _, M = build_pair(D, H, NB, BS, K, R, seed=31)
+        ld = layer.to(dev)
+        for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
+            lin.to(torch.bfloat16)
+        ld.train()
+        ld.noise_scale = 1.0 if noise else 0.0
+        g = torch.Generator().manual_seed(6)
+        x = torch.randn(B, S, D, generator=g).bfloat16().to(dev).requires_grad_(True)
+        dy = torch.randn(B, S, D, generator=g).to(dev)
+        Md = M.to(m_dtype).to(dev).requires_grad_(True)
+        torch.manual_seed(77)  # the router's noise draw
+        torch.cuda.manual_seed(77)
+        if external:
+            kv = mom_kernels.mom_bank_kv_grouped(Md, [ld.k_proj.weight], [ld.v_proj.weight], mem_slots=NB * BS)[0]
+            y = ld(x, Md, kv)
+        else:
+            y = ld(x, Md)
+        idx = ld.last_top_idx.clone()  # (the aux loss consumes the layer's routing record)
+        aux = layer_mod.mom_aux_loss([ld])
+        (y * dy).sum().add(aux).backward()
+        res.append((y.detach(), idx, x.grad.clone(), Md.grad.clone(),
+                    {n: p.grad.clone() for n, p in ld.named_parameters() if p.grad is not None}))
+    (y0, i0, x0, m0, g0), (y1, i1, x1, m1, g1) = res
+    assert torch.equal(i0, i1)
+    assert torch.equal(y0, y1)
+    assert torch.equal(x0, x1)
+    assert torch.equal(m0, m1)
+    assert g0.keys() == g1.keys()
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+
+
 @pytest.mark.parametrize("n,L,D", [(3, 1024, 1024), (20, 1024, 1024), (25, 512, 256)])
 def test_bank_kv_grouped_matches_per_layer(n, L, D, dev):
     """The grouped projection of n layers that read one bank (the decoder's
