@@ -101,12 +101,12 @@ __device__ __forceinline__ float pair_bias(int i0, int i1, float l0, float l1, i
 }  // namespace
 
 // ------------------------------------------------------------------ forward
-// Persistent workgroups of 4 waves over equal ranges of the head-major list
-// of (head, work item), an item being up to 4 consecutive tiles of one pair
+// Persistent workgroups of 4 waves over ranges of the head-major list of
+// (head, work item), an item being up to 4 consecutive tiles of one pair
 // (tile w for wave w): the 8 XCDs take one contiguous share each (the
 // hardware deals workgroup i to XCD i % 8, so an L2 holds the K / V and q
-// columns of about H / 8 heads) and workgroup j of an XCD a contiguous piece
-// of that share.  The pair's K / V rows are staged in LDS when the (head,
+// columns of about H / 8 heads), cut into equal pieces per CU of the XCD and
+// each piece into the contiguous ranges of that CU's two workgroups.  The pair's K / V rows are staged in LDS when the (head,
 // pair) changes from one item to the next; the waves then run through the
 // pair's items without synchronising.  Per tile (32 tokens; lane column =
 // token) a wave forms S^T = K Q^T for all of the pair's slots (eight 32-slot
@@ -136,10 +136,25 @@ __global__ __launch_bounds__(256, 2) void read_fwd_pair_kernel(
   const int n_fit = plan[pl.hdr + 2];
   const long T = (long)H * n_fit;
   const int G = gridDim.x, xcd = blockIdx.x & 7, gw = G >> 3, lw = blockIdx.x >> 3;
+  // Two workgroups share a CU (workgroups j and j + gw / 2 of an XCD), and
+  // the older one wins the issue arbitration, so a CU's time is that of its
+  // two ranges together: the XCD share is cut into equal shares per CU, each
+  // split between its two workgroups (the first taking the odd item).
   const long s0 = T * xcd / 8, sn = T * (xcd + 1) / 8 - s0;
-  const int u0 = (int)(s0 + sn * lw / gw);
-  // (the host sizes the grid so a range fits kPairFwdMaxRange)
-  const int u1 = (int)std::min<long>(s0 + sn * (lw + 1) / gw, (long)u0 + kPairFwdMaxRange);
+  long c0, c1;
+  if (gw >= 2 && (gw & 1) == 0) {
+    const int half = gw >> 1, cu = lw % half;
+    const long a0 = s0 + sn * cu / half, a1 = s0 + sn * (cu + 1) / half, am = a0 + (a1 - a0 + 1) / 2;
+    c0 = lw < half ? a0 : am;
+    c1 = lw < half ? am : a1;
+  } else {
+    c0 = s0 + sn * lw / gw;
+    c1 = s0 + sn * (lw + 1) / gw;
+  }
+  const int u0 = (int)c0;
+  // (the host sizes the grid so a range fits kPairFwdMaxRange: a CU's share
+  // is at most 2 kPairFwdMaxRange items)
+  const int u1 = (int)std::min<long>(c1, (long)u0 + kPairFwdMaxRange);
   if (u0 >= u1) return;  // uniform over the workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, col = lane & 31;
   const int D = H * HD;
