@@ -110,7 +110,11 @@ def layer_step(layer, M, x, dy):
     else:
         y = _forward_with_bias(layer, x, M, bias)
     y.backward(dy)
-    for p in layer.parameters():
+    # the gradient reset (the step's end): the parameter list is taken once
+    params = layer.__dict__.get("_bench_params")
+    if params is None:
+        params = layer.__dict__["_bench_params"] = list(layer.parameters())
+    for p in params:
         p.grad = None
     M.grad = None
     x.grad = None

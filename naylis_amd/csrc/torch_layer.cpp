@@ -8,6 +8,10 @@
 // (hipBLASLt through at::mm / at::linear on torch's current stream), so their
 // results are bitwise those of the Python node.
 //
+// MomLayerNode is the same node as a C++ autograd function: its forward
+// calls layer_fwd and saves what the Python node saves, its backward calls
+// layer_bwd, so the autograd engine runs the backward without Python.
+//
 // The library's symbols are not linked here: libnaylis_mom.so is loaded with
 // global visibility before this module (naylis_amd/_lib.py), so these calls
 // bind to that one instance (its timing state and scratch arrays included).
@@ -226,8 +230,84 @@ std::vector<at::Tensor> layer_bwd(c10::optional<at::Tensor> dy, c10::optional<at
   return {dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds, dk_ext, dv_ext};
 }
 
+namespace {
+
+c10::optional<at::Tensor> opt(const at::Tensor& t) {
+  return t.defined() ? c10::optional<at::Tensor>(t) : c10::nullopt;
+}
+
+// Inputs as MomLayerFunction.forward takes them; the autograd function takes
+// only defined tensors, so an absent noise draw is passed as x with
+// has_noise false, and the bank (m_blocks) or the external K / V that the
+// call does not use likewise (external tells which); no gradient flows to
+// those placeholders.  Outputs y, probs, top_idx.
+struct MomLayerNode : public torch::autograd::Function<MomLayerNode> {
+  static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx, at::Tensor x,
+                                                at::Tensor m_blocks, at::Tensor w_down, at::Tensor w_up,
+                                                at::Tensor w_q, at::Tensor w_k, at::Tensor w_v, at::Tensor w_o,
+                                                at::Tensor scale, at::Tensor noise, bool has_noise,
+                                                double noise_scale, int64_t n_heads, int64_t num_blocks,
+                                                int64_t block_size, int64_t top_k, int64_t noise_kind,
+                                                at::Tensor k_ext, at::Tensor v_ext, bool external, int64_t stream) {
+    const at::Tensor none;
+    x = x.contiguous();
+    std::vector<at::Tensor> r =
+        layer_fwd(x, external ? c10::nullopt : opt(m_blocks), w_down, w_up, w_q, w_k, w_v, w_o, scale,
+                  has_noise ? opt(noise) : c10::nullopt, noise_scale, n_heads, num_blocks, block_size, top_k,
+                  noise_kind, external ? opt(k_ext) : c10::nullopt, external ? opt(v_ext) : c10::nullopt, stream);
+    // r: y, probs, top_idx, act, gates, slots, k, v, q, order, out, side, lse, w_os
+    ctx->save_for_backward({x, r[5], w_down, w_up, w_q, w_k, w_v, w_o, scale, r[3], r[1], r[2], r[4], r[6], r[7],
+                            r[8], r[9], r[10], r[11], r[12], r[13]});
+    ctx->saved_data["geom"] = std::vector<int64_t>{n_heads, num_blocks, block_size, top_k, stream};
+    ctx->saved_data["external"] = external;
+    ctx->saved_data["m_shape"] = external ? std::vector<int64_t>{} : m_blocks.sizes().vec();
+    ctx->saved_data["m_bf16"] = !external && m_blocks.scalar_type() == at::kBFloat16;
+    ctx->mark_non_differentiable({r[2]});
+    ctx->set_materialize_grads(false);
+    return {r[0], r[1], r[2]};
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const torch::autograd::variable_list s = ctx->get_saved_variables();
+    const std::vector<int64_t> geom = ctx->saved_data["geom"].toIntVector();
+    const bool external = ctx->saved_data["external"].toBool();
+    std::vector<int64_t> m_shape = ctx->saved_data["m_shape"].toIntVector();
+    const bool m_bf16 = ctx->saved_data["m_bf16"].toBool();
+    // s: x, slots, w_down, w_up, w_q, w_k, w_v, w_o, scale, act, probs, top_idx, gates, k, v, q, order,
+    // out, side, lse, w_os
+    std::vector<at::Tensor> r =
+        layer_bwd(opt(grads[0]), opt(grads[1]), s[0], opt(s[1]), s[2], s[3], s[4], s[5], s[6], s[7], s[8], s[9],
+                  s[10], s[11], s[12], s[13], s[14], s[15], s[16], s[17], opt(s[18]), s[19], s[20], geom[0],
+                  geom[1], geom[2], geom[3], external, m_shape, m_bf16, geom[4]);
+    // r: dx, d_m, dw_down, dw_up, dw_q, dw_k, dw_v, dw_o, ds, dk_ext, dv_ext
+    const at::Tensor none;
+    return {r[0], r[1],  r[2], r[3], r[4], r[5], r[6], r[7], r[8].view(s[8].sizes()), none, none,
+            none, none, none, none, none, none, r[9], r[10], none, none};
+  }
+};
+
+std::vector<at::Tensor> mom_layer_node(at::Tensor x, c10::optional<at::Tensor> m_blocks, at::Tensor w_down,
+                                       at::Tensor w_up, at::Tensor w_q, at::Tensor w_k, at::Tensor w_v,
+                                       at::Tensor w_o, at::Tensor scale, c10::optional<at::Tensor> noise,
+                                       double noise_scale, int64_t n_heads, int64_t num_blocks, int64_t block_size,
+                                       int64_t top_k, int64_t noise_kind, c10::optional<at::Tensor> k_ext,
+                                       c10::optional<at::Tensor> v_ext, int64_t stream) {
+  const bool external = k_ext.has_value() && k_ext->defined();
+  const bool has_noise = noise.has_value() && noise->defined();
+  TORCH_CHECK(external || (m_blocks.has_value() && m_blocks->defined()), "mom_layer: no bank and no external K / V");
+  TORCH_CHECK(!external || (v_ext.has_value() && v_ext->defined()), "mom_layer: external K without V");
+  return MomLayerNode::apply(x, external ? x : *m_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale,
+                             has_noise ? *noise : x, has_noise, noise_scale, n_heads, num_blocks, block_size, top_k,
+                             noise_kind, external ? *k_ext : x, external ? *v_ext : x, external, stream);
+}
+
+}  // namespace
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Fused MoM layer node over the C ABI of libnaylis_mom.so";
   m.def("layer_fwd", &layer_fwd, "MoM layer forward (router, bank K/V, q projection, read, o projection)");
   m.def("layer_bwd", &layer_bwd, "MoM layer backward (the forward's gradients in one fixed order)");
+  m.def("mom_layer", &mom_layer_node,
+        "The fused layer node as a C++ autograd function: returns (y, probs, top_idx) with its backward attached");
 }

@@ -121,8 +121,10 @@ class MoMLayer(nn.Module):
                 top_k=self.top_blocks, noise=noise, noise_scale=self.noise_scale, noise_is_uniform=True,
                 bank_kv=bank_kv)
             if self.training:
-                self.last_router_probs = router_probs.reshape(-1, self.num_blocks)
-                self.last_top_idx = top_idx.reshape(-1, self.top_blocks)
+                # plain attributes (not parameters, buffers or modules): set
+                # without nn.Module.__setattr__'s registry checks
+                self.__dict__["last_router_probs"] = router_probs.reshape(-1, self.num_blocks)
+                self.__dict__["last_top_idx"] = top_idx.reshape(-1, self.top_blocks)
             return y
         _, router_probs, top_idx, top_gates = self.route(x, noise, noise_is_uniform=True)
         if self.training:

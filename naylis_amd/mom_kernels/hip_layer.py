@@ -38,6 +38,9 @@ _F32, _BF16 = 0, 1
 
 # run the node's host side in the torch extension (one C++ call per direction)
 USE_TORCH_EXT = True
+# the node itself in C++ (the extension's mom_layer: a torch::autograd::Function
+# whose forward / backward make the calls of MomLayerFunction's extension path)
+USE_CPP_NODE = True
 
 
 def _ws(nbytes, dev):
@@ -231,6 +234,12 @@ def mom_layer(x, M_blocks, w_down, w_up, w_q, w_k, w_v, w_o, scale, *, n_heads, 
     if noise is not None:
         noise = noise.detach().float().contiguous()
     k_ext, v_ext = bank_kv if bank_kv is not None else (None, None)
+    if USE_TORCH_EXT and USE_CPP_NODE:
+        y, probs, top_idx = _torch_ext.load().mom_layer(
+            x, M_blocks if bank_kv is None else None, w_down.float().contiguous(), w_up.float().contiguous(), w_q,
+            w_k, w_v, w_o, scale, noise, float(noise_scale), int(n_heads), int(num_blocks), int(block_size),
+            int(top_k), 1 if noise_is_uniform else 0, k_ext, v_ext, _lib.stream_of(x.device))
+        return y, probs, top_idx
     return MomLayerFunction.apply(x, M_blocks if bank_kv is None else None, w_down.float().contiguous(),
                                   w_up.float().contiguous(), w_q, w_k, w_v, w_o, scale, noise, float(noise_scale),
                                   (int(n_heads), int(num_blocks), int(block_size), int(top_k),

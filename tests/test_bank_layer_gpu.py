@@ -190,17 +190,19 @@ EXT_CASES = [
 
 @pytest.mark.parametrize("case", EXT_CASES, ids=[f"case{i}" for i in range(len(EXT_CASES))])
 def test_layer_torch_ext_matches_python_node(case, dev, monkeypatch):
-    """The fused node's host side in C++ (csrc/torch_layer.cpp, one extension
-    call per direction) against its Python statement (the same library and
-    torch calls through ctypes): output, probs, routing and every gradient
-    bitwise equal, with the aux loss reaching the router through the probs."""
+    """The fused node's host side in C++ (csrc/torch_layer.cpp): the node as a
+    C++ autograd function, and the Python node calling the extension once per
+    direction, each against the Python statement (the same library and torch
+    calls through ctypes): output, probs, routing and every gradient bitwise
+    equal, with the aux loss reaching the router through the probs."""
     import naylis_amd.layer as layer_mod
     from naylis_amd import mom_kernels
     from naylis_amd.mom_kernels import hip_layer
     B, S, D, H, NB, BS, K, R, m_dtype, external, noise = case
     res = []
-    for use_ext in (True, False):
+    for use_ext, cpp_node in ((True, True), (True, False), (False, False)):
         monkeypatch.setattr(hip_layer, "USE_TORCH_EXT", use_ext)
+        monkeypatch.setattr(hip_layer, "USE_CPP_NODE", cpp_node)
         layer, _, M = build_pair(D, H, NB, BS, K, R, seed=31)
         ld = layer.to(dev)
         for lin in (ld.q_proj, ld.k_proj, ld.v_proj, ld.o_proj):
@@ -223,14 +225,15 @@ def test_layer_torch_ext_matches_python_node(case, dev, monkeypatch):
         (y * dy).sum().add(aux).backward()
         res.append((y.detach(), idx, x.grad.clone(), Md.grad.clone(),
                     {n: p.grad.clone() for n, p in ld.named_parameters() if p.grad is not None}))
-    (y0, i0, x0, m0, g0), (y1, i1, x1, m1, g1) = res
-    assert torch.equal(i0, i1)
-    assert torch.equal(y0, y1)
-    assert torch.equal(x0, x1)
-    assert torch.equal(m0, m1)
-    assert g0.keys() == g1.keys()
-    for n in g0:
-        assert torch.equal(g0[n], g1[n]), n
+    y1, i1, x1, m1, g1 = res[-1]  # the Python statement
+    for mode, (y0, i0, x0, m0, g0) in zip(("C++ node", "extension calls"), res[:2]):
+        assert torch.equal(i0, i1), mode
+        assert torch.equal(y0, y1), mode
+        assert torch.equal(x0, x1), mode
+        assert torch.equal(m0, m1), mode
+        assert g0.keys() == g1.keys(), mode
+        for n in g0:
+            assert torch.equal(g0[n], g1[n]), (mode, n)
 
 
 @pytest.mark.parametrize("n,L,D", [(3, 1024, 1024), (20, 1024, 1024), (25, 512, 256)])
