@@ -725,13 +725,14 @@ def main(argv=None):
              for k in ("bank_kv_fwd", "bank_kv_bwd_dslots", "bank_kv_bwd_dw", "linear_wgrad") if k in per}
     gemms.update(torch_projection_gemms(layer, x, args.steps))
     # the prefix-mean router against HBM: forward reads x once and writes logits / probs / top-k /
-    # gates / activations (plus the (N, R) projection written and read back); the backward reads x,
+    # gates / activations (plus the (N, R) projection written and read back when it runs as two
+    # launches; the one-launch kernel `router_fwd` keeps it on chip); the backward reads x,
     # the incoming dx and writes dx (the accumulating input gradient), plus the (N, R) and (N, E)
     # per-token terms
     R_, E_, K_ = cfg["R"], E, cfg["K"]
     f_bytes = ntok * D * 2 + ntok * (2 * E_ + 2 * K_ + R_ + 2 * R_) * 4
     b_bytes = 3 * ntok * D * 2 + ntok * (3 * R_ + 2 * E_ + 3 * K_) * 4
-    f_us = sum(per[k][0] * per[k][1] for k in ("router_proj", "router_head") if k in per) * 1e3
+    f_us = sum(per[k][0] * per[k][1] for k in ("router_fwd", "router_proj", "router_head") if k in per) * 1e3
     b_us = sum(per[k][0] * per[k][1] for k in ("router_bwd_token", "router_bwd_scan", "router_bwd_dx",
                                                "router_reduce") if k in per) * 1e3
     router = {"fwd_alg_bytes": f_bytes, "fwd_us": round(f_us, 2), "bwd_alg_bytes": b_bytes, "bwd_us": round(b_us, 2)}

@@ -14,7 +14,7 @@ struct RouterDims {
 
 // Byte offsets into the caller's workspace.  The forward uses [0, fwd_total).
 struct RouterWs {
-  size_t carry, y, ycs, w, wt, scan_csum, dwup_part, dwd_part;
+  size_t carry, y, ycs, pub, w, wt, scan_csum, dwup_part, dwd_part;
   size_t fwd_total, total;
 };
 
@@ -36,7 +36,8 @@ bool router_fast_fwd_ok(const void* x, bool x_bf16, const float* w_down, const f
 bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const RouterDims& d);
 void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_up, const float* noise,
                             float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
-                            float* act, float* y, double* ycs, const RouterDims& d, hipStream_t st);
+                            float* act, float* y, double* ycs, unsigned long long* pub, const RouterDims& d,
+                            hipStream_t st);
 // fast backward (B1 + B2): w, its 32-token chunk sums, W~ (skipped when
 // fuse_scan: the dx kernel then forms it) and the dW_up partials; returns the
 // number of dW_up partials

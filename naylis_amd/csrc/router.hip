@@ -762,6 +762,8 @@ RouterWs plan_router_ws(const RouterDims& d) {
   off += a256((size_t)ntok * d.R * 4);
   w.ycs = off;
   off += a256((size_t)d.B * n_chunks * d.R * 8);
+  w.pub = off;  // one-launch fast forward: each 32-token chunk's sums as (v, v ^ epoch) word pairs
+  off += a256((size_t)d.B * ((d.T + 31) / 32) * d.R * 16);
   w.fwd_total = off;
   w.w = off;
   off += a256((size_t)ntok * d.R * 4);
@@ -828,7 +830,8 @@ hipError_t launch_router_fwd(const void* x, bool x_bf16, const float* w_down, co
   if (router_fast_fwd_ok(x, x_bf16, w_down, h_out, d)) {
     const RouterWs w = plan_router_ws(d);
     launch_router_fast_fwd(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act,
-                           (float*)((char*)ws + w.y), (double*)((char*)ws + w.ycs), d, st);
+                           (float*)((char*)ws + w.y), (double*)((char*)ws + w.ycs),
+                           (unsigned long long*)((char*)ws + w.pub), d, st);
     return hipGetLastError();
   }
   const RouterWs w = plan_router_ws(d);

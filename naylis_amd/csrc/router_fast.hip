@@ -204,34 +204,36 @@ __device__ __forceinline__ double chunk_carry(const double* __restrict__ cs, int
 // The prefix is one serial fp64 chain per rank (carry + y_0 + ... + y_t, in
 // token order); everything else runs over (token, rank) pairs or over 8
 // lanes per token (lane p of token t owns experts p, p + 8, ...).
+// LDS of one chunk's head (router_head_body)
+template <int EMAX>
+struct HeadLds {
+  float a[kFastChunk * 65];
+  float lg[kFastChunk * (EMAX + 1)];
+  float ex[kFastChunk * (EMAX + 1)];
+  float sum[kFastChunk];
+};
+
+// The head of chunk c of sequence b from its projections y (y_lds, row pitch
+// 65) and the fp64 carry of the earlier chunks (carry_lds[r]); run by 256
+// threads (tid 0..255) with the W_up rows in wu_lds; zs_lds (32 x 65
+// doubles) takes the in-chunk prefix.  Every thread of the workgroup must
+// call it (it has barriers).
 template <int EMAX, int TK>
-__global__ __launch_bounds__(256) void router_head_kernel(
-    const float* __restrict__ y, const double* __restrict__ ycs, const float* __restrict__ w_up,
+__device__ __forceinline__ void router_head_body(
+    int tid, int c, int b, const float* y_lds, const double* carry_lds, const float* wu_lds, double* zs_lds,
+    HeadLds<EMAX>& L,
     const float* __restrict__ noise, float noise_scale, int noise_kind, float* __restrict__ logits,
-    float* __restrict__ probs,
-    int32_t* __restrict__ top_idx, float* __restrict__ top_gates, float* __restrict__ act, int T, int R, int E,
-    int topk, int n_ch) {
+    float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_gates,
+    float* __restrict__ act, int T, int R, int E, int topk) {
   constexpr int CT = kFastChunk;
   constexpr int LP = EMAX + 1;
   constexpr int EPL = EMAX / 8;  // experts per lane
   constexpr int NONE = 0x7fffffff;
-  __shared__ float y_lds[CT * 65];
-  __shared__ float a_lds[CT * 65];
-  __shared__ double zs_lds[4096];  // carry staging, then the in-chunk prefix
-  __shared__ float wu_lds[EMAX * 65];
-  __shared__ float lg_lds[CT * LP];
-  __shared__ float ex_lds[CT * LP];
-  __shared__ float sum_lds[CT];
-  __shared__ double carry_lds[64];
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x;
   const int t0 = c * CT, nt = min(CT, T - t0);
-  for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
-  for (int i = tid; i < nt * R; i += 256) y_lds[(i / R) * 65 + i % R] = y[((long)b * T + t0) * R + i];
-  // carry = sum of the earlier chunks' fp64 sums, in chunk order
-  const double carry = chunk_carry(ycs + (long)b * n_ch * R, 0, c, R, zs_lds, tid);
-  if (tid < R) carry_lds[tid] = carry;
-  __syncthreads();
+  float* a_lds = L.a;
+  float* lg_lds = L.lg;
+  float* ex_lds = L.ex;
+  float* sum_lds = L.sum;
   // Z_t = carry + y_0 + ... + y_t in token order (fp64), one chain per rank
   if (tid < R) {
     double run = carry_lds[tid];
@@ -357,6 +359,197 @@ __global__ __launch_bounds__(256) void router_head_kernel(
         top_gates[tok * topk + s] = expf(val[s] - val[0]) / gs;
       }
   }
+}
+
+// ---------------------------------------------------------------------------
+// (F) The forward in one launch: router_proj_kernel's projection of two
+// chunks per workgroup, then router_head_body on both chunks (one per half of
+// the workgroup), the carry of the earlier chunks' fp64 sums taken from the
+// other workgroups of the sequence.  Each chunk's sums are published as word
+// pairs (v, v ^ epoch), written and read with device-scope atomic 64-bit
+// accesses: a pair is valid for this launch only when the words XOR to its
+// epoch, so stale pairs (another launch) and torn ones (one word new, one
+// old) are both rejected without a flag or a fence.  A workgroup waits only
+// on the chunks before its own, i.e. on workgroups of lower dispatch order in
+// the same sequence; the wait is bounded, and a chunk still missing after it
+// is projected again from x here, the same operations in the same order, so
+// the carry is bitwise that of the two launches whatever happens.
+constexpr int kFusedSpin = 20000;  // polls (s_sleep between them) before a workgroup projects a chunk itself
+
+template <int RT, int KSW, int EMAX, int TK>
+__global__ __launch_bounds__(512) void router_fwd_fused_kernel(
+    const bf16_t* __restrict__ x, const float* __restrict__ w_down, const float* __restrict__ w_up,
+    const float* __restrict__ noise, float noise_scale, int noise_kind, float* __restrict__ logits,
+    float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_gates,
+    float* __restrict__ act, unsigned long long* __restrict__ pub, unsigned long long epoch, int T, int D, int R,
+    int E, int topk, int n_ch) {
+  constexpr int CT = kFastChunk;
+  constexpr int NW = 8, NC = 2;
+  constexpr int P = 33;  // partial tile pitch
+  __shared__ float part[NW][RT][CT * P];
+  __shared__ float yk[NC][CT * 65];             // the two chunks' projections (head layout)
+  __shared__ double stage[4160];                // earlier chunks' sums, then the two halves' prefixes
+  __shared__ float wu_lds[EMAX * 65];
+  __shared__ double carry_lds[NC][64];
+  __shared__ HeadLds<EMAX> hl[NC];
+  const int cg = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int nks = D / (16 * NW);
+  const int d0 = wave * nks * 16;
+  const int c_first = cg * NC;
+  unsigned long long* pub_b = pub + (long)b * n_ch * R * 2;
+
+  for (int i = tid; i < E * R; i += NW * 64) wu_lds[(i / R) * 65 + i % R] = w_up[i];
+  auto load_x = [&](bf16x8 (&xf)[KSW], int c) {
+    const int t0 = c * CT, nt = min(CT, T - t0);
+    const bf16_t* xrow = x + ((long)b * T + t0 + min(l32, nt - 1)) * D + d0 + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks) xf[ks] = *reinterpret_cast<const bf16x8*>(xrow + 16 * min(ks, nks - 1));
+  };
+  bf16x8 xf[KSW];
+  load_x(xf, c_first);
+  bf16x8 p1[KSW][RT], p2[KSW][RT], p3[KSW][RT];
+  {
+    f32x4 wf[KSW][RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float* wrow = w_down + (long)min(rt * 32 + l32, R - 1) * D + d0 + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < KSW; ++ks) {
+        const int kc = min(ks, nks - 1);
+        wf[ks][rt][0] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc);
+        wf[ks][rt][1] = *reinterpret_cast<const f32x4*>(wrow + 16 * kc + 4);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) split3(wf[ks][rt][0], wf[ks][rt][1], p1[ks][rt], p2[ks][rt], p3[ks][rt]);
+  }
+  const int RW = RT * 32;
+  // chunk c's projections into out (row pitch 65) and, for threads tid < R,
+  // its fp64 column sum (the operations of router_proj_kernel, in its order)
+  auto project = [&](const bf16x8 (&xc)[KSW], int c, float* out) -> double {
+    const int t0 = c * CT, nt = min(CT, T - t0);
+    f32x16 acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KSW; ++ks) {
+      if (ks < nks) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          acc[rt] = mfma32(xc[ks], p3[ks][rt], acc[rt]);  // smallest terms first
+          acc[rt] = mfma32(xc[ks], p2[ks][rt], acc[rt]);
+          acc[rt] = mfma32(xc[ks], p1[ks][rt], acc[rt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) part[wave][rt][acc_row(g, v) * P + l32] = acc[rt][v];
+    __syncthreads();
+    for (int i = tid; i < CT * RW; i += NW * 64) {
+      const int t = i / RW, r = i % RW, rt = r >> 5, rl = r & 31;
+      float sum = part[0][rt][t * P + rl];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) sum += part[w][rt][t * P + rl];
+      if (r < R) out[t * 65 + r] = sum;
+    }
+    __syncthreads();
+    double cs = 0.0;
+    if (tid < R)
+      for (int t = 0; t < nt; ++t) cs += (double)out[t * 65 + tid];
+    return cs;
+  };
+  // ---- the two chunks, each published as soon as its sums exist
+  double cs_own[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = c_first + j;
+    bf16x8 xn[KSW];
+    if (j + 1 < NC) load_x(xn, c + 1);  // in flight during this chunk's reduction
+    cs_own[j] = project(xf, c, yk[j]);
+    if (tid < R) {
+      const unsigned long long w1 = __double_as_longlong(cs_own[j]);
+      unsigned long long* q = pub_b + ((long)c * R + tid) * 2;
+      __hip_atomic_store(q, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(q + 1, w1 ^ epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (j + 1 < NC) {
+#pragma unroll
+      for (int ks = 0; ks < KSW; ++ks) xf[ks] = xn[ks];
+    }
+  }
+  // ---- carry of chunk c_first: the published sums of chunks 0 .. c_first - 1
+  // in chunk order (as chunk_carry), staged per block of 4096 / R chunks
+  double run = 0.0;
+  const int per = 4096 / R;
+  for (int cb = 0; cb < c_first; cb += per) {
+    const int nc = min(per, c_first - cb), n = nc * R;
+    bool done = false;
+    for (int it = 0; it < kFusedSpin && !done; ++it) {
+      int ok = 1;
+      for (int i = tid; i < n; i += NW * 64) {
+        const unsigned long long* q = pub_b + ((long)cb * R + i) * 2;
+        const unsigned long long w1 = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long w2 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((w1 ^ w2) == epoch) stage[i] = __longlong_as_double(w1);
+        else ok = 0;
+      }
+      done = __syncthreads_and(ok) != 0;
+      if (!done) __builtin_amdgcn_s_sleep(2);
+    }
+    if (!done) {
+      // still missing after the bound: project the block's chunks here
+      for (int k = 0; k < nc; ++k) {
+        bf16x8 xc[KSW];
+        load_x(xc, cb + k);
+        const double cs = project(xc, cb + k, hl[0].a);  // (hl[0].a: scratch until the head)
+        if (tid < R) stage[k * R + tid] = cs;
+        __syncthreads();
+      }
+    }
+    if (tid < R) run = add_in_order(run, stage + tid, R, nc);
+    __syncthreads();
+  }
+  if (tid < R) {
+    carry_lds[0][tid] = run;
+    carry_lds[1][tid] = run + cs_own[0];  // the carry of chunk c_first + 1, extending the same chain
+  }
+  __syncthreads();
+  // ---- the heads: chunk c_first + h by the threads of half h
+  const int h = tid >> 8;
+  router_head_body<EMAX, TK>(tid & 255, c_first + h, b, yk[h], carry_lds[h], wu_lds, stage + h * 2080, hl[h],
+                             noise, noise_scale, noise_kind, logits, probs, top_idx, top_gates, act, T, R, E, topk);
+}
+
+template <int EMAX, int TK>
+__global__ __launch_bounds__(256) void router_head_kernel(
+    const float* __restrict__ y, const double* __restrict__ ycs, const float* __restrict__ w_up,
+    const float* __restrict__ noise, float noise_scale, int noise_kind, float* __restrict__ logits,
+    float* __restrict__ probs,
+    int32_t* __restrict__ top_idx, float* __restrict__ top_gates, float* __restrict__ act, int T, int R, int E,
+    int topk, int n_ch) {
+  constexpr int CT = kFastChunk;
+  __shared__ float y_lds[CT * 65];
+  __shared__ double stage[4096];  // carry staging, then the in-chunk prefix
+  __shared__ float wu_lds[EMAX * 65];
+  __shared__ double carry_lds[64];
+  __shared__ HeadLds<EMAX> hl;
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int t0 = c * CT, nt = min(CT, T - t0);
+  for (int i = tid; i < E * R; i += 256) wu_lds[(i / R) * 65 + i % R] = w_up[i];
+  for (int i = tid; i < nt * R; i += 256) y_lds[(i / R) * 65 + i % R] = y[((long)b * T + t0) * R + i];
+  // carry = sum of the earlier chunks' fp64 sums, in chunk order
+  const double carry = chunk_carry(ycs + (long)b * n_ch * R, 0, c, R, stage, tid);
+  if (tid < R) carry_lds[tid] = carry;
+  __syncthreads();
+  router_head_body<EMAX, TK>(tid, c, b, y_lds, carry_lds, wu_lds, stage, hl, noise, noise_scale, noise_kind, logits,
+                             probs, top_idx, top_gates, act, T, R, E, topk);
 }
 
 // ---------------------------------------------------------------------------
@@ -756,11 +949,27 @@ bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const Router
   return x_bf16 && d.D % kFastDxSlab == 0 && d.R <= 64 && (((uintptr_t)x | (uintptr_t)dx) & 15) == 0;
 }
 
+// Launch epoch of the one-launch forward (never 0), per device.
+static unsigned long long next_router_epoch() {
+  static std::atomic<unsigned long long> epochs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  unsigned long long e = epochs[dev].fetch_add(1, std::memory_order_relaxed) + 1;
+  if (e == 0) e = epochs[dev].fetch_add(1, std::memory_order_relaxed) + 1;
+  return e;
+}
+
 template <int RT, int EMAX, int TK>
 static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
                           float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
-                          const RouterDims& d, hipStream_t st) {
+                          unsigned long long* pub, const RouterDims& d, hipStream_t st) {
   const int n_ch = (d.T + kFastChunk - 1) / kFastChunk;
+  // One launch (router_fwd_fused_kernel) where its two-chunk workgroups
+  // apply: R <= 32, an even chunk count, and a stream that is not being
+  // captured (a captured launch would replay one epoch)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool capturing = hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
+  const bool fused = RT == 1 && pub != nullptr && n_ch % 2 == 0 && !capturing;
   // 8 waves split D; a wave takes D / 128 K-steps, held in registers at once
   const int nks = d.D / 128;
   auto go = [&](auto ksw) {
@@ -770,6 +979,16 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
     // still has a workgroup per CU, so the grid runs in one round
     constexpr int NCW = KSW * RT <= 12 ? 2 : 1;
     const int nc = (NCW > 1 && (long)((n_ch + 1) / 2) * d.B >= 256) ? 2 : 1;
+    if constexpr (NCW == 2 && RT == 1) {
+      if (fused) {
+        NAYLIS_TIMED("router_fwd", st,
+                     hipLaunchKernelGGL((router_fwd_fused_kernel<RT, KSW, EMAX, TK>), dim3(n_ch / 2, d.B), dim3(512),
+                                        0, st, (const bf16_t*)x, w_down, w_up, noise, ns, d.noise_kind, logits, probs,
+                                        idx, gates, act, pub, next_router_epoch(), d.T, d.D, d.R, d.E, d.topk,
+                                        n_ch));
+        return true;
+      }
+    }
     if (nc == 2)
       NAYLIS_TIMED("router_proj", st,
                    hipLaunchKernelGGL((router_proj_kernel<RT, KSW, NCW>), dim3((n_ch + NCW - 1) / NCW, d.B),
@@ -778,21 +997,24 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
       NAYLIS_TIMED("router_proj", st,
                    hipLaunchKernelGGL((router_proj_kernel<RT, KSW, 1>), dim3(n_ch, d.B), dim3(512), 0, st,
                                       (const bf16_t*)x, w_down, y, ycs, d.T, d.D, d.R, n_ch));
+    return false;
   };
+  bool one_launch;
   if (nks <= 2)
-    go(std::integral_constant<int, 2>{});
+    one_launch = go(std::integral_constant<int, 2>{});
   else if (nks <= 4)
-    go(std::integral_constant<int, 4>{});
+    one_launch = go(std::integral_constant<int, 4>{});
   else if (nks <= 8)
-    go(std::integral_constant<int, 8>{});
+    one_launch = go(std::integral_constant<int, 8>{});
   else if constexpr (RT == 1) {
     if (nks <= 12)
-      go(std::integral_constant<int, 12>{});
+      one_launch = go(std::integral_constant<int, 12>{});
     else
-      go(std::integral_constant<int, 16>{});
+      one_launch = go(std::integral_constant<int, 16>{});
   } else {
-    go(std::integral_constant<int, 16 / RT>{});  // router_fast_fwd_ok bounds nks by 16 / RT
+    one_launch = go(std::integral_constant<int, 16 / RT>{});  // router_fast_fwd_ok bounds nks by 16 / RT
   }
+  if (one_launch) return;
   NAYLIS_TIMED("router_head", st,
                hipLaunchKernelGGL((router_head_kernel<EMAX, TK>), dim3(n_ch, d.B), dim3(256), 0, st, y, ycs, w_up,
                                   noise, ns, d.noise_kind, logits, probs, idx, gates, act, d.T, d.R, d.E, d.topk,
@@ -802,24 +1024,25 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
 template <int RT>
 static void fast_fwd_rt(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
                         float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
-                        const RouterDims& d, hipStream_t st) {
+                        unsigned long long* pub, const RouterDims& d, hipStream_t st) {
   if (d.E <= 8 && d.topk <= 2)
-    fast_fwd_inst<RT, 8, 2>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+    fast_fwd_inst<RT, 8, 2>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, pub, d, st);
   else if (d.E <= 8)
-    fast_fwd_inst<RT, 8, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+    fast_fwd_inst<RT, 8, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, pub, d, st);
   else if (d.E <= 32)
-    fast_fwd_inst<RT, 32, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+    fast_fwd_inst<RT, 32, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, pub, d, st);
   else
-    fast_fwd_inst<RT, 64, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, d, st);
+    fast_fwd_inst<RT, 64, 8>(x, w_down, w_up, noise, ns, logits, probs, idx, gates, act, y, ycs, pub, d, st);
 }
 
 void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_up, const float* noise,
                             float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
-                            float* act, float* y, double* ycs, const RouterDims& d, hipStream_t st) {
+                            float* act, float* y, double* ycs, unsigned long long* pub, const RouterDims& d,
+                            hipStream_t st) {
   if (d.R <= 32)
-    fast_fwd_rt<1>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, d, st);
+    fast_fwd_rt<1>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, pub, d, st);
   else
-    fast_fwd_rt<2>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, d, st);
+    fast_fwd_rt<2>(x, w_down, w_up, noise, noise_scale, logits, probs, top_idx, top_gates, act, y, ycs, pub, d, st);
 }
 
 // The fused prologue (two memory rounds and the carry chains) is paid once

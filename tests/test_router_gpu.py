@@ -228,3 +228,58 @@ def test_router_backward_accumulates_dx(dev):
                                    ti.data_ptr(), tg.data_ptr(), dg.data_ptr(), None, E, None, xf.data_ptr(), 1,
                                    dwd.data_ptr(), dwu.data_ptr(), ws.data_ptr(), nbytes, B, T, D, R, E, k, st)
     assert rc == _lib.NAYLIS_ERR_ARG
+
+
+@pytest.mark.parametrize("B,T,D,R,E,k,with_noise", [
+    (8, 2048, 1024, 32, 8, 2, False),   # config 2
+    (4, 4096, 1536, 32, 32, 2, True),   # config 4 shape, additive logit noise
+    (2, 512, 256, 16, 8, 2, True),      # rank 16, two sequences of 16 chunks
+])
+def test_router_one_launch_matches_two_launches(B, T, D, R, E, k, with_noise, dev):
+    """The forward in one launch (workgroups publish their chunks' fp64 sums
+    to the later chunks' workgroups) against the two launches (projection,
+    then head) that the same call makes under stream capture: logits, probs,
+    top_idx, gates and act bitwise equal.  A launch on other data through the
+    same workspace first leaves published sums of another epoch behind, which
+    the checked launch must not take; the captured graph is replayed twice
+    with eager launches between, every replay checked."""
+    from naylis_amd import _lib
+    lib = _lib.load()
+    x, w_down, w_up, noise = make(B, T, D, R, E, torch.bfloat16, seed=11, bias_blocks=(1, 3) if with_noise else None)
+    x_other, _, _, _ = make(B, T, D, R, E, torch.bfloat16, seed=12)
+    xd, xo, wd, wu = x.to(dev), x_other.to(dev), w_down.to(dev), w_up.to(dev)
+    nz = noise.to(dev) if noise is not None else None
+    nbytes = lib.naylis_mom_router_workspace_bytes(B, T, D, R, E, k)
+
+    def outputs():
+        return (torch.empty(B, T, E, device=dev), torch.empty(B, T, E, device=dev),
+                torch.empty(B, T, k, dtype=torch.int32, device=dev), torch.empty(B, T, k, device=dev),
+                torch.empty(B, T, R, device=dev))
+
+    def call(xin, outs, ws):
+        lg, pr, ti, tg, act = outs
+        rc = lib.naylis_mom_router_fwd(xin.data_ptr(), 1, wd.data_ptr(), wu.data_ptr(),
+                                       nz.data_ptr() if nz is not None else None, 0, 1.0, lg.data_ptr(),
+                                       pr.data_ptr(), ti.data_ptr(), tg.data_ptr(), act.data_ptr(), None,
+                                       ws.data_ptr(), nbytes, B, T, D, R, E, k, _lib.stream_of(dev))
+        assert rc == 0, lib.naylis_mom_last_error()
+
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    call(xo, outputs(), ws)          # other data: its sums stay published in ws
+    eager = outputs()
+    call(xd, eager, ws)              # one launch
+    torch.cuda.synchronize()
+    ws_cap = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    cap = outputs()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(xd, cap, ws_cap)        # under capture: the two launches
+    for rep in range(2):
+        for t in cap:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("logits", "probs", "top_idx", "gates", "act"), eager, cap):
+            assert torch.equal(a, b), (rep, name)
+        call(xo, outputs(), ws)      # eager work between the replays
+        torch.cuda.synchronize()
