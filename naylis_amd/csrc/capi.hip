@@ -407,6 +407,8 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
                     "mom_route_fwd");
 }
 
+int naylis_mom_router_spin_limit(int polls) { return router_fused_spin_limit(polls); }
+
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,
                           const float* d_probs, int64_t d_probs_stride, const float* d_logits, void* dx,

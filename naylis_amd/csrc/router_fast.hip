@@ -373,8 +373,10 @@ __device__ __forceinline__ void router_head_body(
 // on the chunks before its own, i.e. on workgroups of lower dispatch order in
 // the same sequence; the wait is bounded, and a chunk still missing after it
 // is projected again from x here, the same operations in the same order, so
-// the carry is bitwise that of the two launches whatever happens.
-constexpr int kFusedSpin = 20000;  // polls (s_sleep between them) before a workgroup projects a chunk itself
+// the carry is bitwise that of the two launches whatever happens.  The bound
+// (spin: polls, an s_sleep between them, per block of earlier chunks) is a
+// launch argument; 0 skips the wait and re-projects every earlier chunk.
+constexpr int kFusedSpinDefault = 20000;
 
 template <int RT, int KSW, int EMAX, int TK>
 __global__ __launch_bounds__(512) void router_fwd_fused_kernel(
@@ -382,7 +384,7 @@ __global__ __launch_bounds__(512) void router_fwd_fused_kernel(
     const float* __restrict__ noise, float noise_scale, int noise_kind, float* __restrict__ logits,
     float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_gates,
     float* __restrict__ act, unsigned long long* __restrict__ pub, unsigned long long epoch, int T, int D, int R,
-    int E, int topk, int n_ch) {
+    int E, int topk, int n_ch, int spin) {
   constexpr int CT = kFastChunk;
   constexpr int NW = 8, NC = 2;
   constexpr int P = 33;  // partial tile pitch
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(512) void router_fwd_fused_kernel(
   for (int cb = 0; cb < c_first; cb += per) {
     const int nc = min(per, c_first - cb), n = nc * R;
     bool done = false;
-    for (int it = 0; it < kFusedSpin && !done; ++it) {
+    for (int it = 0; it < spin && !done; ++it) {
       int ok = 1;
       for (int i = tid; i < n; i += NW * 64) {
         const unsigned long long* q = pub_b + ((long)cb * R + i) * 2;
@@ -959,6 +961,13 @@ static unsigned long long next_router_epoch() {
   return e;
 }
 
+static std::atomic<int> g_fused_spin{kFusedSpinDefault};
+
+int router_fused_spin_limit(int polls) {
+  return polls < 0 ? g_fused_spin.load(std::memory_order_relaxed)
+                   : g_fused_spin.exchange(polls, std::memory_order_relaxed);
+}
+
 template <int RT, int EMAX, int TK>
 static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
                           float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
@@ -985,7 +994,7 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
                      hipLaunchKernelGGL((router_fwd_fused_kernel<RT, KSW, EMAX, TK>), dim3(n_ch / 2, d.B), dim3(512),
                                         0, st, (const bf16_t*)x, w_down, w_up, noise, ns, d.noise_kind, logits, probs,
                                         idx, gates, act, pub, next_router_epoch(), d.T, d.D, d.R, d.E, d.topk,
-                                        n_ch));
+                                        n_ch, g_fused_spin.load(std::memory_order_relaxed)));
         return true;
       }
     }

@@ -235,16 +235,31 @@ def test_router_backward_accumulates_dx(dev):
     (4, 4096, 1536, 32, 32, 2, True),   # config 4 shape, additive logit noise
     (2, 512, 256, 16, 8, 2, True),      # rank 16, two sequences of 16 chunks
 ])
-def test_router_one_launch_matches_two_launches(B, T, D, R, E, k, with_noise, dev):
+@pytest.mark.parametrize("spin", [None, 0, 1])
+def test_router_one_launch_matches_two_launches(B, T, D, R, E, k, with_noise, spin, dev):
     """The forward in one launch (workgroups publish their chunks' fp64 sums
     to the later chunks' workgroups) against the two launches (projection,
     then head) that the same call makes under stream capture: logits, probs,
     top_idx, gates and act bitwise equal.  A launch on other data through the
     same workspace first leaves published sums of another epoch behind, which
     the checked launch must not take; the captured graph is replayed twice
-    with eager launches between, every replay checked."""
+    with eager launches between, every replay checked.  spin sets the one
+    launch's poll bound from the host: 0 makes every workgroup project all
+    earlier chunks itself (the fallback for sums still missing at the bound),
+    1 mixes taken and re-projected blocks; None keeps the default bound."""
     from naylis_amd import _lib
     lib = _lib.load()
+    if spin is not None:
+        prev = lib.naylis_mom_router_spin_limit(spin)
+        try:
+            _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev)
+        finally:
+            assert lib.naylis_mom_router_spin_limit(prev) == spin
+    else:
+        _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev)
+
+
+def _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev):
     x, w_down, w_up, noise = make(B, T, D, R, E, torch.bfloat16, seed=11, bias_blocks=(1, 3) if with_noise else None)
     x_other, _, _, _ = make(B, T, D, R, E, torch.bfloat16, seed=12)
     xd, xo, wd, wu = x.to(dev), x_other.to(dev), w_down.to(dev), w_up.to(dev)
