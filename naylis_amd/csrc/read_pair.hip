@@ -775,19 +775,21 @@ __global__ __launch_bounds__(512, 1) void read_bwd_pair_kernel(
 }
 
 // ------------------------------------------------------------------- reduce
-// dK / dV of block e (rows e * 128 ..), head h, a quarter of its slots: the
+// dK / dV of block e (rows e * 128 ..), head h, an eighth of its slots: the
 // A partials of the run of pairs (e, *) over its ranges (ascending), then
 // for each pair (a, e) with a != e (ascending) the B partials over its
-// ranges (ascending); dK scaled.
+// ranges (ascending); dK scaled.  A thread holds one float4 of each tensor,
+// so a batch of 16 partials' loads is in flight at once.
 // Workgroups past the dK / dV ones sum the per-head gate-gradient partials
 // (head order) into d(top_gates) through log(max(g, 1e-9)).
+constexpr int kPairReduceParts = 8;  // workgroups per (head, block)
 __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
     const float* __restrict__ dk_part, const float* __restrict__ dv_part, const int32_t* __restrict__ plan,
     bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, long N, int H, int E, int R, int n_seg_a, int n_seg_b,
     float dk_scale,
     int kv_blocks, const float* __restrict__ dlg_part, const float* __restrict__ top_gates,
     float* __restrict__ dgates) {
-  constexpr int HD = kPHD, QS = kPBS / 4;  // slots per workgroup
+  constexpr int HD = kPHD, QS = kPBS / kPairReduceParts;  // slots per workgroup
   constexpr int MK = kPairBwdMaxE * (kPairBwdMaxE + 1) / 2;
   __shared__ long seg_off[1024];  // first float of each partial's block rows
   __shared__ int4 key_lds[MK];    // the pair table (block a, block b, first tile, tiles)
@@ -813,7 +815,7 @@ __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
   }
   const PairPlanLayout pl = pair_plan_layout(N, E);
   const int b = blockIdx.x;
-  const int qtr = b & 3, e = (b >> 2) % E, h = (b >> 2) / E;
+  const int part = b % kPairReduceParts, e = (b / kPairReduceParts) % E, h = (b / kPairReduceParts) / E;
   const int n_tiles = plan[pl.hdr], n_keys = plan[pl.hdr + 1];
   const int per = (n_tiles + R - 1) / R;
   const int nk = min(n_keys, MK);  // (the backward's pair path takes E <= kPairBwdMaxE)
@@ -855,53 +857,38 @@ __global__ __launch_bounds__(256) void read_pair_reduce_kernel(
   __syncthreads();
   const int ns = n_s;
   const int D = H * HD;
-  // 32 slots x 64 features = 512 float4 per tensor: two per thread, all of a
-  // batch of 8 partials' loads in flight before the (ascending) sums
-  static_assert(QS * HD / 4 == 2 * 256, "two float4 per thread and tensor");
-  int s_in[2], f4[2];
+  // 16 slots x 64 features = 256 float4 per tensor: one per thread, all of a
+  // batch of 16 partials' loads in flight before the (ascending) sums
+  constexpr int NB = 16;
+  static_assert(QS * HD / 4 == 256, "one float4 per thread and tensor");
+  const int s_in = part * QS + (int)threadIdx.x / (HD / 4);  // slot within the block
+  const int f4 = (int)threadIdx.x % (HD / 4);
+  f32x4 sk = f32x4{0.f, 0.f, 0.f, 0.f}, sv = sk;
+  for (int i = 0; i < ns; i += NB) {
+    f32x4 pk[NB], pv[NB];
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    const int c = threadIdx.x + 256 * cc;
-    s_in[cc] = qtr * QS + c / (HD / 4);  // slot within the block
-    f4[cc] = c % (HD / 4);
-  }
-  f32x4 sk[2], sv[2];
-#pragma unroll
-  for (int cc = 0; cc < 2; ++cc) sk[cc] = sv[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < ns; i += 8) {
-    f32x4 pk[8][2], pv[8][2];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < NB; ++u)
       if (i + u < ns) {
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const long off = seg_off[i + u] + (long)s_in[cc] * HD + 4 * f4[cc];
-          pk[u][cc] = *reinterpret_cast<const f32x4*>(dk_part + off);
-          pv[u][cc] = *reinterpret_cast<const f32x4*>(dv_part + off);
-        }
+        const long off = seg_off[i + u] + (long)s_in * HD + 4 * f4;
+        pk[u] = *reinterpret_cast<const f32x4*>(dk_part + off);
+        pv[u] = *reinterpret_cast<const f32x4*>(dv_part + off);
       }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < NB; ++u)
       if (i + u < ns) {
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          sk[cc] += pk[u][cc];
-          sv[cc] += pv[u][cc];
-        }
+        sk += pk[u];
+        sv += pv[u];
       }
   }
+  bf16x4 ok, ov;
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    bf16x4 ok, ov;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ok[u] = (__bf16)(sk[cc][u] * dk_scale);
-      ov[u] = (__bf16)sv[cc][u];
-    }
-    const long dst = ((long)e * kPBS + s_in[cc]) * D + (long)h * HD + 4 * f4[cc];
-    *reinterpret_cast<bf16x4*>(dk + dst) = ok;
-    *reinterpret_cast<bf16x4*>(dv + dst) = ov;
+  for (int u = 0; u < 4; ++u) {
+    ok[u] = (__bf16)(sk[u] * dk_scale);
+    ov[u] = (__bf16)sv[u];
   }
+  const long dst = ((long)e * kPBS + s_in) * D + (long)h * HD + 4 * f4;
+  *reinterpret_cast<bf16x4*>(dk + dst) = ok;
+  *reinterpret_cast<bf16x4*>(dv + dst) = ov;
 }
 
 // ------------------------------------------------------------------ host side
@@ -985,7 +972,7 @@ hipError_t launch_read_bwd_pair(const void* q, const void* k, const void* v, con
                                   (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)o, (const float*)side,
                                   (const bf16_t*)dout, d.order, (bf16_t*)dq, dlg_part,
                                   dk_part, dv_part, N, d.H, d.L, d.E, alpha, scale, R, nsa, ns));
-  const int kv_blocks = d.H * d.E * 4;
+  const int kv_blocks = d.H * d.E * kPairReduceParts;
   const int g_blocks = (int)std::min<long>(1024, (N * 2 + 255) / 256);
   NAYLIS_TIMED("read_bwd_reduce", st,
                hipLaunchKernelGGL(read_pair_reduce_kernel, dim3(kv_blocks + g_blocks), dim3(256), 0, st, dk_part,
