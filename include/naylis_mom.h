@@ -193,15 +193,17 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
                           int64_t B, int64_t T, int64_t D, int64_t R, int64_t E, int64_t top_k, void* stream);
 
 /* No counterpart in the reference; for tests and for callers that want to
- * bound the forward's cross-workgroup wait.  With bf16 x, R <= 32 and an even
- * number of 32-token chunks, naylis_mom_router_fwd runs in one launch whose
- * workgroups read the earlier chunks' projection sums from the workgroups
- * that made them, polling at most `polls` times per block of chunks and
- * projecting the chunks still missing themselves (same results, bitwise).
- * Sets the process-wide bound to polls (0: never wait, always re-project) and
- * returns the previous one; polls < 0 only returns the current bound
- * (default 20000).  Launches already enqueued keep the bound they took. */
-int naylis_mom_router_spin_limit(int polls);
+ * bound the cross-workgroup wait of the library's one-launch kernel: with
+ * bf16 x, R <= 32 and an even number of 32-token chunks, naylis_mom_router_fwd
+ * runs in one launch whose workgroups read the earlier chunks' projection
+ * sums from the workgroups that made them, polling at most `polls` times per
+ * block of chunks, and project the chunks still missing themselves (same
+ * results, bitwise).  Not taken on a stream that is capturing a graph (the
+ * two launches run there).  Sets the process-wide bound to polls (0: never
+ * wait, always re-project) and returns the previous one; polls < 0 only
+ * returns the current bound (default 20000).  Launches already enqueued keep
+ * the bound they took. */
+int naylis_mom_spin_limit(int polls);
 
 /* Backward of the router: any of d_gates (B,T,k), d_probs, d_logits
  * (B,T,E) may be NULL (no gradient from that output).  d_probs_stride is the

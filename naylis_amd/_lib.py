@@ -43,7 +43,7 @@ SIGNATURES = {
     "naylis_mom_router_workspace_bytes": (_size_t, [_i64] * 6),
     "naylis_mom_router_fwd": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _float]
                               + [_c_void_p] * 6 + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
-    "naylis_mom_router_spin_limit": (_int, [_int]),
+    "naylis_mom_spin_limit": (_int, [_int]),
     "naylis_mom_router_bwd": (_int, [_c_void_p, _int] + [_c_void_p] * 8 + [_i64] + [_c_void_p] * 2 + [_int]
                               + [_c_void_p] * 2 + [_c_void_p, _size_t] + [_i64] * 6 + [_c_void_p]),
     "naylis_mom_router_stats_workspace_bytes": (_size_t, [_i64] * 2),

@@ -25,6 +25,42 @@
 #include "launch_gemm.h"
 #include "launch_rezero.h"
 
+namespace naylis {
+
+// The epoch is the per-device launch count passed through the SplitMix64
+// finalizer (Steele, Lea and Flood, 2014), so its bits look random: a word
+// left in a reused workspace by other data (small integers, zeros, floats)
+// matches it only by a 2^-48 chance, where a plain counter would collide
+// with small integers.
+unsigned long long next_launch_epoch() {
+  static std::atomic<unsigned long long> counts[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  unsigned long long z;
+  do {
+    z = counts[dev].fetch_add(1, std::memory_order_relaxed) + 1 + ((unsigned long long)dev << 56);
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+  } while ((z >> 16) == 0);
+  return z;
+}
+
+static std::atomic<int> g_spin_limit{20000};
+
+int one_launch_spin_limit(int polls) {
+  return polls < 0 ? g_spin_limit.load(std::memory_order_relaxed)
+                   : g_spin_limit.exchange(polls, std::memory_order_relaxed);
+}
+
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
+}
+
+}  // namespace naylis
+
 using namespace naylis;
 
 namespace {
@@ -407,7 +443,7 @@ int naylis_mom_router_fwd(const void* x, int x_dtype, const float* w_down, const
                     "mom_route_fwd");
 }
 
-int naylis_mom_router_spin_limit(int polls) { return router_fused_spin_limit(polls); }
+int naylis_mom_spin_limit(int polls) { return one_launch_spin_limit(polls); }
 
 int naylis_mom_router_bwd(const void* x, int x_dtype, const float* w_down, const float* w_up, const float* act,
                           const float* probs, const int32_t* top_idx, const float* top_gates, const float* d_gates,

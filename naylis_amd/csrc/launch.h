@@ -16,6 +16,17 @@ struct ReadDims {
   const int32_t* order = nullptr;
 };
 
+// One-launch kernels whose workgroups take other workgroups' results (the
+// router forward) tag them with a per-device launch epoch (pseudo-random
+// bits, never 0 in its upper 48) and wait for them at most a process-wide
+// number of polls: one_launch_spin_limit(polls) sets it (polls >= 0) and
+// returns the previous bound; polls < 0 only reads it.
+unsigned long long next_launch_epoch();
+int one_launch_spin_limit(int polls);
+// true when st is capturing a graph (a replay would reuse the captured epoch,
+// so the one-launch kernels are not taken then)
+bool stream_capturing(hipStream_t st);
+
 // The read's token order (read_order.hip): tokens grouped by selected blocks
 // when that lowers the (tile, block) pairs, else the sequence-order mode word.
 size_t read_order_ws_bytes(long N, int E, int topk);

@@ -38,9 +38,6 @@ void launch_router_fast_fwd(const void* x, const float* w_down, const float* w_u
                             float noise_scale, float* logits, float* probs, int32_t* top_idx, float* top_gates,
                             float* act, float* y, double* ycs, unsigned long long* pub, const RouterDims& d,
                             hipStream_t st);
-// Poll bound of the one-launch forward's wait for earlier chunks' sums: sets
-// it to polls (>= 0) and returns the previous bound; polls < 0 only reads it.
-int router_fused_spin_limit(int polls);
 // fast backward (B1 + B2): w, its 32-token chunk sums, W~ (skipped when
 // fuse_scan: the dx kernel then forms it) and the dW_up partials; returns the
 // number of dW_up partials

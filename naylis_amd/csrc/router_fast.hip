@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "launch.h"
 #include "launch_router.h"
 #include "timing.h"
 
@@ -376,7 +377,6 @@ __device__ __forceinline__ void router_head_body(
 // the carry is bitwise that of the two launches whatever happens.  The bound
 // (spin: polls, an s_sleep between them, per block of earlier chunks) is a
 // launch argument; 0 skips the wait and re-projects every earlier chunk.
-constexpr int kFusedSpinDefault = 20000;
 
 template <int RT, int KSW, int EMAX, int TK>
 __global__ __launch_bounds__(512) void router_fwd_fused_kernel(
@@ -951,23 +951,6 @@ bool router_fast_bwd_ok(const void* x, bool x_bf16, const void* dx, const Router
   return x_bf16 && d.D % kFastDxSlab == 0 && d.R <= 64 && (((uintptr_t)x | (uintptr_t)dx) & 15) == 0;
 }
 
-// Launch epoch of the one-launch forward (never 0), per device.
-static unsigned long long next_router_epoch() {
-  static std::atomic<unsigned long long> epochs[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  unsigned long long e = epochs[dev].fetch_add(1, std::memory_order_relaxed) + 1;
-  if (e == 0) e = epochs[dev].fetch_add(1, std::memory_order_relaxed) + 1;
-  return e;
-}
-
-static std::atomic<int> g_fused_spin{kFusedSpinDefault};
-
-int router_fused_spin_limit(int polls) {
-  return polls < 0 ? g_fused_spin.load(std::memory_order_relaxed)
-                   : g_fused_spin.exchange(polls, std::memory_order_relaxed);
-}
-
 template <int RT, int EMAX, int TK>
 static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up, const float* noise, float ns,
                           float* logits, float* probs, int32_t* idx, float* gates, float* act, float* y, double* ycs,
@@ -976,9 +959,7 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
   // One launch (router_fwd_fused_kernel) where its two-chunk workgroups
   // apply: R <= 32, an even chunk count, and a stream that is not being
   // captured (a captured launch would replay one epoch)
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  const bool capturing = hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
-  const bool fused = RT == 1 && pub != nullptr && n_ch % 2 == 0 && !capturing;
+  const bool fused = RT == 1 && pub != nullptr && n_ch % 2 == 0 && !stream_capturing(st);
   // 8 waves split D; a wave takes D / 128 K-steps, held in registers at once
   const int nks = d.D / 128;
   auto go = [&](auto ksw) {
@@ -993,8 +974,8 @@ static void fast_fwd_inst(const void* x, const float* w_down, const float* w_up,
         NAYLIS_TIMED("router_fwd", st,
                      hipLaunchKernelGGL((router_fwd_fused_kernel<RT, KSW, EMAX, TK>), dim3(n_ch / 2, d.B), dim3(512),
                                         0, st, (const bf16_t*)x, w_down, w_up, noise, ns, d.noise_kind, logits, probs,
-                                        idx, gates, act, pub, next_router_epoch(), d.T, d.D, d.R, d.E, d.topk,
-                                        n_ch, g_fused_spin.load(std::memory_order_relaxed)));
+                                        idx, gates, act, pub, next_launch_epoch(), d.T, d.D, d.R, d.E, d.topk,
+                                        n_ch, one_launch_spin_limit(-1)));
         return true;
       }
     }

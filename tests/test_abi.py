@@ -50,15 +50,15 @@ def test_abi_version(lib):
     assert lib.naylis_mom_abi_version() == _lib.ABI_VERSION
 
 
-def test_router_spin_limit_setter(lib):
+def test_spin_limit_setter(lib):
     """The one-launch router's poll bound: a negative argument reads it, any
     other sets it and returns the previous bound (host state only)."""
-    cur = lib.naylis_mom_router_spin_limit(-1)
+    cur = lib.naylis_mom_spin_limit(-1)
     assert cur == 20000
-    assert lib.naylis_mom_router_spin_limit(0) == cur
-    assert lib.naylis_mom_router_spin_limit(-5) == 0
-    assert lib.naylis_mom_router_spin_limit(cur) == 0
-    assert lib.naylis_mom_router_spin_limit(-1) == cur
+    assert lib.naylis_mom_spin_limit(0) == cur
+    assert lib.naylis_mom_spin_limit(-5) == 0
+    assert lib.naylis_mom_spin_limit(cur) == 0
+    assert lib.naylis_mom_spin_limit(-1) == cur
 
 
 READ_OK = dict(B=2, S=64, H=2, hd=16, nb=4, bs=16, k=2)

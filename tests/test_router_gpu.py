@@ -250,11 +250,11 @@ def test_router_one_launch_matches_two_launches(B, T, D, R, E, k, with_noise, sp
     from naylis_amd import _lib
     lib = _lib.load()
     if spin is not None:
-        prev = lib.naylis_mom_router_spin_limit(spin)
+        prev = lib.naylis_mom_spin_limit(spin)
         try:
             _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev)
         finally:
-            assert lib.naylis_mom_router_spin_limit(prev) == spin
+            assert lib.naylis_mom_spin_limit(prev) == spin
     else:
         _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev)
 
