@@ -280,9 +280,17 @@ def _one_launch_vs_two(lib, _lib, B, T, D, R, E, k, with_noise, dev):
         assert rc == 0, lib.naylis_mom_last_error()
 
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    call(xo, outputs(), ws)          # other data: its sums stay published in ws
+    # small-integer words everywhere (consecutive 64-bit words differ in one low bit: their XOR is a
+    # small number, which a plain launch counter used as the epoch could equal); then a launch on
+    # other data, whose sums stay published in ws
+    ws[:nbytes // 8 * 8].view(torch.int64)[:] = torch.arange(nbytes // 8, device=dev)
+    ramp = outputs()
+    call(xd, ramp, ws)               # one launch over the ramp
+    call(xo, outputs(), ws)
     eager = outputs()
     call(xd, eager, ws)              # one launch
+    for name, a, b in zip(("logits", "probs", "top_idx", "gates", "act"), eager, ramp):
+        assert torch.equal(a, b), ("ramp", name)
     torch.cuda.synchronize()
     ws_cap = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     cap = outputs()
